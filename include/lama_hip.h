@@ -1,0 +1,122 @@
+/*
+ * lama_hip.h -- the drop-in C ABI of the MI355X backend (liblama_hip.so).
+ *
+ * It replaces the reference's CUDA engine, `lama-rs/src/cuda.rs`, at the one
+ * boundary its caller uses: `cuda::run(store, model, input, h, w) ->
+ * Result<Vec<f32>, String>` (cuda.rs:1542-1548, called from main.rs:330-346),
+ * plus the device bring-up, the memory query of `mem.rs` and the stats hooks.
+ * Below it, the library dlopens `libamdhip64` (LAMA_HIP_LIB overrides the
+ * path, like LA_CUDA_LIB) and loads its own gfx950 code object with
+ * hipModuleLoadData; no HIP or torch types cross this interface.
+ *
+ * Conventions: activations are planar f32 [c][h][w]; `h`, `w` are multiples
+ * of 8 (the caller pads, main.rs:241-242), any size >= 8.  Every call returns
+ * 0 on success or nonzero with a UTF-8 message in `err` (when non-NULL), the
+ * analogue of `Err(String)`; a failed call leaves the process able to run
+ * another engine.  Single host thread, not re-entrant (cuda.rs keeps its
+ * state thread-local too).
+ */
+#ifndef LAMA_HIP_H
+#define LAMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lama_host.h" /* lama_tensor_info */
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lama_hip_ctx lama_hip_ctx;
+
+/* Replaces Cuda::open / ctx() (cuda.rs:222-275): load the HIP runtime, pick
+ * the device (LAMA_HIP_DEVICE, default 0), load the kernel module, create the
+ * engine stream. */
+int lama_hip_open(lama_hip_ctx **out, char *err, size_t errlen);
+void lama_hip_close(lama_hip_ctx *ctx);
+
+/* Replaces the weight side of load_steps (cuda.rs:330-387 blob_arena,
+ * 595-693 Staging, 695-734 load_conv, 737-830 BN fold, 903-962 load_steps):
+ * `blob` is the whole safetensors file and `table` its tensor index with
+ * absolute offsets (WeightStore, weights.rs:80-139).  Every derived tensor
+ * (folded BNs, MFMA-packed convolution weights, sub-pixel phase weights) is
+ * built once and uploaded in one copy; it stays resident for later calls. */
+int lama_hip_load_weights(lama_hip_ctx *ctx, const void *blob, size_t blob_len,
+                          const lama_tensor_info *table, size_t n, char *err, size_t errlen);
+
+/* Replaces cuda::run (cuda.rs:1542-1691): one forward pass.  `input` is the
+ * host [4][h][w] tensor of build_input (main.rs:175-196); `output` receives
+ * the host [3][h][w] sigmoid output.  Synchronous. */
+int lama_hip_forward(lama_hip_ctx *ctx, const float *input, int h, int w, float *output,
+                     char *err, size_t errlen);
+
+/* The same pass on device-resident buffers, enqueued on `stream` (a
+ * hipStream_t; NULL = the engine's own stream).  Asynchronous. */
+int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int w,
+                            float *d_output, void *stream, char *err, size_t errlen);
+
+/* LAMA_DUMP_STEP (cuda.rs:1572-1574, 1647-1662): a forward that also copies
+ * the activation after plan step i (local planes then global planes, the
+ * layout of cpu.rs:536-546) into steps[i] when steps[i] is non-NULL,
+ * for i in [0, 29).  Synchronous. */
+int lama_hip_forward_steps(lama_hip_ctx *ctx, const float *input, int h, int w, float *output,
+                           float *const *steps, char *err, size_t errlen);
+
+/* Replaces mem.rs:93-99 device_memory(): free/total bytes and device name
+ * of the device lama_hip_open would use.  Works without an open context. */
+int lama_hip_vram(uint64_t *free_bytes, uint64_t *total_bytes, char *name, size_t namelen,
+                  char *err, size_t errlen);
+
+/* Per-kernel timing, the analogue of LAMA_PROFILE_OPS / print_op_stats
+ * (cuda.rs:1703-1782): while enabled, every launch of a kernel family whose
+ * bit is set in `mask` is bracketed by events on the stream it runs on.
+ * Families: 0 conv7x7, 1 conv3x3s2, 2 conv3x3 (FFC), 3 conv1x1, 4 convt,
+ * 5 rfft2, 6 irfft2, 7 tail. */
+int lama_hip_profile(lama_hip_ctx *ctx, uint32_t mask);
+void lama_hip_profile_reset(lama_hip_ctx *ctx);
+/* Family i's accumulated launches, device milliseconds (waits for the
+ * recorded events), and algorithmic FLOPs and HBM bytes (sums over launches).
+ * Returns 1 for a valid i, 0 past the end. */
+int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, uint64_t *launches,
+                          double *ms, double *flops, double *bytes);
+/* print_stats (cuda.rs:1785-1806): a summary to stderr. */
+void lama_hip_print_stats(lama_hip_ctx *ctx);
+/* Launches per forward at h x w (after a plan exists for that shape). */
+int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w);
+
+/* Device buffers for callers that keep their data resident (the role of
+ * lightgpu's upload/download, cuda.rs:390-444). */
+int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size_t errlen);
+int lama_hip_free(lama_hip_ctx *ctx, void *ptr);
+int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, size_t bytes, int kind,
+                    char *err, size_t errlen); /* kind: 1 HtoD, 2 DtoH, 3 DtoD */
+int lama_hip_synchronize(lama_hip_ctx *ctx, char *err, size_t errlen);
+
+/* Single kernel families on host buffers, for parity tests against the
+ * oracle.  These have no counterpart in the reference; each runs one family
+ * on freshly uploaded data and returns the result synchronously.
+ *  conv2d: k in {1,3,7}; reflect padding k/2; stride 1 or 2 (k = 3 only);
+ *          weights [cout][cin][k][k]; optional bias, BN scale/shift, relu.
+ *  conv_transpose: k3 s2 p1 op1, weights [cin][cout][3][3] + bias, optional
+ *          BN scale/shift, relu; output [cout][2h][2w].
+ *  rfft2:  [c][h][w] -> stacked [2c][h][w/2+1] (ortho).
+ *  irfft2: stacked [2c][h][w/2+1] -> [c][h][w] (ortho), plus feat if given.
+ *  tail:   7x7 reflect-padded conv [cin] -> 3 with bias, then sigmoid. */
+int lama_hip_op_conv2d(lama_hip_ctx *ctx, const float *x, int cin, int h, int w, const float *wt,
+                       const float *bias, int cout, int k, int stride, const float *scale,
+                       const float *shift, int relu, float *out, char *err, size_t errlen);
+int lama_hip_op_conv_transpose(lama_hip_ctx *ctx, const float *x, int cin, int h, int w,
+                               const float *wt, const float *bias, int cout, const float *scale,
+                               const float *shift, int relu, float *out, char *err, size_t errlen);
+int lama_hip_op_rfft2(lama_hip_ctx *ctx, const float *x, int c, int h, int w, float *out,
+                      char *err, size_t errlen);
+int lama_hip_op_irfft2(lama_hip_ctx *ctx, const float *spec, const float *feat, int c, int h, int w,
+                       float *out, char *err, size_t errlen);
+int lama_hip_op_tail(lama_hip_ctx *ctx, const float *x, int cin, int h, int w, const float *wt,
+                     const float *bias, float *out, char *err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

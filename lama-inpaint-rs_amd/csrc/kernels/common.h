@@ -1,0 +1,71 @@
+// Shared definitions of the gfx950 kernels and the host engine: launch
+// descriptors live in device memory (written once per input shape), so every
+// kernel takes a pointer to a small table instead of a large by-value argument.
+#pragma once
+#include <stdint.h>
+
+#define LAMA_NT 256  // threads per block (4 waves of 64)
+
+// One K segment of an implicit-GEMM convolution.  `src` is planar
+// [C][IH][IW]; `wt` points at row 0 of the packed weights
+// [M][nchunk][taps][KC] (KC input channels per chunk, zero-padded).
+struct ConvSeg {
+    const float *src;
+    const float *wt;
+    int C, IH, IW;
+    int nchunk;
+    int wrow;  // floats per packed weight row = nchunk * taps * KC
+    int pad_;
+};
+
+// One output problem: out[co][oy'][ox'] for co < M, (oy, ox) on the OH x OW
+// GEMM grid, stored at oy' = oy*oy_mul + oy_off, ox' = ox*ox_mul + ox_off
+// (the conv-transpose phases interleave four grids into one plane).
+// Epilogue: v = acc (+bias) -> *scale + shift -> ReLU -> (+res) -> store.
+struct ConvProblem {
+    ConvSeg s0, s1;  // s1.nchunk == 0 when absent; s1 is always 1x1
+    int M, OH, OW;
+    int tiles_x, tiles_y, mblocks, nblocks;
+    const float *bias, *scale, *shift;
+    int relu;
+    const float *res;
+    float *out;
+    long out_cstride;  // floats between output channel planes
+    int outW;          // output row stride
+    int oy_mul, oy_off, ox_mul, ox_off;
+    int pad_;
+};
+
+// FFT length descriptor.  Twiddles tw[k] = exp(-2*pi*i*k/n) in f32 (computed
+// in f64 on the host).  `sign_fwd` is the exponent sign the reference CPU
+// engine effectively uses for its forward transform of this length: -1 for a
+// power of two (radix-2 path), +1 otherwise (its Bluestein path computes the
+// opposite-sign DFT).  The inverse uses -sign_fwd.
+struct FftLen {
+    int n;
+    int nstages;
+    int radix[16];
+    int sign_fwd;
+    int pad_;
+    const float *tw;  // float2[n]
+};
+
+struct FftArgs {
+    FftLen row, col;  // row: length W, col: length H
+    int C, H, W, Wh;
+    const float *in;    // rfft: real [C][H][W]; irfft: stacked [2C][H][Wh]
+    float *out;         // rfft: stacked [2C][H][Wh]; irfft: real [C][H][W]
+    const float *feat;  // irfft only: added to the output (f + ifft)
+    float scale;        // 1/sqrt(H*W)
+    int pad_;
+};
+
+// The 7x7 output convolution (64 -> 3, reflect pad 3, bias, sigmoid).
+struct TailArgs {
+    const float *src;  // [Cin][H][W]
+    const float *wt;   // [3][Cin][7][7]
+    const float *bias; // [3]
+    float *out;        // [3][H][W]
+    int Cin, H, W;
+    int pad_;
+};

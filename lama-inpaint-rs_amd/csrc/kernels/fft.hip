@@ -1,0 +1,275 @@
+// FourierUnit transforms: rfft2 / irfft2 with norm='ortho' over one channel
+// plane per block, resident in LDS.
+//
+// rfft2 (cpu.rs:769-783): rows are real, so two rows ride in one complex
+// transform (z = a + i b) and are split afterwards with the Hermitian
+// identities; then the W/2+1 kept columns are transformed along y.  The
+// result is scaled by 1/sqrt(HW) and written straight into the stacked
+// layout the FourierUnit's 1x1 convolution reads: plane 2c = real part,
+// plane 2c+1 = imaginary part, each [H][W/2+1].
+//
+// irfft2 (cpu.rs:801-837): the reference completes the full plane with
+// F[(h-y)%h][w-x] = conj(X[y][x]) and keeps the real part of the 2-D inverse.
+// Transforming the stored columns along y first makes every row of the
+// result Hermitian, so the x pass is a complex-to-real transform that ignores
+// the imaginary parts of the DC and Nyquist columns; two rows again share one
+// complex transform.  The output is scaled and added to `feat` (f + FU(f)).
+//
+// 1-D transforms are Stockham auto-sort passes with radix 4, 2, 3, 5 (or a
+// direct DFT for other prime factors), ping-ponging between two LDS buffers.
+// Twiddles come from a per-length table exp(-2 pi i k/n) built in f64 on the
+// host.  The exponent sign per length follows the reference CPU engine: a
+// power-of-two length uses the usual sign, any other length the opposite one
+// (its Bluestein path computes the opposite-sign DFT); `sign_fwd` carries it.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ float2 cmul(float2 a, float2 b)
+{
+    return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+// multiply by s*i (s = +-1)
+__device__ __forceinline__ float2 mul_si(float2 a, int s)
+{
+    return s > 0 ? make_float2(-a.y, a.x) : make_float2(a.y, -a.x);
+}
+// exp(sign * 2 pi i idx / n) from the table exp(-2 pi i k / n)
+__device__ __forceinline__ float2 twd(const float2 *tw, int idx, int sign)
+{
+    float2 w = tw[idx];
+    if (sign > 0) w.y = -w.y;
+    return w;
+}
+
+template <int R>
+__device__ __forceinline__ void dft(float2 (&v)[R], int sign);
+
+template <>
+__device__ __forceinline__ void dft<2>(float2 (&v)[2], int)
+{
+    float2 a = v[0], b = v[1];
+    v[0] = cadd(a, b);
+    v[1] = csub(a, b);
+}
+
+template <>
+__device__ __forceinline__ void dft<4>(float2 (&v)[4], int s)
+{
+    float2 t0 = cadd(v[0], v[2]), t1 = csub(v[0], v[2]);
+    float2 t2 = cadd(v[1], v[3]), t3 = mul_si(csub(v[1], v[3]), s);
+    v[0] = cadd(t0, t2);
+    v[2] = csub(t0, t2);
+    v[1] = cadd(t1, t3);
+    v[3] = csub(t1, t3);
+}
+
+template <>
+__device__ __forceinline__ void dft<3>(float2 (&v)[3], int s)
+{
+    const float s3 = s * 0.86602540378443864676f;
+    float2 t1 = cadd(v[1], v[2]), t2 = csub(v[1], v[2]);
+    float2 m = make_float2(v[0].x - 0.5f * t1.x, v[0].y - 0.5f * t1.y);
+    float2 q = make_float2(-s3 * t2.y, s3 * t2.x);
+    v[0] = cadd(v[0], t1);
+    v[1] = cadd(m, q);
+    v[2] = csub(m, q);
+}
+
+template <>
+__device__ __forceinline__ void dft<5>(float2 (&v)[5], int s)
+{
+    const float c1 = 0.30901699437494742410f, c2 = -0.80901699437494742410f;
+    const float s1 = s * 0.95105651629515357212f, s2 = s * 0.58778525229247312917f;
+    float2 a1 = cadd(v[1], v[4]), b1 = csub(v[1], v[4]);
+    float2 a2 = cadd(v[2], v[3]), b2 = csub(v[2], v[3]);
+    float2 x0 = v[0];
+    float2 m1 = make_float2(x0.x + c1 * a1.x + c2 * a2.x, x0.y + c1 * a1.y + c2 * a2.y);
+    float2 m2 = make_float2(x0.x + c2 * a1.x + c1 * a2.x, x0.y + c2 * a1.y + c1 * a2.y);
+    // i * (s1 b1 + s2 b2) and i * (s2 b1 - s1 b2)
+    float2 n1 = make_float2(-(s1 * b1.y + s2 * b2.y), s1 * b1.x + s2 * b2.x);
+    float2 n2 = make_float2(-(s2 * b1.y - s1 * b2.y), s2 * b1.x - s1 * b2.x);
+    v[0] = make_float2(x0.x + a1.x + a2.x, x0.y + a1.y + a2.y);
+    v[1] = cadd(m1, n1);
+    v[4] = csub(m1, n1);
+    v[2] = cadd(m2, n2);
+    v[3] = csub(m2, n2);
+}
+
+// Butterfly (b, j) of a radix-R Stockham pass over `count` transforms of
+// length n; element e of transform b sits at b*bstride + e*estride.
+struct Pass {
+    const float2 *in;
+    float2 *out;
+    int n, Ns, count, bstride, estride, sign;
+    const float2 *tw;
+};
+
+__device__ __forceinline__ void split_idx(const Pass &P, int m, int idx, int &b, int &j)
+{
+    // Columns (estride > 1): neighbouring threads take neighbouring
+    // transforms so LDS rows are read across lanes.
+    if (P.estride != 1) {
+        b = idx % P.count;
+        j = idx / P.count;
+    } else {
+        b = idx / m;
+        j = idx - b * m;
+    }
+}
+
+template <int R>
+__device__ void pass_fixed(const Pass &P)
+{
+    const int m = P.n / R, twstep = P.n / (P.Ns * R), total = P.count * m;
+    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+        int b, j;
+        split_idx(P, m, idx, b, j);
+        const int k = j % P.Ns;
+        const float2 *src = P.in + (long)b * P.bstride;
+        float2 v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float2 x = src[(j + r * m) * P.estride];
+            if (r > 0 && k > 0) x = cmul(x, twd(P.tw, k * r * twstep, P.sign));
+            v[r] = x;
+        }
+        dft<R>(v, P.sign);
+        float2 *dst = P.out + (long)b * P.bstride;
+        const int base = (j / P.Ns) * P.Ns * R + k;
+#pragma unroll
+        for (int r = 0; r < R; ++r) dst[(base + r * P.Ns) * P.estride] = v[r];
+    }
+}
+
+// Any other radix: a direct DFT per butterfly.
+__device__ void pass_generic(const Pass &P, int R)
+{
+    const int m = P.n / R, twstep = P.n / (P.Ns * R), total = P.count * m, unit = P.n / R;
+    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+        int b, j;
+        split_idx(P, m, idx, b, j);
+        const int k = j % P.Ns;
+        const float2 *src = P.in + (long)b * P.bstride;
+        float2 *dst = P.out + (long)b * P.bstride;
+        const int base = (j / P.Ns) * P.Ns * R + k;
+        for (int q = 0; q < R; ++q) {
+            float2 acc = make_float2(0.f, 0.f);
+            for (int r = 0; r < R; ++r) {
+                float2 x = src[(j + r * m) * P.estride];
+                if (r > 0 && k > 0) x = cmul(x, twd(P.tw, k * r * twstep, P.sign));
+                acc = cadd(acc, cmul(x, twd(P.tw, ((r * q) % R) * unit, P.sign)));
+            }
+            dst[(base + q * P.Ns) * P.estride] = acc;
+        }
+    }
+}
+
+// All passes of one length over a batch; returns the buffer with the result.
+__device__ float2 *stockham(const FftLen &L, float2 *a, float2 *b, int count, int bstride, int estride, int sign)
+{
+    Pass P{a, b, L.n, 1, count, bstride, estride, sign, reinterpret_cast<const float2 *>(L.tw)};
+    for (int s = 0; s < L.nstages; ++s) {
+        const int R = L.radix[s];
+        switch (R) {
+        case 2: pass_fixed<2>(P); break;
+        case 3: pass_fixed<3>(P); break;
+        case 4: pass_fixed<4>(P); break;
+        case 5: pass_fixed<5>(P); break;
+        default: pass_generic(P, R); break;
+        }
+        __syncthreads();
+        P.Ns *= R;
+        float2 *t = const_cast<float2 *>(P.in);
+        P.in = P.out;
+        P.out = t;
+    }
+    return const_cast<float2 *>(P.in);
+}
+
+}  // namespace
+
+// One block per channel: real [C][H][W] -> stacked [2C][H][W/2+1], ortho.
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *__restrict__ args)
+{
+    extern __shared__ float2 sm[];
+    const FftArgs &A = *args;
+    const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
+    const int NB = max(HP * W, H * Wh);
+    float2 *b0 = sm, *b1 = sm + NB;
+    const float *src = A.in + (long)c * H * W;
+    for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
+        const int p = idx / W, x = idx - p * W;
+        const float a = src[(2 * p) * W + x];
+        const float b = 2 * p + 1 < H ? src[(2 * p + 1) * W + x] : 0.f;
+        b0[idx] = make_float2(a, b);
+    }
+    __syncthreads();
+    float2 *r = stockham(A.row, b0, b1, HP, W, 1, A.row.sign_fwd);
+    float2 *o = r == b0 ? b1 : b0;
+    // split each row pair into the two half spectra
+    for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) {
+        const int y = idx / Wh, k = idx - y * Wh, p = y >> 1;
+        const float2 z = r[p * W + k], zm = r[p * W + (W - k) % W];
+        o[idx] = (y & 1) ? make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x))
+                         : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+    }
+    __syncthreads();
+    float2 *q = stockham(A.col, o, r, Wh, 1, Wh, A.col.sign_fwd);
+    float *dre = A.out + (long)(2 * c) * H * Wh, *dim = dre + (long)H * Wh;
+    for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) {
+        const float2 v = q[idx];
+        dre[idx] = v.x * A.scale;
+        dim[idx] = v.y * A.scale;
+    }
+}
+
+// One block per channel: stacked [2C][H][W/2+1] -> real [C][H][W], ortho,
+// plus feat: out = feat + irfft2(in).
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_irfft2(const FftArgs *__restrict__ args)
+{
+    extern __shared__ float2 sm[];
+    const FftArgs &A = *args;
+    const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
+    const int NB = max(HP * W, H * Wh);
+    float2 *b0 = sm, *b1 = sm + NB;
+    const float *sre = A.in + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
+    for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) b0[idx] = make_float2(sre[idx], sim[idx]);
+    __syncthreads();
+    float2 *r = stockham(A.col, b0, b1, Wh, 1, Wh, -A.col.sign_fwd);
+    float2 *o = r == b0 ? b1 : b0;
+    // Hermitian rows, two per complex transform: z = Ga + i Gb
+    for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
+        const int p = idx / W, x = idx - p * W;
+        float2 g[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int y = 2 * p + h;
+            float2 v = make_float2(0.f, 0.f);
+            if (y < H) {
+                if (x < Wh) {
+                    v = r[y * Wh + x];
+                    if (x == 0 || 2 * x == W) v.y = 0.f;
+                } else {
+                    v = r[y * Wh + (W - x)];
+                    v.y = -v.y;
+                }
+            }
+            g[h] = v;
+        }
+        o[idx] = make_float2(g[0].x - g[1].y, g[0].y + g[1].x);
+    }
+    __syncthreads();
+    float2 *q = stockham(A.row, o, r, HP, W, 1, -A.row.sign_fwd);
+    const float *f = A.feat + (long)c * H * W;
+    float *d = A.out + (long)c * H * W;
+    for (int idx = threadIdx.x; idx < H * W; idx += blockDim.x) {
+        const int y = idx / W, x = idx - y * W;
+        const float2 v = q[(y >> 1) * W + x];
+        d[idx] = ((y & 1) ? v.y : v.x) * A.scale + f[idx];
+    }
+}

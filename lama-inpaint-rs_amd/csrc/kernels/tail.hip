@@ -1,0 +1,87 @@
+// model.34 + model.35: 7x7 convolution 64 -> 3 over the ReflectionPad2d(3)
+// plane, with bias, then sigmoid (cpu.rs:531-534, 384-388).
+//
+// With only three output channels an MFMA tile would be >90% padding, so this
+// is VALU work: a block covers 8 rows x 64 columns, each thread two adjacent
+// pixels x 3 channels (6 accumulators).  Per input channel the block stages
+// the reflect-padded 14 x 70 patch in LDS; the channel's 147 weights are
+// wave-uniform and read through the scalar cache.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace {
+constexpr int TROWS = 8, TCOLS = 64, PX = 2;
+constexpr int PR = TROWS + 6, PC = TCOLS + 6;
+
+__device__ __forceinline__ int reflect_t(int i, int n)
+{
+    if (n == 1) return 0;
+    if (i < 0) i = -i;
+    if (i >= n) {
+        int period = 2 * n - 2;
+        i %= period;
+        if (i >= n) i = period - i;
+    }
+    return i;
+}
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
+{
+    __shared__ float patch[2][PR * PC];
+    const TailArgs &A = *args;
+    const int H = A.H, W = A.W;
+    const int tiles_x = (W + TCOLS - 1) / TCOLS;
+    const int oy0 = (blockIdx.x / tiles_x) * TROWS, ox0 = (blockIdx.x % tiles_x) * TCOLS;
+    const int tr = threadIdx.x / (TCOLS / PX), tc = (threadIdx.x % (TCOLS / PX)) * PX;
+    float acc[3][PX];
+#pragma unroll
+    for (int co = 0; co < 3; ++co)
+#pragma unroll
+        for (int p = 0; p < PX; ++p) acc[co][p] = 0.f;
+
+    const long plane = (long)H * W;
+    auto stage = [&](int ci, float *dst) {
+        const float *src = A.src + (long)ci * plane;
+        for (int idx = threadIdx.x; idx < PR * PC; idx += LAMA_NT) {
+            const int r = idx / PC, c = idx - r * PC;
+            dst[idx] = src[(long)reflect_t(oy0 - 3 + r, H) * W + reflect_t(ox0 - 3 + c, W)];
+        }
+    };
+    stage(0, patch[0]);
+    for (int ci = 0; ci < A.Cin; ++ci) {
+        __syncthreads();
+        if (ci + 1 < A.Cin) stage(ci + 1, patch[(ci + 1) & 1]);
+        const float *pp = patch[ci & 1] + tr * PC + tc;
+        const float *w0 = A.wt + (long)ci * 49;
+        const long wstride = (long)A.Cin * 49;
+#pragma unroll
+        for (int ky = 0; ky < 7; ++ky) {
+            float row[PX + 6];
+#pragma unroll
+            for (int q = 0; q < PX + 6; ++q) row[q] = pp[ky * PC + q];
+#pragma unroll
+            for (int kx = 0; kx < 7; ++kx) {
+#pragma unroll
+                for (int co = 0; co < 3; ++co) {
+                    const float wv = w0[co * wstride + ky * 7 + kx];
+#pragma unroll
+                    for (int p = 0; p < PX; ++p) acc[co][p] += wv * row[p + kx];
+                }
+            }
+        }
+    }
+    const int oy = oy0 + tr;
+    if (oy >= H) return;
+#pragma unroll
+    for (int co = 0; co < 3; ++co)
+#pragma unroll
+        for (int p = 0; p < PX; ++p) {
+            const int ox = ox0 + tc + p;
+            if (ox < W) {
+                const float v = acc[co][p] + A.bias[co];
+                A.out[co * plane + (long)oy * W + ox] = 1.0f / (1.0f + expf(-v));
+            }
+        }
+}

@@ -1,0 +1,193 @@
+// extern "C" entry points of liblama_hip.so (include/lama_hip.h) and the
+// embedded gfx950 code object.
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "engine.h"
+#include "lama_hip.h"
+
+// The code object built by `hipcc --genco --offload-arch=gfx950`, linked in
+// verbatim so the library is self-contained.
+__asm__(".section .rodata\n"
+        ".balign 4096\n"
+        ".global lama_hsaco_start\n"
+        "lama_hsaco_start:\n"
+        ".incbin \"" LAMA_HSACO_PATH "\"\n"
+        ".global lama_hsaco_end\n"
+        "lama_hsaco_end:\n"
+        ".byte 0\n"
+        ".previous\n");
+
+struct lama_hip_ctx {
+    lama::Engine eng;
+};
+
+namespace {
+int fail(char *err, size_t len, const std::string &m)
+{
+    if (err && len) snprintf(err, len, "%s", m.c_str());
+    return 1;
+}
+}  // namespace
+
+#define GUARD(expr)                          \
+    do {                                     \
+        std::string e_;                      \
+        try {                                \
+            if (!(expr)) return fail(err, errlen, e_); \
+        } catch (const std::exception &x) {  \
+            return fail(err, errlen, x.what()); \
+        }                                    \
+        return 0;                            \
+    } while (0)
+
+extern "C" int lama_hip_open(lama_hip_ctx **out, char *err, size_t errlen)
+{
+    *out = nullptr;
+    auto *c = new lama_hip_ctx;
+    std::string e;
+    if (!c->eng.open(e)) {
+        delete c;
+        return fail(err, errlen, e);
+    }
+    *out = c;
+    return 0;
+}
+
+extern "C" void lama_hip_close(lama_hip_ctx *ctx) { delete ctx; }
+
+extern "C" int lama_hip_load_weights(lama_hip_ctx *ctx, const void *blob, size_t blob_len,
+                                     const lama_tensor_info *table, size_t n, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.load_weights((const uint8_t *)blob, blob_len, table, n, e_));
+}
+
+extern "C" int lama_hip_forward(lama_hip_ctx *ctx, const float *input, int h, int w, float *output, char *err,
+                                size_t errlen)
+{
+    GUARD(ctx->eng.forward_host(input, h, w, output, nullptr, e_));
+}
+
+extern "C" int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int w, float *d_output,
+                                       void *stream, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.forward_device(d_input, h, w, d_output, (hipStream_t)stream, e_));
+}
+
+extern "C" int lama_hip_forward_steps(lama_hip_ctx *ctx, const float *input, int h, int w, float *output,
+                                      float *const *steps, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.forward_host(input, h, w, output, steps, e_));
+}
+
+extern "C" int lama_hip_vram(uint64_t *free_bytes, uint64_t *total_bytes, char *name, size_t namelen, char *err,
+                             size_t errlen)
+{
+    std::string e;
+    const lama::HipApi *h = lama::hip_api(e);
+    if (!h) return fail(err, errlen, e);
+    int dev = getenv("LAMA_HIP_DEVICE") ? atoi(getenv("LAMA_HIP_DEVICE")) : 0;
+    hipError_t r = h->hipInit(0);
+    if (r == hipSuccess) r = h->hipSetDevice(dev);
+    size_t f = 0, t = 0;
+    if (r == hipSuccess) r = h->hipMemGetInfo(&f, &t);
+    if (r != hipSuccess) return fail(err, errlen, lama::hip_error(*h, r, "hipMemGetInfo"));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    if (name && namelen) {
+        char buf[256] = {0};
+        if (h->hipDeviceGetName(buf, sizeof buf, dev) != hipSuccess) snprintf(buf, sizeof buf, "the GPU");
+        snprintf(name, namelen, "%s", buf);
+    }
+    return 0;
+}
+
+extern "C" int lama_hip_profile(lama_hip_ctx *ctx, uint32_t mask)
+{
+    ctx->eng.set_profile(mask);
+    return 0;
+}
+
+extern "C" void lama_hip_profile_reset(lama_hip_ctx *ctx) { ctx->eng.profile_reset(); }
+
+extern "C" int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, uint64_t *launches,
+                                     double *ms, double *flops, double *bytes)
+{
+    std::string n;
+    uint64_t l = 0;
+    double m = 0, f = 0, b = 0;
+    if (!ctx->eng.profile_read(i, n, l, m, f, b)) return 0;
+    if (name && namelen) snprintf(name, namelen, "%s", n.c_str());
+    if (launches) *launches = l;
+    if (ms) *ms = m;
+    if (flops) *flops = f;
+    if (bytes) *bytes = b;
+    return 1;
+}
+
+extern "C" void lama_hip_print_stats(lama_hip_ctx *ctx)
+{
+    for (int i = 0;; ++i) {
+        std::string n;
+        uint64_t l;
+        double m, f, b;
+        if (!ctx->eng.profile_read(i, n, l, m, f, b)) break;
+        if (!l) continue;
+        fprintf(stderr, "gpu op %-10s %6llu launches %9.3f ms  %8.2f TFLOP/s  %8.1f GB/s\n", n.c_str(),
+                (unsigned long long)l, m, m > 0 ? f / (m * 1e9) : 0.0, m > 0 ? b / (m * 1e6) : 0.0);
+    }
+}
+
+extern "C" int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w) { return ctx->eng.launch_count(h, w); }
+
+extern "C" int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.check(ctx->eng.hip()->hipMalloc(ptr, bytes), "hipMalloc", e_));
+}
+
+extern "C" int lama_hip_free(lama_hip_ctx *ctx, void *ptr) { return ctx->eng.hip()->hipFree(ptr) == hipSuccess ? 0 : 1; }
+
+extern "C" int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, size_t bytes, int kind, char *err,
+                               size_t errlen)
+{
+    hipMemcpyKind k = kind == 1 ? hipMemcpyHostToDevice : kind == 2 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    GUARD(ctx->eng.check(ctx->eng.hip()->hipMemcpy(dst, src, bytes, k), "hipMemcpy", e_));
+}
+
+extern "C" int lama_hip_synchronize(lama_hip_ctx *ctx, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.check(ctx->eng.hip()->hipStreamSynchronize(ctx->eng.stream()), "hipStreamSynchronize", e_));
+}
+
+extern "C" int lama_hip_op_conv2d(lama_hip_ctx *ctx, const float *x, int cin, int h, int w, const float *wt,
+                                  const float *bias, int cout, int k, int stride, const float *scale,
+                                  const float *shift, int relu, float *out, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.op_conv2d(x, cin, h, w, wt, bias, cout, k, stride, scale, shift, relu, out, e_));
+}
+
+extern "C" int lama_hip_op_conv_transpose(lama_hip_ctx *ctx, const float *x, int cin, int h, int w,
+                                          const float *wt, const float *bias, int cout, const float *scale,
+                                          const float *shift, int relu, float *out, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.op_convt(x, cin, h, w, wt, bias, cout, scale, shift, relu, out, e_));
+}
+
+extern "C" int lama_hip_op_rfft2(lama_hip_ctx *ctx, const float *x, int c, int h, int w, float *out, char *err,
+                                 size_t errlen)
+{
+    GUARD(ctx->eng.op_fft(false, x, nullptr, c, h, w, out, e_));
+}
+
+extern "C" int lama_hip_op_irfft2(lama_hip_ctx *ctx, const float *spec, const float *feat, int c, int h, int w,
+                                  float *out, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.op_fft(true, spec, feat, c, h, w, out, e_));
+}
+
+extern "C" int lama_hip_op_tail(lama_hip_ctx *ctx, const float *x, int cin, int h, int w, const float *wt,
+                                const float *bias, float *out, char *err, size_t errlen)
+{
+    GUARD(ctx->eng.op_tail(x, cin, h, w, wt, bias, out, e_));
+}

@@ -1,0 +1,986 @@
+// The HIP engine: the reference's cuda.rs host side rebuilt around a fused,
+// preplanned forward.
+//
+//  * Weights: derived once on the host from the container and uploaded in
+//    one copy (cuda.rs uploads the raw file and derives on every call):
+//    BatchNorms folded as cpu.rs:58-62, convolution weights packed for the
+//    MFMA kernels ([M][nchunk][taps][KC]), the FFC's local convolutions
+//    concatenated along K (l2l | g2l, so out_l = l2l(x_l) + g2l(x_g) is one
+//    GEMM), model.4's l2l/l2g stacked along M, and every ConvTranspose split
+//    into its four sub-pixel phases.
+//  * Activations: one device arena per input shape with the whole plan laid
+//    out up front; local and global branches share one [512][h/8][w/8]
+//    buffer (local planes first), which makes the reference's concat free.
+//  * Launches: a static list per shape whose descriptors live in device
+//    memory, so a forward is only kernel launches (and two copies).
+#include "engine.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <functional>
+
+namespace lama {
+
+const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3", "conv1x1",
+                                          "convt",   "rfft2",     "irfft2",  "tail"};
+
+size_t step_numel(int step, int h, int w)
+{
+    const size_t h8 = h / 8, w8 = w / 8;
+    switch (step) {
+    case 0: return 4ul * (h + 6) * (w + 6);
+    case 1: return 64ul * h * w;
+    case 2: return 128ul * (h / 2) * (w / 2);
+    case 3: return 256ul * (h / 4) * (w / 4);
+    case 24: return 256ul * (h / 4) * (w / 4);
+    case 25: return 128ul * (h / 2) * (w / 2);
+    case 26: return 64ul * h * w;
+    case 27: return 64ul * (h + 6) * (w + 6);
+    case 28: return 3ul * h * w;
+    default: return (step >= 4 && step <= 23) ? 512ul * h8 * w8 : 0;
+    }
+}
+
+namespace {
+
+const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lama_conv3x3", "lama_conv1x1",
+                                          "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail"};
+
+// Tile geometry of each conv family (kernels/conv.hip): rows x columns.
+void tile_shape(int family, int &tr, int &tc)
+{
+    if (family == F_CONV1) {
+        tr = 1;
+        tc = 64;
+    } else {
+        tr = 2;
+        tc = 32;
+    }
+}
+
+struct WeightSrc {
+    const uint8_t *blob;
+    size_t len;
+    std::map<std::string, const lama_tensor_info *> idx;
+
+    // The tensor `name` as f32, checked against `shape`.
+    bool get(const std::string &name, std::initializer_list<int64_t> shape, std::vector<float> &out,
+             std::string &err) const
+    {
+        auto it = idx.find(name);
+        if (it == idx.end()) {
+            err = "missing tensor in weight blob: " + name;  // weights.rs:116-120
+            return false;
+        }
+        const lama_tensor_info *t = it->second;
+        bool ok = (size_t)t->ndim == shape.size();
+        size_t i = 0, n = 1;
+        for (int64_t d : shape) {
+            ok = ok && t->shape[i++] == d;
+            n *= (size_t)d;
+        }
+        if (!ok || t->nbytes != n * 4 || t->offset + t->nbytes > len) {
+            std::string want, got;
+            for (int64_t d : shape) want += (want.empty() ? "" : ",") + std::to_string(d);
+            for (int d = 0; d < t->ndim; ++d) got += (d ? "," : "") + std::to_string(t->shape[d]);
+            err = "tensor " + name + ": expected shape [" + want + "], found [" + got + "]";
+            return false;
+        }
+        out.resize(n);
+        std::memcpy(out.data(), blob + t->offset, n * 4);
+        return true;
+    }
+};
+
+struct Arena {
+    std::vector<float> h;
+    size_t add(size_t n)
+    {
+        size_t off = (h.size() + 63) / 64 * 64;
+        h.resize(off + n, 0.f);
+        return off;
+    }
+};
+
+Packed pack(Arena &A, int M, int C, int T, int KC, const std::function<float(int, int, int)> &get)
+{
+    Packed p;
+    p.M = M;
+    p.C = C;
+    p.T = T;
+    p.KC = KC;
+    p.nchunk = (C + KC - 1) / KC;
+    p.wrow = p.nchunk * T * KC;
+    p.off = A.add((size_t)M * p.wrow);
+    float *d = A.h.data() + p.off;
+    for (int co = 0; co < M; ++co)
+        for (int ck = 0; ck < p.nchunk; ++ck)
+            for (int t = 0; t < T; ++t)
+                for (int kc = 0; kc < KC; ++kc) {
+                    const int ci = ck * KC + kc;
+                    d[(((size_t)co * p.nchunk + ck) * T + t) * KC + kc] = ci < C ? get(co, ci, t) : 0.f;
+                }
+    return p;
+}
+
+// cpu.rs:58-62: s = w / sqrt(var + 1e-5), t = b - mean * s, in f32.
+void fold_into(const std::vector<float> &w, const std::vector<float> &b, const std::vector<float> &mean,
+               const std::vector<float> &var, float *scale, float *shift)
+{
+    for (size_t i = 0; i < w.size(); ++i) {
+        const float s = w[i] / std::sqrt(var[i] + 1e-5f);
+        scale[i] = s;
+        const float ms = mean[i] * s;
+        shift[i] = b[i] - ms;
+    }
+}
+
+bool fold_bns(Arena &A, const WeightSrc &S, const std::vector<std::pair<std::string, int>> &parts, size_t &off,
+              std::string &err)
+{
+    int n = 0;
+    for (auto &p : parts) n += p.second;
+    off = A.add(2 * (size_t)n);
+    int at = 0;
+    for (auto &p : parts) {
+        std::vector<float> w, b, m, v;
+        const int64_t c = p.second;
+        if (!S.get(p.first + ".weight", {c}, w, err) || !S.get(p.first + ".bias", {c}, b, err) ||
+            !S.get(p.first + ".running_mean", {c}, m, err) || !S.get(p.first + ".running_var", {c}, v, err))
+            return false;
+        fold_into(w, b, m, v, A.h.data() + off + at, A.h.data() + off + n + at);
+        at += p.second;
+    }
+    return true;
+}
+
+bool is_pow2(int n) { return n > 0 && (n & (n - 1)) == 0; }
+
+}  // namespace
+
+Engine::~Engine()
+{
+    if (!hip_) return;
+    for (auto &kv : plans_)
+        if (kv.second.arena) hip_->hipFree(kv.second.arena);
+    if (warena_) hip_->hipFree(warena_);
+    for (auto &p : pending_) {
+        hip_->hipEventDestroy(p.a);
+        hip_->hipEventDestroy(p.b);
+    }
+    for (auto e : event_pool_) hip_->hipEventDestroy(e);
+    if (stream_) hip_->hipStreamDestroy(stream_);
+    if (module_) hip_->hipModuleUnload(module_);
+}
+
+bool Engine::check(hipError_t e, const char *what, std::string &err)
+{
+    if (e == hipSuccess) return true;
+    err = hip_error(*hip_, e, what);
+    return false;
+}
+
+extern "C" const unsigned char lama_hsaco_start[];
+extern "C" const unsigned char lama_hsaco_end[];
+
+bool Engine::open(std::string &err)
+{
+    hip_ = hip_api(err);
+    if (!hip_) return false;
+    if (!check(hip_->hipInit(0), "hipInit", err)) return false;
+    int count = 0;
+    if (!check(hip_->hipGetDeviceCount(&count), "hipGetDeviceCount", err)) return false;
+    if (count < 1) {
+        err = "no HIP device visible";
+        return false;
+    }
+    const char *dev = getenv("LAMA_HIP_DEVICE");
+    device_ = dev ? atoi(dev) : 0;
+    if (device_ < 0 || device_ >= count) {
+        err = "LAMA_HIP_DEVICE=" + std::to_string(device_) + " but " + std::to_string(count) + " device(s) visible";
+        return false;
+    }
+    if (!check(hip_->hipSetDevice(device_), "hipSetDevice", err)) return false;
+    hipDeviceProp_t prop;
+    if (!check(hip_->hipGetDevicePropertiesR0600(&prop, device_), "hipGetDeviceProperties", err)) return false;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        err = std::string("device ") + prop.name + " is " + prop.gcnArchName +
+              "; this backend carries gfx950 (MI355X) code only";
+        return false;
+    }
+    if (!check(hip_->hipModuleLoadData(&module_, lama_hsaco_start), "hipModuleLoadData", err)) return false;
+    for (int f = 0; f < F_COUNT; ++f)
+        if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
+    return check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err);
+}
+
+bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_info *t, size_t n, std::string &err)
+{
+    WeightSrc S{blob, len, {}};
+    for (size_t i = 0; i < n; ++i) S.idx[t[i].name] = &t[i];
+    Arena A;
+    std::vector<float> w, w2;
+    // model.1: 7x7 4 -> 64 (model.rs:142-144)
+    if (!S.get("model.1.ffc.convl2l.weight", {64, 4, 7, 7}, w, err)) return false;
+    head_ = pack(A, 64, 4, 49, 4, [&](int co, int ci, int t) { return w[((size_t)co * 4 + ci) * 49 + t]; });
+    if (!fold_bns(A, S, {{"model.1.bn_l", 64}}, head_bn_, err)) return false;
+    // model.2 / model.3: 3x3 s2, local only
+    const int dc[2][2] = {{64, 128}, {128, 256}};
+    for (int d = 0; d < 2; ++d) {
+        const int cin = dc[d][0], cout = dc[d][1];
+        const std::string p = "model." + std::to_string(d + 2);
+        if (!S.get(p + ".ffc.convl2l.weight", {cout, cin, 3, 3}, w, err)) return false;
+        down_[d] = pack(A, cout, cin, 9, 8, [&](int co, int ci, int t) { return w[((size_t)co * cin + ci) * 9 + t]; });
+        if (!fold_bns(A, S, {{p + ".bn_l", cout}}, down_bn_[d], err)) return false;
+    }
+    // model.4: 256 -> 128 local + 384 global, stacked along M
+    if (!S.get("model.4.ffc.convl2l.weight", {128, 256, 3, 3}, w, err) ||
+        !S.get("model.4.ffc.convl2g.weight", {384, 256, 3, 3}, w2, err))
+        return false;
+    down_[2] = pack(A, 512, 256, 9, 8, [&](int co, int ci, int t) {
+        return co < 128 ? w[((size_t)co * 256 + ci) * 9 + t] : w2[((size_t)(co - 128) * 256 + ci) * 9 + t];
+    });
+    if (!fold_bns(A, S, {{"model.4.bn_l", 128}, {"model.4.bn_g", 384}}, down_bn_[2], err)) return false;
+    // model.5..22: 36 FFC_BN_ACT (model.rs:157-165), ratio 0.75: 128 local / 384 global
+    for (int i = 5; i <= 22; ++i)
+        for (int s = 1; s <= 2; ++s) {
+            FfcW &F = ffc_[(i - 5) * 2 + (s - 1)];
+            const std::string pb = "model." + std::to_string(i) + ".conv" + std::to_string(s);
+            const std::string pf = pb + ".ffc";
+            std::vector<float> l2l, g2l, l2g, c1, c2, fu;
+            if (!S.get(pf + ".convl2l.weight", {128, 128, 3, 3}, l2l, err) ||
+                !S.get(pf + ".convg2l.weight", {128, 384, 3, 3}, g2l, err) ||
+                !S.get(pf + ".convl2g.weight", {384, 128, 3, 3}, l2g, err) ||
+                !S.get(pf + ".convg2g.conv1.0.weight", {192, 384, 1, 1}, c1, err) ||
+                !S.get(pf + ".convg2g.fu.conv_layer.weight", {384, 384, 1, 1}, fu, err) ||
+                !S.get(pf + ".convg2g.conv2.weight", {384, 192, 1, 1}, c2, err))
+                return false;
+            F.local = pack(A, 128, 512, 9, 8, [&](int co, int ci, int t) {
+                return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
+            });
+            F.l2g = pack(A, 384, 128, 9, 8, [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; });
+            F.conv2 = pack(A, 384, 192, 1, 8, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
+            F.conv1 = pack(A, 192, 384, 1, 32, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
+            F.fu = pack(A, 384, 384, 1, 32, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
+            if (!fold_bns(A, S, {{pf + ".convg2g.conv1.1", 192}}, F.bn1, err) ||
+                !fold_bns(A, S, {{pf + ".convg2g.fu.bn", 384}}, F.fu_bn, err) ||
+                !fold_bns(A, S, {{pb + ".bn_l", 128}}, F.bn_l, err) || !fold_bns(A, S, {{pb + ".bn_g", 384}}, F.bn_g, err))
+                return false;
+        }
+    // model.24/27/30: ConvTranspose2d k3 s2 p1 op1 + BN (model.rs:172-201)
+    const int ups[3][3] = {{24, 512, 256}, {27, 256, 128}, {30, 128, 64}};
+    for (int u = 0; u < 3; ++u) {
+        UpW &U = up_[u];
+        U.cin = ups[u][1];
+        U.cout = ups[u][2];
+        const std::string p = "model." + std::to_string(ups[u][0]);
+        std::vector<float> bias;
+        if (!S.get(p + ".weight", {U.cin, U.cout, 3, 3}, w, err) || !S.get(p + ".bias", {U.cout}, bias, err))
+            return false;
+        // Phase (py, px) of output pixel (2m+py, 2n+px) reads input (m+a, n+b)
+        // with a in [0, 1+py): kernel row ky = 1 for py = 0, else 2 (a = 0)
+        // or 0 (a = 1); the same for columns.
+        for (int ph = 0; ph < 4; ++ph) {
+            const int py = ph >> 1, px = ph & 1, nx = 1 + px;
+            const int cout = U.cout;
+            U.ph[ph] = pack(A, cout, U.cin, (1 + py) * nx, 8, [&](int co, int ci, int t) {
+                const int a = t / nx, b = t % nx;
+                const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
+                return w[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
+            });
+        }
+        U.bias = A.add(U.cout);
+        std::copy(bias.begin(), bias.end(), A.h.begin() + U.bias);
+        if (!fold_bns(A, S, {{"model." + std::to_string(ups[u][0] + 1), U.cout}}, U.bn, err)) return false;
+    }
+    // model.34: 7x7 64 -> 3 with bias
+    std::vector<float> tb;
+    if (!S.get("model.34.weight", {3, 64, 7, 7}, w, err) || !S.get("model.34.bias", {3}, tb, err)) return false;
+    tail_w_ = A.add(w.size());
+    std::copy(w.begin(), w.end(), A.h.begin() + tail_w_);
+    tail_b_ = A.add(3);
+    std::copy(tb.begin(), tb.end(), A.h.begin() + tail_b_);
+
+    // one upload (cuda.rs:330-369 does one HtoD of the raw file)
+    if (warena_) {
+        hip_->hipFree(warena_);
+        warena_ = nullptr;
+    }
+    if (!check(hip_->hipMalloc((void **)&warena_, A.h.size() * 4), "hipMalloc(weights)", err)) return false;
+    if (!check(hip_->hipMemcpy(warena_, A.h.data(), A.h.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(weights)",
+               err))
+        return false;
+    // plans hold pointers into the old arena
+    for (auto &kv : plans_)
+        if (kv.second.arena) hip_->hipFree(kv.second.arena);
+    plans_.clear();
+    have_weights_ = true;
+    return true;
+}
+
+bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
+{
+    std::memset(&L, 0, sizeof L);
+    L.n = n;
+    L.sign_fwd = is_pow2(n) ? -1 : 1;
+    int m = n;
+    auto push = [&](int r) {
+        if (L.nstages >= 16) return false;
+        L.radix[L.nstages++] = r;
+        m /= r;
+        return true;
+    };
+    while (m % 4 == 0)
+        if (!push(4)) break;
+    while (m % 2 == 0)
+        if (!push(2)) break;
+    for (int p = 3; m > 1 && p <= m; p += 2)
+        while (m % p == 0)
+            if (!push(p)) break;
+    if (m != 1) {
+        err = "FFT length " + std::to_string(n) + " needs too many passes";
+        return false;
+    }
+    tw.resize(2 * (size_t)n);
+    for (int k = 0; k < n; ++k) {
+        const double a = -2.0 * M_PI * (double)k / (double)n;
+        tw[2 * k] = (float)std::cos(a);
+        tw[2 * k + 1] = (float)std::sin(a);
+    }
+    return true;
+}
+
+Plan *Engine::plan_for(int h, int w, std::string &err)
+{
+    if (!have_weights_) {
+        err = "no weights loaded";
+        return nullptr;
+    }
+    if (h < 8 || w < 8 || h % 8 || w % 8) {
+        err = "input " + std::to_string(w) + "x" + std::to_string(h) + " is not a multiple of 8 (the caller pads)";
+        return nullptr;
+    }
+    auto key = std::make_pair(h, w);
+    auto it = plans_.find(key);
+    if (it != plans_.end()) return &it->second;
+    Plan p;
+    p.H = h;
+    p.W = w;
+    if (!build_plan(p, err)) {
+        if (p.arena) hip_->hipFree(p.arena);
+        return nullptr;
+    }
+    return &(plans_[key] = p);
+}
+
+bool Engine::build_plan(Plan &p, std::string &err)
+{
+    const int H = p.H, W = p.W, H2 = H / 2, W2 = W / 2, H4 = H / 4, W4 = W / 4, H8 = H / 8, W8 = W / 8;
+    const int Wh = W8 / 2 + 1;
+    const size_t P = (size_t)H * W, P2 = (size_t)H2 * W2, P4 = (size_t)H4 * W4, P8 = (size_t)H8 * W8;
+    const size_t PS = (size_t)H8 * Wh;
+
+    FftLen frow, fcol;
+    std::vector<float> twr, twc;
+    if (!fft_len(W8, frow, twr, err) || !fft_len(H8, fcol, twc, err)) return false;
+    const int HP = (H8 + 1) / 2;
+    const size_t fft_lds = 2 * std::max((size_t)HP * W8, PS) * 8;
+    if (fft_lds > 160 * 1024) {
+        err = "bottleneck plane " + std::to_string(W8) + "x" + std::to_string(H8) +
+              " exceeds the LDS-resident FFT (input up to about 1024x1024)";
+        return false;
+    }
+
+    // arena layout
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off = (off + bytes + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_in = take(4 * P * 4), o_a1 = take(64 * P * 4), o_a2 = take(128 * P2 * 4), o_a3 = take(256 * P4 * 4);
+    const size_t o_x = take(512 * P8 * 4), o_y = take(512 * P8 * 4), o_f = take(192 * P8 * 4), o_g = take(192 * P8 * 4);
+    const size_t o_s = take(384 * PS * 4), o_s2 = take(384 * PS * 4), o_out = take(3 * P * 4);
+    const size_t o_twr = take(twr.size() * 4), o_twc = take(twc.size() * 4);
+    const size_t n_conv = 4 + 36 * 4 + 4 * 3;
+    const size_t n_puts = 4 + 36 * 3 + 3 + 3;  // descriptor uploads, each 256-byte aligned
+    const size_t o_desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
+    p.arena_bytes = off;
+    if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
+    char *base = (char *)p.arena;
+    auto F = [&](size_t o) { return (float *)(base + o); };
+    float *in = F(o_in), *a1 = F(o_a1), *a2 = F(o_a2), *a3 = F(o_a3), *X = F(o_x), *Y = F(o_y), *Fb = F(o_f),
+          *G = F(o_g), *Sb = F(o_s), *S2 = F(o_s2), *out = F(o_out);
+    p.in = in;
+    p.out = out;
+    frow.tw = F(o_twr);
+    fcol.tw = F(o_twc);
+
+    // descriptors, staged on the host and uploaded once
+    std::vector<char> desc;
+    auto put = [&](const void *src, size_t bytes) {
+        size_t o = (desc.size() + 255) / 256 * 256;
+        desc.resize(o + bytes);
+        std::memcpy(desc.data() + o, src, bytes);
+        return (void *)(base + o_desc + o);
+    };
+    auto seg = [&](const float *src, const Packed &pk, int C, int IH, int IW) {
+        ConvSeg s{};
+        s.src = src;
+        s.wt = wp(pk.off);
+        s.C = C;
+        s.IH = IH;
+        s.IW = IW;
+        s.nchunk = pk.nchunk;
+        s.wrow = pk.wrow;
+        return s;
+    };
+    auto problem = [&](int family, const ConvSeg &s0, int M, int OH, int OW, size_t bn, int bn_n, float *o,
+                       size_t ocs, int outW, const float *res) {
+        ConvProblem q{};
+        q.s0 = s0;
+        q.M = M;
+        q.OH = OH;
+        q.OW = OW;
+        int tr, tc;
+        tile_shape(family, tr, tc);
+        q.tiles_x = (OW + tc - 1) / tc;
+        q.tiles_y = (OH + tr - 1) / tr;
+        q.mblocks = (M + 63) / 64;
+        q.nblocks = q.tiles_x * q.tiles_y * q.mblocks;
+        q.scale = wp(bn);
+        q.shift = wp(bn + bn_n);
+        q.relu = 1;
+        q.res = res;
+        q.out = o;
+        q.out_cstride = (long)ocs;
+        q.outW = outW;
+        q.oy_mul = q.ox_mul = 1;
+        return q;
+    };
+    auto conv_launch = [&](int family, std::vector<ConvProblem> probs, int step, double flops, double bytes) {
+        Launch L{};
+        L.fn = fn_[family];
+        L.family = family;
+        unsigned nb = 0;
+        for (auto &q : probs) nb += (unsigned)q.nblocks;
+        L.grid = nb;
+        L.shmem = 0;
+        L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
+        L.nprob = (int)probs.size();
+        L.nparams = 2;
+        L.step_end = step;
+        L.flops = flops;
+        L.bytes = bytes;
+        p.launches.push_back(L);
+    };
+    const double f4 = 4.0;  // bytes per float
+
+    // step 1: model.1 (ReflectionPad2d(3) folded into the 7x7's reflect indexing)
+    conv_launch(F_CONV7, {problem(F_CONV7, seg(in, head_, 4, H, W), 64, H, W, head_bn_, 64, a1, P, W, nullptr)}, 1,
+                2.0 * 4 * 64 * 49 * P, f4 * (4 * P + 64 * P + 64 * 4 * 49));
+    // steps 2-4: the stride-2 downsamplers (model.4 emits local and global)
+    conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a1, down_[0], 64, H, W), 128, H2, W2, down_bn_[0], 128, a2, P2, W2, nullptr)},
+                2, 2.0 * 64 * 128 * 9 * P2, f4 * (64 * P + 128 * P2 + 128 * 64 * 9));
+    conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a2, down_[1], 128, H2, W2), 256, H4, W4, down_bn_[1], 256, a3, P4, W4, nullptr)},
+                3, 2.0 * 128 * 256 * 9 * P4, f4 * (128 * P2 + 256 * P4 + 256 * 128 * 9));
+    conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a3, down_[2], 256, H4, W4), 512, H8, W8, down_bn_[2], 512, X, P8, W8, nullptr)},
+                4, 2.0 * 256 * 512 * 9 * P8, f4 * (256 * P4 + 512 * P8 + 512 * 256 * 9));
+
+    // FFT descriptors (the same buffers serve all 36 spectral transforms)
+    FftArgs fa{};
+    fa.row = frow;
+    fa.col = fcol;
+    fa.C = 192;
+    fa.H = H8;
+    fa.W = W8;
+    fa.Wh = Wh;
+    fa.scale = (float)(1.0 / std::sqrt((double)H8 * W8));
+    fa.in = Fb;
+    fa.out = Sb;
+    void *d_rfft = put(&fa, sizeof fa);
+    fa.in = S2;
+    fa.out = G;
+    fa.feat = Fb;
+    void *d_irfft = put(&fa, sizeof fa);
+    const double fft_bytes = f4 * 192 * P8 + 8.0 * 192 * PS;  // real plane + half spectrum (re, im)
+
+    // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual)
+    for (int r = 0; r < 18; ++r)
+        for (int s = 0; s < 2; ++s) {
+            const FfcW &Fw = ffc_[r * 2 + s];
+            float *src = s == 0 ? X : Y, *dst = s == 0 ? Y : X;
+            const float *res = s == 0 ? nullptr : X;
+            // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
+            conv_launch(F_CONV1,
+                        {problem(F_CONV1, seg(src + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1, 192, Fb, P8, (int)P8, nullptr)},
+                        -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384));
+            Launch L{};
+            L.fn = fn_[F_RFFT];
+            L.family = F_RFFT;
+            L.grid = 192;
+            L.shmem = (unsigned)fft_lds;
+            L.arg = d_rfft;
+            L.nparams = 1;
+            L.step_end = -1;
+            L.flops = 0;
+            L.bytes = fft_bytes;
+            p.launches.push_back(L);
+            // FourierUnit conv over the stacked spectrum + BN + ReLU
+            conv_launch(F_CONV1,
+                        {problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS, (int)PS, nullptr)},
+                        -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384));
+            L.fn = fn_[F_IRFFT];
+            L.family = F_IRFFT;
+            L.arg = d_irfft;
+            L.bytes = fft_bytes + f4 * 192 * P8;  // + the fused feat read
+            p.launches.push_back(L);
+            // local: BN_l(l2l(x_l) + g2l(x_g)); global: BN_g(l2g(x_l) + conv2(f + ifft))
+            ConvProblem ql = problem(F_CONV3, seg(src, Fw.local, 512, H8, W8), 128, H8, W8, Fw.bn_l, 128, dst, P8, W8, res);
+            ConvProblem qg = problem(F_CONV3, seg(src, Fw.l2g, 128, H8, W8), 384, H8, W8, Fw.bn_g, 384, dst + 128 * P8, P8,
+                                     W8, res ? res + 128 * P8 : nullptr);
+            qg.s1 = seg(G, Fw.conv2, 192, H8, W8);
+            const double fl = 2.0 * P8 * (128.0 * 512 * 9 + 384.0 * 128 * 9 + 384.0 * 192);
+            const double by = f4 * (512 * P8 + 192 * P8 + 512 * P8 * (res ? 2 : 1) + 128 * 512 * 9 + 384 * 128 * 9 + 384 * 192);
+            conv_launch(F_CONV3, {ql, qg}, s == 1 ? 5 + r : -1, fl, by);
+        }
+    // step 23 (concat) is the same buffer as step 22; steps 24-26 the upsamplers
+    const float *usrc[3] = {X, a3, a2};
+    float *udst[3] = {a3, a2, a1};
+    const int uh[3] = {H8, H4, H2}, uw[3] = {W8, W4, W2};
+    for (int u = 0; u < 3; ++u) {
+        const UpW &U = up_[u];
+        std::vector<ConvProblem> ph;
+        for (int k = 0; k < 4; ++k) {
+            const size_t oplane = (size_t)(2 * uh[u]) * (2 * uw[u]);
+            ConvProblem q = problem(F_CONVT, seg(usrc[u], U.ph[k], U.cin, uh[u], uw[u]), U.cout, uh[u], uw[u], U.bn, U.cout,
+                                    udst[u], oplane, 2 * uw[u], nullptr);
+            q.bias = wp(U.bias);
+            q.oy_mul = q.ox_mul = 2;
+            q.oy_off = k >> 1;
+            q.ox_off = k & 1;
+            ph.push_back(q);
+        }
+        const double pin = (double)uh[u] * uw[u];
+        conv_launch(F_CONVT, ph, 24 + u, 2.0 * U.cin * U.cout * 9 * pin,
+                    f4 * (U.cin * pin + U.cout * 4 * pin + U.cin * U.cout * 9));
+    }
+    // step 28: model.34 + sigmoid (ReflectionPad2d(3) folded into the indexing)
+    TailArgs ta{};
+    ta.src = a1;
+    ta.wt = wp(tail_w_);
+    ta.bias = wp(tail_b_);
+    ta.out = out;
+    ta.Cin = 64;
+    ta.H = H;
+    ta.W = W;
+    {
+        Launch L{};
+        L.fn = fn_[F_TAIL];
+        L.family = F_TAIL;
+        L.grid = (unsigned)(((W + 63) / 64) * ((H + 7) / 8));
+        L.arg = put(&ta, sizeof ta);
+        L.nparams = 1;
+        L.step_end = 28;
+        L.flops = 2.0 * 64 * 3 * 49 * P;
+        L.bytes = f4 * (64 * P + 3 * P);
+        p.launches.push_back(L);
+    }
+    if (desc.size() > p.arena_bytes - o_desc) {
+        err = "internal: descriptor region overflow";
+        return false;
+    }
+    // dump sources per step (nullptr: derived on the host)
+    p.step_src.assign(kSteps, {nullptr, 0});
+    p.step_src[1] = {a1, 64 * P};
+    p.step_src[2] = {a2, 128 * P2};
+    p.step_src[3] = {a3, 256 * P4};
+    for (int s = 4; s <= 23; ++s) p.step_src[s] = {X, 512 * P8};
+    p.step_src[24] = {a3, 256 * P4};
+    p.step_src[25] = {a2, 128 * P2};
+    p.step_src[26] = {a1, 64 * P};
+    p.step_src[28] = {out, 3 * P};
+
+    if (!check(hip_->hipMemcpy(base + o_desc, desc.data(), desc.size(), hipMemcpyHostToDevice), "hipMemcpy(descriptors)", err))
+        return false;
+    if (!check(hip_->hipMemcpy((void *)frow.tw, twr.data(), twr.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err))
+        return false;
+    return check(hip_->hipMemcpy((void *)fcol.tw, twc.data(), twc.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err);
+}
+
+bool Engine::launch(const Launch &L, hipStream_t s, std::string &err)
+{
+    void *arg = L.arg;
+    int nprob = L.nprob;
+    void *params[2] = {&arg, &nprob};
+    const bool prof = (prof_mask_ >> L.family) & 1u;
+    Pending pe{};
+    if (prof) {
+        for (hipEvent_t *e : {&pe.a, &pe.b}) {
+            if (!event_pool_.empty()) {
+                *e = event_pool_.back();
+                event_pool_.pop_back();
+            } else if (!check(hip_->hipEventCreate(e), "hipEventCreate", err)) {
+                return false;
+            }
+        }
+        pe.family = L.family;
+        pe.flops = L.flops;
+        pe.bytes = L.bytes;
+        if (!check(hip_->hipEventRecord(pe.a, s), "hipEventRecord", err)) return false;
+    }
+    if (!check(hip_->hipModuleLaunchKernel(L.fn, L.grid, 1, 1, LAMA_NT, 1, 1, L.shmem, s, params, nullptr),
+               kFamilyName[L.family], err))
+        return false;
+    if (prof) {
+        if (!check(hip_->hipEventRecord(pe.b, s), "hipEventRecord", err)) return false;
+        pending_.push_back(pe);
+    }
+    return true;
+}
+
+static void host_reflect_pad(const float *src, int c, int h, int w, int pad, float *dst)
+{
+    const int oh = h + 2 * pad, ow = w + 2 * pad;
+    for (int ch = 0; ch < c; ++ch)
+        for (int y = 0; y < oh; ++y) {
+            const size_t sy = lama_reflect_index(y - pad, (size_t)h);
+            for (int x = 0; x < ow; ++x)
+                dst[((size_t)ch * oh + y) * ow + x] =
+                    src[((size_t)ch * h + sy) * w + lama_reflect_index(x - pad, (size_t)w)];
+        }
+}
+
+bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
+{
+    for (const Launch &L : p.launches) {
+        if (!launch(L, s, err)) return false;
+        if (!steps || L.step_end < 0) continue;
+        int done[2] = {L.step_end, L.step_end == 22 ? 23 : -1};
+        for (int st : done) {
+            if (st < 0) continue;
+            const bool want = steps[st] || (st == 26 && steps[27]);
+            if (!want) continue;
+            auto src = p.step_src[st];
+            std::vector<float> tmp;
+            float *dst = steps[st];
+            if (!dst) {
+                tmp.resize(src.second);
+                dst = tmp.data();
+            }
+            if (!check(hip_->hipMemcpyAsync(dst, src.first, src.second * 4, hipMemcpyDeviceToHost, s), "hipMemcpy(dump)", err) ||
+                !check(hip_->hipStreamSynchronize(s), "hipStreamSynchronize", err))
+                return false;
+            if (st == 26 && steps[27]) host_reflect_pad(dst, 64, p.H, p.W, 3, steps[27]);
+        }
+    }
+    return true;
+}
+
+bool Engine::forward_host(const float *in, int h, int w, float *out, float *const *steps, std::string &err)
+{
+    Plan *p = plan_for(h, w, err);
+    if (!p) return false;
+    if (steps && steps[0]) host_reflect_pad(in, 4, h, w, 3, steps[0]);
+    if (!check(hip_->hipMemcpyAsync(p->in, in, 4ul * h * w * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(input)", err))
+        return false;
+    if (!run(*p, stream_, steps, err)) return false;
+    if (!check(hip_->hipMemcpyAsync(out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(output)", err))
+        return false;
+    return check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err);
+}
+
+bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err)
+{
+    Plan *p = plan_for(h, w, err);
+    if (!p) return false;
+    if (!s) s = stream_;
+    if (!check(hip_->hipMemcpyAsync(p->in, d_in, 4ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(input)", err))
+        return false;
+    if (!run(*p, s, nullptr, err)) return false;
+    return check(hip_->hipMemcpyAsync(d_out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err);
+}
+
+int Engine::launch_count(int h, int w)
+{
+    auto it = plans_.find({h, w});
+    return it == plans_.end() ? -1 : (int)it->second.launches.size();
+}
+
+void Engine::collect_events()
+{
+    for (auto &pe : pending_) {
+        float ms = 0.f;
+        if (hip_->hipEventSynchronize(pe.b) == hipSuccess && hip_->hipEventElapsedTime(&ms, pe.a, pe.b) == hipSuccess) {
+            prof_launches_[pe.family] += 1;
+            prof_ms_[pe.family] += ms;
+            prof_flops_[pe.family] += pe.flops;
+            prof_bytes_[pe.family] += pe.bytes;
+        }
+        event_pool_.push_back(pe.a);
+        event_pool_.push_back(pe.b);
+    }
+    pending_.clear();
+}
+
+void Engine::profile_reset()
+{
+    collect_events();
+    for (int f = 0; f < F_COUNT; ++f) {
+        prof_launches_[f] = 0;
+        prof_ms_[f] = prof_flops_[f] = prof_bytes_[f] = 0;
+    }
+}
+
+bool Engine::profile_read(int i, std::string &name, uint64_t &launches, double &ms, double &flops, double &bytes)
+{
+    if (i < 0 || i >= F_COUNT) return false;
+    collect_events();
+    name = kFamilyName[i];
+    launches = prof_launches_[i];
+    ms = prof_ms_[i];
+    flops = prof_flops_[i];
+    bytes = prof_bytes_[i];
+    return true;
+}
+
+// ---------------------------------------------------------------- single ops
+
+namespace {
+// Device allocations of one test op, released on scope exit.
+struct Scratch {
+    const HipApi *h;
+    std::vector<void *> ptrs;
+    ~Scratch()
+    {
+        for (void *p : ptrs) h->hipFree(p);
+    }
+};
+}  // namespace
+
+#define UPLOAD(var, hostptr, nfloats)                                                                 \
+    float *var = nullptr;                                                                             \
+    if (!check(hip_->hipMalloc((void **)&var, std::max<size_t>(1, (nfloats)) * 4), "hipMalloc", err)) \
+        return false;                                                                                 \
+    sc.ptrs.push_back(var);                                                                           \
+    if ((hostptr) && !check(hip_->hipMemcpy(var, (hostptr), (nfloats) * 4, hipMemcpyHostToDevice), "hipMemcpy", err)) \
+        return false;
+
+bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, const float *bias, int cout, int k,
+                       int stride, const float *scale, const float *shift, int relu, float *out, std::string &err)
+{
+    int family;
+    if (k == 1 && stride == 1)
+        family = F_CONV1;
+    else if (k == 3 && stride == 1)
+        family = F_CONV3;
+    else if (k == 3 && stride == 2)
+        family = F_CONV3S2;
+    else if (k == 7 && stride == 1)
+        family = F_CONV7;
+    else {
+        err = "op_conv2d: unsupported k/stride";
+        return false;
+    }
+    const int pad = k / 2;
+    const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
+    const int KC = family == F_CONV1 ? 32 : family == F_CONV7 ? 4 : 8;
+    Arena A;
+    const int T = k * k;
+    Packed pk = pack(A, cout, cin, T, KC, [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; });
+    size_t bn = A.add(2 * (size_t)cout);
+    for (int i = 0; i < cout; ++i) {
+        A.h[bn + i] = scale ? scale[i] : 1.f;
+        A.h[bn + cout + i] = scale ? shift[i] : 0.f;
+    }
+    size_t bo = A.add(cout);
+    if (bias) std::copy(bias, bias + cout, A.h.begin() + bo);
+    Scratch sc{hip_, {}};
+    UPLOAD(dx, x, (size_t)cin * h * w);
+    UPLOAD(dw, A.h.data(), A.h.size());
+    UPLOAD(dout, nullptr, (size_t)cout * oh * ow);
+    ConvProblem q{};
+    q.s0.src = dx;
+    q.s0.wt = dw + pk.off;
+    q.s0.C = cin;
+    q.s0.IH = family == F_CONV1 ? 1 : h;
+    q.s0.IW = family == F_CONV1 ? h * w : w;
+    q.s0.nchunk = pk.nchunk;
+    q.s0.wrow = pk.wrow;
+    q.M = cout;
+    q.OH = family == F_CONV1 ? 1 : oh;
+    q.OW = family == F_CONV1 ? oh * ow : ow;
+    int tr, tc;
+    tile_shape(family, tr, tc);
+    q.tiles_x = (q.OW + tc - 1) / tc;
+    q.tiles_y = (q.OH + tr - 1) / tr;
+    q.mblocks = (cout + 63) / 64;
+    q.nblocks = q.tiles_x * q.tiles_y * q.mblocks;
+    q.bias = bias ? dw + bo : nullptr;
+    q.scale = scale ? dw + bn : nullptr;
+    q.shift = scale ? dw + bn + cout : nullptr;
+    q.relu = relu;
+    q.out = dout;
+    q.out_cstride = (long)oh * ow;
+    q.outW = q.OW;
+    q.oy_mul = q.ox_mul = 1;
+    UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
+    if (!check(hip_->hipMemcpy(dq, &q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    Launch L{};
+    L.fn = fn_[family];
+    L.family = family;
+    L.grid = (unsigned)q.nblocks;
+    L.arg = dq;
+    L.nprob = 1;
+    L.nparams = 2;
+    if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
+    return check(hip_->hipMemcpy(out, dout, (size_t)cout * oh * ow * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);
+}
+
+bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, const float *bias, int cout,
+                      const float *scale, const float *shift, int relu, float *out, std::string &err)
+{
+    Arena A;
+    Packed ph[4];
+    for (int k = 0; k < 4; ++k) {
+        const int py = k >> 1, px = k & 1, nx = 1 + px;
+        ph[k] = pack(A, cout, cin, (1 + py) * nx, 8, [&](int co, int ci, int t) {
+            const int a = t / nx, b = t % nx;
+            const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
+            return wt[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
+        });
+    }
+    size_t bn = A.add(2 * (size_t)cout), bo = A.add(cout);
+    for (int i = 0; i < cout; ++i) {
+        A.h[bn + i] = scale ? scale[i] : 1.f;
+        A.h[bn + cout + i] = scale ? shift[i] : 0.f;
+        A.h[bo + i] = bias ? bias[i] : 0.f;
+    }
+    Scratch sc{hip_, {}};
+    UPLOAD(dx, x, (size_t)cin * h * w);
+    UPLOAD(dw, A.h.data(), A.h.size());
+    UPLOAD(dout, nullptr, (size_t)cout * 4 * h * w);
+    ConvProblem q[4];
+    unsigned nb = 0;
+    for (int k = 0; k < 4; ++k) {
+        ConvProblem &c = q[k];
+        std::memset(&c, 0, sizeof c);
+        c.s0.src = dx;
+        c.s0.wt = dw + ph[k].off;
+        c.s0.C = cin;
+        c.s0.IH = h;
+        c.s0.IW = w;
+        c.s0.nchunk = ph[k].nchunk;
+        c.s0.wrow = ph[k].wrow;
+        c.M = cout;
+        c.OH = h;
+        c.OW = w;
+        c.tiles_x = (w + 31) / 32;
+        c.tiles_y = (h + 1) / 2;
+        c.mblocks = (cout + 63) / 64;
+        c.nblocks = c.tiles_x * c.tiles_y * c.mblocks;
+        nb += c.nblocks;
+        c.bias = dw + bo;
+        c.scale = dw + bn;
+        c.shift = dw + bn + cout;
+        c.relu = relu;
+        c.out = dout;
+        c.out_cstride = 4l * h * w;
+        c.outW = 2 * w;
+        c.oy_mul = c.ox_mul = 2;
+        c.oy_off = k >> 1;
+        c.ox_off = k & 1;
+    }
+    UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
+    if (!check(hip_->hipMemcpy(dq, q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    Launch L{};
+    L.fn = fn_[F_CONVT];
+    L.family = F_CONVT;
+    L.grid = nb;
+    L.arg = dq;
+    L.nprob = 4;
+    L.nparams = 2;
+    if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
+    return check(hip_->hipMemcpy(out, dout, (size_t)cout * 4 * h * w * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);
+}
+
+bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int h, int w, float *out, std::string &err)
+{
+    FftLen fr, fc;
+    std::vector<float> twr, twc;
+    if (!fft_len(w, fr, twr, err) || !fft_len(h, fc, twc, err)) return false;
+    const int Wh = w / 2 + 1, HP = (h + 1) / 2;
+    const size_t lds = 2 * std::max((size_t)HP * w, (size_t)h * Wh) * 8;
+    if (lds > 160 * 1024) {
+        err = "plane too large for the LDS-resident FFT";
+        return false;
+    }
+    const size_t nin = inverse ? 2ul * c * h * Wh : (size_t)c * h * w;
+    const size_t nout = inverse ? (size_t)c * h * w : 2ul * c * h * Wh;
+    std::vector<float> zeros;
+    if (inverse && !feat) {
+        zeros.assign((size_t)c * h * w, 0.f);
+        feat = zeros.data();
+    }
+    Scratch sc{hip_, {}};
+    UPLOAD(din, in, nin);
+    UPLOAD(dout, nullptr, nout);
+    UPLOAD(dtr, twr.data(), twr.size());
+    UPLOAD(dtc, twc.data(), twc.size());
+    UPLOAD(dfeat, inverse ? feat : nullptr, inverse ? (size_t)c * h * w : 1);
+    FftArgs a{};
+    a.row = fr;
+    a.col = fc;
+    a.row.tw = dtr;
+    a.col.tw = dtc;
+    a.C = c;
+    a.H = h;
+    a.W = w;
+    a.Wh = Wh;
+    a.in = din;
+    a.out = dout;
+    a.feat = inverse ? dfeat : nullptr;
+    a.scale = (float)(1.0 / std::sqrt((double)h * w));
+    UPLOAD(da, nullptr, (sizeof a + 3) / 4);
+    if (!check(hip_->hipMemcpy(da, &a, sizeof a, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    Launch L{};
+    L.fn = fn_[inverse ? F_IRFFT : F_RFFT];
+    L.family = inverse ? F_IRFFT : F_RFFT;
+    L.grid = (unsigned)c;
+    L.shmem = (unsigned)lds;
+    L.arg = da;
+    L.nparams = 1;
+    if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
+    return check(hip_->hipMemcpy(out, dout, nout * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);
+}
+
+bool Engine::op_tail(const float *x, int cin, int h, int w, const float *wt, const float *bias, float *out,
+                     std::string &err)
+{
+    Scratch sc{hip_, {}};
+    UPLOAD(dx, x, (size_t)cin * h * w);
+    UPLOAD(dw, wt, (size_t)3 * cin * 49);
+    UPLOAD(db, bias, 3);
+    UPLOAD(dout, nullptr, (size_t)3 * h * w);
+    TailArgs a{};
+    a.src = dx;
+    a.wt = dw;
+    a.bias = db;
+    a.out = dout;
+    a.Cin = cin;
+    a.H = h;
+    a.W = w;
+    UPLOAD(da, nullptr, (sizeof a + 3) / 4);
+    if (!check(hip_->hipMemcpy(da, &a, sizeof a, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    Launch L{};
+    L.fn = fn_[F_TAIL];
+    L.family = F_TAIL;
+    L.grid = (unsigned)(((w + 63) / 64) * ((h + 7) / 8));
+    L.arg = da;
+    L.nparams = 1;
+    if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
+    return check(hip_->hipMemcpy(out, dout, (size_t)3 * h * w * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);
+}
+
+}  // namespace lama

@@ -1,0 +1,126 @@
+// The HIP engine behind lama_hip.h: weights resident on the device, one
+// preplanned buffer set and launch list per input shape.
+#pragma once
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "hip_api.h"
+#include "kernels/common.h"
+#include "lama_host.h"
+
+namespace lama {
+
+enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_COUNT };
+extern const char *const kFamilyName[F_COUNT];
+
+// Number of plan steps of the reference (model.rs:135-207) and the size in
+// floats of the activation after each (cpu.rs:536-546 dump layout).
+constexpr int kSteps = 29;
+size_t step_numel(int step, int h, int w);
+
+// Convolution weights packed for the MFMA kernels: [M][nchunk][taps][KC].
+struct Packed {
+    size_t off = 0;  // float offset in the weight arena
+    int M = 0, C = 0, T = 0, KC = 0, nchunk = 0, wrow = 0;
+};
+
+struct Launch {
+    hipFunction_t fn;
+    int family;
+    unsigned grid;
+    unsigned shmem;
+    void *arg;   // device pointer to this launch's descriptor(s)
+    int nprob;   // conv kernels: number of problems (second parameter)
+    int nparams;
+    int step_end;  // plan step completed by this launch, or -1
+    double flops, bytes;
+};
+
+struct Plan {
+    int H = 0, W = 0;
+    void *arena = nullptr;
+    size_t arena_bytes = 0;
+    float *in = nullptr, *out = nullptr;
+    std::vector<std::pair<const float *, size_t>> step_src;  // per step (nullptr: host-derived)
+    std::vector<Launch> launches;
+};
+
+class Engine {
+public:
+    ~Engine();
+    bool open(std::string &err);
+    bool load_weights(const uint8_t *blob, size_t len, const lama_tensor_info *t, size_t n, std::string &err);
+    bool forward_host(const float *in, int h, int w, float *out, float *const *steps, std::string &err);
+    bool forward_device(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err);
+
+    // profiling (families whose bit is set get per-launch events)
+    void set_profile(uint32_t mask) { prof_mask_ = mask; }
+    void profile_reset();
+    bool profile_read(int i, std::string &name, uint64_t &launches, double &ms, double &flops, double &bytes);
+    int launch_count(int h, int w);
+
+    // single kernel families (parity tests)
+    bool op_conv2d(const float *x, int cin, int h, int w, const float *wt, const float *bias, int cout, int k,
+                   int stride, const float *scale, const float *shift, int relu, float *out, std::string &err);
+    bool op_convt(const float *x, int cin, int h, int w, const float *wt, const float *bias, int cout,
+                  const float *scale, const float *shift, int relu, float *out, std::string &err);
+    bool op_fft(bool inverse, const float *in, const float *feat, int c, int h, int w, float *out, std::string &err);
+    bool op_tail(const float *x, int cin, int h, int w, const float *wt, const float *bias, float *out,
+                 std::string &err);
+
+    const HipApi *hip() const { return hip_; }
+    hipStream_t stream() const { return stream_; }
+    bool check(hipError_t e, const char *what, std::string &err);
+
+private:
+    struct FfcW {
+        Packed local, l2g, conv2, conv1, fu;
+        size_t bn1, fu_bn, bn_l, bn_g;  // folded: scale at off, shift at off + n
+    };
+    struct UpW {
+        Packed ph[4];
+        size_t bias = 0, bn = 0;
+        int cin = 0, cout = 0;
+    };
+
+    Plan *plan_for(int h, int w, std::string &err);
+    bool build_plan(Plan &p, std::string &err);
+    bool run(Plan &p, hipStream_t s, float *const *steps, std::string &err);
+    bool launch(const Launch &L, hipStream_t s, std::string &err);
+    bool fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err);
+    void collect_events();
+
+    const HipApi *hip_ = nullptr;
+    int device_ = 0;
+    hipModule_t module_ = nullptr;
+    hipFunction_t fn_[F_COUNT] = {};
+    hipStream_t stream_ = nullptr;
+
+    // weights
+    bool have_weights_ = false;
+    float *warena_ = nullptr;
+    Packed head_, down_[3];
+    size_t head_bn_ = 0, down_bn_[3] = {0, 0, 0};
+    FfcW ffc_[36];
+    UpW up_[3];
+    size_t tail_w_ = 0, tail_b_ = 0;
+    const float *wp(size_t off) const { return warena_ + off; }
+
+    std::map<std::pair<int, int>, Plan> plans_;
+
+    // profiling
+    uint32_t prof_mask_ = 0;
+    struct Pending {
+        hipEvent_t a, b;
+        int family;
+        double flops, bytes;
+    };
+    std::vector<Pending> pending_;
+    std::vector<hipEvent_t> event_pool_;
+    uint64_t prof_launches_[F_COUNT] = {};
+    double prof_ms_[F_COUNT] = {}, prof_flops_[F_COUNT] = {}, prof_bytes_[F_COUNT] = {};
+};
+
+}  // namespace lama

@@ -1,0 +1,251 @@
+"""ctypes binding of liblama_hip.so (include/lama_hip.h), mirroring the
+reference's engine interface: `run(store, model, input, h, w)` is
+`cuda::run` (lama-rs/src/cuda.rs:1542-1548) and raises where it returns Err.
+
+There is no fallback: if the library is not built or no gfx950 device can be
+opened, every call raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import host_api
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+HIP_SO = os.path.join(HERE, "lib", "liblama_hip.so")
+
+FAMILIES = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt", "rfft2", "irfft2", "tail"]
+N_STEPS = 29
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(HIP_SO):
+            raise RuntimeError(f"{HIP_SO} is not built: the HIP backend is unavailable (run __graft_entry__.build())")
+        host_api.lib()  # liblama_hip.so links liblama_host.so
+        L = ctypes.CDLL(HIP_SO)
+        vp, cp, sz = ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t
+        fp = ctypes.POINTER(ctypes.c_float)
+        L.lama_hip_open.argtypes = [ctypes.POINTER(vp), cp, sz]
+        L.lama_hip_close.argtypes = [vp]
+        L.lama_hip_load_weights.argtypes = [vp, vp, sz, ctypes.POINTER(host_api.TensorInfo), sz, cp, sz]
+        L.lama_hip_forward.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, fp, cp, sz]
+        L.lama_hip_forward_device.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, cp, sz]
+        L.lama_hip_forward_steps.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(fp), cp, sz]
+        L.lama_hip_vram.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64), cp, sz, cp, sz]
+        L.lama_hip_profile.argtypes = [vp, ctypes.c_uint32]
+        L.lama_hip_profile_reset.argtypes = [vp]
+        L.lama_hip_profile_read.argtypes = [vp, ctypes.c_int, cp, sz, ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_double)]
+        L.lama_hip_print_stats.argtypes = [vp]
+        L.lama_hip_launch_count.argtypes = [vp, ctypes.c_int, ctypes.c_int]
+        L.lama_hip_malloc.argtypes = [vp, sz, ctypes.POINTER(vp), cp, sz]
+        L.lama_hip_free.argtypes = [vp, vp]
+        L.lama_hip_memcpy.argtypes = [vp, vp, vp, sz, ctypes.c_int, cp, sz]
+        L.lama_hip_synchronize.argtypes = [vp, cp, sz]
+        L.lama_hip_op_conv2d.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, fp, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, fp, fp, ctypes.c_int, fp, cp, sz]
+        L.lama_hip_op_conv_transpose.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, fp,
+                                                 ctypes.c_int, fp, fp, ctypes.c_int, fp, cp, sz]
+        L.lama_hip_op_rfft2.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, cp, sz]
+        L.lama_hip_op_irfft2.argtypes = [vp, fp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, cp, sz]
+        L.lama_hip_op_tail.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, fp, fp, cp, sz]
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    return None if a is None else a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _c(a):
+    return None if a is None else np.ascontiguousarray(a, np.float32)
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class Engine:
+    """One device context (lama_hip_open) with resident weights."""
+
+    def __init__(self):
+        self._err = ctypes.create_string_buffer(4096)
+        h = ctypes.c_void_p()
+        if lib().lama_hip_open(ctypes.byref(h), self._err, 4096):
+            raise HipError(self._msg())
+        self.ctx = h
+
+    def _msg(self):
+        return self._err.value.decode(errors="replace")
+
+    def _check(self, rc):
+        if rc:
+            raise HipError(self._msg())
+
+    def close(self):
+        if getattr(self, "ctx", None):
+            lib().lama_hip_close(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        self.close()
+
+    def load_weights(self, store):
+        """store: host_api.Store (the mapped container and its index)."""
+        ptr, n = store.bytes_ptr()
+        self._store = store  # the container must outlive the call
+        self._check(lib().lama_hip_load_weights(self.ctx, ptr, n, store.table(), len(store), self._err, 4096))
+
+    def forward(self, x):
+        x = _c(x)
+        _, h, w = x.shape
+        out = np.empty((3, h, w), np.float32)
+        self._check(lib().lama_hip_forward(self.ctx, _f(x), h, w, _f(out), self._err, 4096))
+        return out
+
+    def forward_steps(self, x, steps):
+        """Forward that also returns {step: activation} for the requested
+        plan steps (the reference's LAMA_DUMP_STEP layout)."""
+        x = _c(x)
+        _, h, w = x.shape
+        out = np.empty((3, h, w), np.float32)
+        arr = (ctypes.POINTER(ctypes.c_float) * N_STEPS)()
+        dumps = {}
+        for s in steps:
+            d = np.empty(step_numel(s, h, w), np.float32)
+            dumps[s] = d
+            arr[s] = _f(d)
+        self._check(lib().lama_hip_forward_steps(self.ctx, _f(x), h, w, _f(out), arr, self._err, 4096))
+        return out, dumps
+
+    def forward_device(self, d_in, h, w, d_out, stream=None):
+        self._check(lib().lama_hip_forward_device(self.ctx, d_in, h, w, d_out, stream, self._err, 4096))
+
+    # device buffers
+    def malloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self._check(lib().lama_hip_malloc(self.ctx, nbytes, ctypes.byref(p), self._err, 4096))
+        return p.value
+
+    def free(self, p):
+        lib().lama_hip_free(self.ctx, p)
+
+    def upload(self, dptr, a):
+        a = np.ascontiguousarray(a)
+        self._check(lib().lama_hip_memcpy(self.ctx, dptr, a.ctypes.data, a.nbytes, 1, self._err, 4096))
+
+    def download(self, a, dptr):
+        self._check(lib().lama_hip_memcpy(self.ctx, a.ctypes.data, dptr, a.nbytes, 2, self._err, 4096))
+        return a
+
+    def synchronize(self):
+        self._check(lib().lama_hip_synchronize(self.ctx, self._err, 4096))
+
+    # profiling
+    def profile(self, families):
+        mask = 0
+        for f in families:
+            mask |= 1 << FAMILIES.index(f)
+        lib().lama_hip_profile(self.ctx, mask)
+
+    def profile_reset(self):
+        lib().lama_hip_profile_reset(self.ctx)
+
+    def profile_read(self):
+        out = {}
+        name = ctypes.create_string_buffer(64)
+        n = ctypes.c_uint64()
+        ms, fl, by = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        i = 0
+        while lib().lama_hip_profile_read(self.ctx, i, name, 64, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl),
+                                          ctypes.byref(by)):
+            out[name.value.decode()] = dict(launches=n.value, ms=ms.value, flops=fl.value, bytes=by.value)
+            i += 1
+        return out
+
+    def print_stats(self):
+        lib().lama_hip_print_stats(self.ctx)
+
+    def launch_count(self, h, w):
+        return lib().lama_hip_launch_count(self.ctx, h, w)
+
+    # single kernel families (parity tests)
+    def op_conv2d(self, x, wt, bias=None, stride=1, scale=None, shift=None, relu=False):
+        x, wt, bias, scale, shift = map(_c, (x, wt, bias, scale, shift))
+        cin, h, w = x.shape
+        cout, _, k, _ = wt.shape
+        pad = k // 2
+        oh, ow = (h + 2 * pad - k) // stride + 1, (w + 2 * pad - k) // stride + 1
+        out = np.empty((cout, oh, ow), np.float32)
+        self._check(lib().lama_hip_op_conv2d(self.ctx, _f(x), cin, h, w, _f(wt), _f(bias), cout, k, stride,
+                                             _f(scale), _f(shift), int(relu), _f(out), self._err, 4096))
+        return out
+
+    def op_conv_transpose(self, x, wt, bias, scale=None, shift=None, relu=False):
+        x, wt, bias, scale, shift = map(_c, (x, wt, bias, scale, shift))
+        cin, h, w = x.shape
+        cout = wt.shape[1]
+        out = np.empty((cout, 2 * h, 2 * w), np.float32)
+        self._check(lib().lama_hip_op_conv_transpose(self.ctx, _f(x), cin, h, w, _f(wt), _f(bias), cout, _f(scale),
+                                                     _f(shift), int(relu), _f(out), self._err, 4096))
+        return out
+
+    def op_rfft2(self, x):
+        x = _c(x)
+        c, h, w = x.shape
+        out = np.empty((2 * c, h, w // 2 + 1), np.float32)
+        self._check(lib().lama_hip_op_rfft2(self.ctx, _f(x), c, h, w, _f(out), self._err, 4096))
+        return out
+
+    def op_irfft2(self, spec, w, feat=None):
+        spec, feat = _c(spec), _c(feat)
+        c2, h, _ = spec.shape
+        out = np.empty((c2 // 2, h, w), np.float32)
+        self._check(lib().lama_hip_op_irfft2(self.ctx, _f(spec), _f(feat), c2 // 2, h, w, _f(out), self._err, 4096))
+        return out
+
+    def op_tail(self, x, wt, bias):
+        x, wt, bias = map(_c, (x, wt, bias))
+        cin, h, w = x.shape
+        out = np.empty((3, h, w), np.float32)
+        self._check(lib().lama_hip_op_tail(self.ctx, _f(x), cin, h, w, _f(wt), _f(bias), _f(out), self._err, 4096))
+        return out
+
+
+def step_numel(step, h, w):
+    h8, w8 = h // 8, w // 8
+    table = {0: 4 * (h + 6) * (w + 6), 1: 64 * h * w, 2: 128 * (h // 2) * (w // 2), 3: 256 * (h // 4) * (w // 4),
+             24: 256 * (h // 4) * (w // 4), 25: 128 * (h // 2) * (w // 2), 26: 64 * h * w,
+             27: 64 * (h + 6) * (w + 6), 28: 3 * h * w}
+    return table.get(step, 512 * h8 * w8 if 4 <= step <= 23 else 0)
+
+
+def vram():
+    """mem.rs device_memory(): (free, total, name) or None."""
+    f, t = ctypes.c_uint64(), ctypes.c_uint64()
+    name = ctypes.create_string_buffer(256)
+    err = ctypes.create_string_buffer(1024)
+    if lib().lama_hip_vram(ctypes.byref(f), ctypes.byref(t), name, 256, err, 1024):
+        return None
+    return f.value, t.value, name.value.decode()
+
+
+_ENGINE = None
+
+
+def run(store, model, input, h, w):
+    """cuda::run: one forward over [4][h][w] -> [3][h][w] with a
+    process-wide engine whose weights stay resident (cuda.rs:222-231)."""
+    global _ENGINE
+    if _ENGINE is None or getattr(_ENGINE, "_store", None) is not store:
+        if _ENGINE is None:
+            _ENGINE = Engine()
+        _ENGINE.load_weights(store)
+    x = np.asarray(input, np.float32).reshape(4, h, w)
+    return _ENGINE.forward(x)

@@ -1,0 +1,107 @@
+"""Each HIP kernel family against the CPU oracle on seeded random data.
+
+Tolerance: FP32 MFMA products with FP32 accumulation in a different order
+than the oracle's sequential sum -- relative L2 error <= 1e-5 for the GEMM
+families and the f32 FFT (the oracle's FFT runs in f64), far inside the
+1e-3 per-layer bound the north star states.
+"""
+import numpy as np
+import pytest
+
+import oracle_api as O
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _bn(rng, c):
+    return (rng.uniform(0.5, 1.5, c).astype(np.float32), rng.normal(0, 0.1, c).astype(np.float32))
+
+
+def _oracle_bn_relu(y, s, t):
+    # cpu.rs:66-76 then 376-382
+    y = y * s[:, None, None]
+    y = y + t[:, None, None]
+    return np.where(y < 0, np.float32(0), y)
+
+
+@pytest.mark.parametrize("cin,cout,h,w,k,stride", [
+    (40, 72, 13, 37, 3, 1),    # ragged channel chunk, partial tiles, M % 64 != 0
+    (128, 128, 16, 16, 3, 1),  # resblock l2l shape at a 128x128 input
+    (16, 24, 9, 70, 3, 2),     # stride 2, odd height
+    (64, 128, 32, 32, 3, 2),   # model.2 shape at a 64x64 input
+    (4, 64, 20, 40, 7, 1),     # model.1 head (cin 4)
+    (6, 10, 8, 8, 7, 1),       # 7x7 on a plane barely wider than the kernel
+    (384, 192, 8, 8, 1, 1),    # SpectralTransform conv1
+    (40, 70, 5, 33, 1, 1),     # 1x1, ragged everything
+])
+def test_conv2d(engine, cin, cout, h, w, k, stride):
+    rng = np.random.default_rng(cin * 1000 + cout + k)
+    x = rng.standard_normal((cin, h, w), np.float32)
+    wt = (rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32)
+    s, t = _bn(rng, cout)
+    got = engine.op_conv2d(x, wt, None, stride, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv2d(x, wt, None, pad=k // 2, stride=stride, reflect=True), s, t)
+    assert got.shape == ref.shape
+    assert rel_err(got, ref) < TOL
+
+
+def test_conv2d_bias_no_bn(engine):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((12, 11, 19), np.float32)
+    wt = rng.standard_normal((5, 12, 3, 3)).astype(np.float32)
+    b = rng.standard_normal(5).astype(np.float32)
+    got = engine.op_conv2d(x, wt, b, 1)
+    ref = O.conv2d(x, wt, b, pad=1, stride=1, reflect=True)
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("cin,cout,h,w", [(32, 16, 5, 7), (512, 256, 8, 8), (64, 64, 3, 40)])
+def test_conv_transpose(engine, cin, cout, h, w):
+    rng = np.random.default_rng(cin + cout + h)
+    x = np.maximum(rng.standard_normal((cin, h, w)), 0).astype(np.float32)  # post-ReLU: zeros are skipped
+    wt = (rng.standard_normal((cin, cout, 3, 3)) * np.sqrt(2.0 / (cout * 9))).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.05).astype(np.float32)
+    s, t = _bn(rng, cout)
+    got = engine.op_conv_transpose(x, wt, b, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv_transpose(x, wt, b), s, t)
+    assert rel_err(got, ref) < TOL
+
+
+SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), (64, 33), (16, 12), (38, 19)]
+
+
+@pytest.mark.parametrize("h,w", SIZES)
+def test_rfft2(engine, h, w):
+    rng = np.random.default_rng(h * 100 + w)
+    c = 3
+    x = rng.standard_normal((c, h, w), np.float32)
+    got = engine.op_rfft2(x)
+    ref = np.concatenate([O.rfft2_ortho(x[i]) for i in range(c)], axis=0)
+    assert got.shape == ref.shape
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("h,w", SIZES)
+def test_irfft2(engine, h, w):
+    rng = np.random.default_rng(h * 100 + w + 1)
+    c = 3
+    wh = w // 2 + 1
+    spec = rng.standard_normal((2 * c, h, wh), np.float32)  # not Hermitian: exercises the completion rule
+    feat = rng.standard_normal((c, h, w), np.float32)
+    got = engine.op_irfft2(spec, w, feat)
+    ref = np.stack([O.irfft2_ortho(spec[2 * i:2 * i + 2], w) for i in range(c)]) + feat
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("h,w", [(16, 64), (24, 40), (8, 8), (64, 128)])
+def test_tail(engine, h, w):
+    rng = np.random.default_rng(h + w)
+    x = rng.standard_normal((64, h, w), np.float32)
+    wt = (rng.standard_normal((3, 64, 7, 7)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(3) * 0.05).astype(np.float32)
+    got = engine.op_tail(x, wt, b)
+    z = O.conv2d(O.reflect_pad(x, 3), wt, b, pad=0, stride=1, reflect=False)
+    ref = (1.0 / (1.0 + np.exp(-z.astype(np.float64)))).astype(np.float32)
+    assert rel_err(got, ref) < TOL
