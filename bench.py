@@ -1,0 +1,170 @@
+#!/usr/bin/env python3
+"""Throughput of the Big-LaMa FP32 generator forward on one MI355X.
+
+Workload: one 512x512 whole-image pass, batch 1,
+seeded random-init weights of the real architecture (989 tensors), a seeded
+blurred-noise image with a ~25% brush-stroke mask.  A "step" is one forward
+pass; the input tensor is resident in HBM before the timed region starts.
+
+Prints one JSON line: passes/s, the roofline of the dominant kernel (the FFC
+3x3 implicit-GEMM family, algorithmic FLOPs per launch / mean launch time from
+HIP events on its stream, against the 157.3 TFLOP/s FP32 MFMA peak), and the
+CPU baseline (the C restatement of the reference CPU engine, timed on this
+host's cores on one bounded pass).
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
+PEAK_HBM = 8000.0  # GB/s
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--size", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-size", type=int, default=0, help="CPU sample size (default: the workload size)")
+    ap.add_argument("--traffic", type=str, default=None,
+                    help="JSON file with measured HBM bytes per launch of the dominant kernel")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this backend runs one forward on one GPU; multi-GPU runs are not part of this build "
+              "(a batch-1 pass does not shard; see DESIGN.md for how it would)", file=sys.stderr)
+        sys.exit(2)
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    H = pkg.host_api
+    E = pkg.hip_engine
+    S = args.size
+
+    tmp = tempfile.mkdtemp(prefix="lama_bench_")
+    wpath = os.path.join(tmp, "big-lama-synth.safetensors")
+    H.synth_weights(wpath, 0)
+    store = H.Store(wpath)
+    eng = E.Engine()
+    eng.load_weights(store)
+
+    img = H.synth_image(S, S, 1)
+    mask, coverage = H.synth_mask_strokes(S, S, 0.25, 2)
+    x = H.build_input(img, mask)
+    d_in = eng.malloc(x.nbytes)
+    d_out = eng.malloc(3 * S * S * 4)
+    eng.upload(d_in, x)
+
+    for _ in range(args.warmup):
+        eng.forward_device(d_in, S, S, d_out)
+    eng.synchronize()
+
+    dom = "conv3x3"
+    eng.profile([dom])
+    eng.profile_reset()
+    eng.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.forward_device(d_in, S, S, d_out)
+    eng.synchronize()
+    elapsed = time.perf_counter() - t0
+    prof = eng.profile_read()
+    eng.profile(())
+
+    # per-family device times in one extra (untimed) profiled pass set
+    eng.profile(E.FAMILIES)
+    eng.profile_reset()
+    for _ in range(3):
+        eng.forward_device(d_in, S, S, d_out)
+    eng.synchronize()
+    fam = eng.profile_read()
+    eng.profile(())
+
+    out = np.empty((3, S, S), np.float32)
+    eng.download(out, d_out)
+    assert np.isfinite(out).all()
+
+    ms = elapsed * 1e3 / args.steps
+    d = prof[dom]
+    launch_ms = d["ms"] / max(1, d["launches"])
+    flops_launch = d["flops"] / max(1, d["launches"])
+    achieved = flops_launch / (launch_ms * 1e-3) / 1e12
+    traffic = None
+    if args.traffic and os.path.exists(args.traffic):
+        with open(args.traffic) as fh:
+            traffic = json.load(fh).get(dom)
+
+    conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt"]
+    conv_ms = sum(fam[f]["ms"] for f in conv_fams) / 3
+    conv_flops = sum(fam[f]["flops"] for f in conv_fams) / 3
+    fft_ms = sum(fam[f]["ms"] for f in ("rfft2", "irfft2")) / 3
+    fft_bytes = sum(fam[f]["bytes"] for f in ("rfft2", "irfft2")) / 3
+    per_family = {f: {"ms_per_pass": round(v["ms"] / 3, 4), "launches_per_pass": v["launches"] // 3,
+                      "tflops": round(v["flops"] / (v["ms"] * 1e9), 2) if v["ms"] > 0 else None,
+                      "gbps": round(v["bytes"] / (v["ms"] * 1e6), 1) if v["ms"] > 0 else None}
+                  for f, v in fam.items()}
+
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_api as O
+
+        cs = args.cpu_size or S
+        net = O.OracleNet(O.read_safetensors(wpath))
+        cimg = H.synth_image(cs, cs, 1)
+        cmask, _ = H.synth_mask_strokes(cs, cs, 0.25, 2)
+        cx = H.build_input(cimg, cmask)
+        t = time.perf_counter()
+        net.forward(cx)
+        cpu_s = time.perf_counter() - t
+        scale = (cs / S) ** 2  # work scales with the pixel count
+        cpu = {"value": round(scale / cpu_s, 5), "unit": "passes/s", "cores": O.lib().or_num_threads(),
+               "kind": "port",
+               "sample": f"one {cs}x{cs} whole-image pass of the C restatement of cpu.rs "
+                         f"(-O3 -ffp-contract=off, OpenMP), {cpu_s:.2f} s"
+                         + ("" if cs == S else f", scaled by pixel count to {S}x{S}")}
+
+    line = {
+        "metric": "512x512 inpaint passes/sec (FP32, batch 1)",
+        "value": round(args.steps / elapsed, 3),
+        "unit": "passes/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random-init Big-LaMa weights, blurred-noise image, brush-stroke mask)",
+        "config": {"workload": f"Big-LaMa generator whole-image pass {S}x{S}, batch 1 (BASELINE configs[3])",
+                   "h": S, "w": S, "mask_coverage": round(coverage, 4), "launches_per_pass": eng.launch_count(S, S)},
+        "roofline": {"bound": "mfma", "kernel": "lama_conv3x3 (FFC 3x3 implicit GEMM + conv2 segment)",
+                     "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
+                     "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5)},
+        "conv_tflops": round(conv_flops / (conv_ms * 1e9), 2),
+        "conv_frac_of_peak": round(conv_flops / (conv_ms * 1e9) / PEAK_FP32_MFMA, 4),
+        "fft_gbps": round(fft_bytes / (fft_ms * 1e6), 1) if fft_ms > 0 else None,
+        "fft_frac_of_hbm": round(fft_bytes / (fft_ms * 1e6) / PEAK_HBM, 4) if fft_ms > 0 else None,
+        "per_family": per_family,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    eng.free(d_in)
+    eng.free(d_out)
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()
