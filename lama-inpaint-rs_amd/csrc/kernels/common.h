@@ -6,6 +6,33 @@
 
 #define LAMA_NT 256  // threads per block (4 waves of 64)
 
+#ifdef __HIP_DEVICE_COMPILE__
+// Pointers read out of descriptors are generic; casting them to the global
+// address space lets the compiler emit global_load/global_store instead of
+// flat accesses (which also count against lgkmcnt and so serialise with LDS
+// waits).
+#define LAMA_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const LAMA_GLOBAL T *gp(const T *p)
+{
+    return (const LAMA_GLOBAL T *)p;
+}
+template <class T>
+__device__ __forceinline__ LAMA_GLOBAL T *gp(T *p)
+{
+    return (LAMA_GLOBAL T *)p;
+}
+
+// PyTorch 'reflect' index for |overshoot| < n (one reflection), clamped into
+// [0, n).  Exact for every input position a stored output reads (pad < n,
+// or n == 1); positions read only by out-of-range tile pixels are clamped.
+__device__ __forceinline__ int reflect1(int i, int n)
+{
+    i = i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i);
+    return min(max(i, 0), n - 1);
+}
+#endif
+
 // One K segment of an implicit-GEMM convolution.  `src` is planar
 // [C][IH][IW]; `wt` points at row 0 of the packed weights
 // [M][nchunk][taps][KC] (KC input channels per chunk, zero-padded).

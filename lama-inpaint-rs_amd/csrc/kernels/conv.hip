@@ -26,20 +26,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
-__device__ __forceinline__ int reflect_idx(int i, int n)
-{
-    // PyTorch 'reflect' (edge sample not repeated), periodic with 2n-2 so
-    // that indices of tile pixels far outside the plane stay in bounds.
-    if (n == 1) return 0;
-    if (i < 0) i = -i;
-    if (i >= n) {
-        int period = 2 * n - 2;
-        i %= period;
-        if (i >= n) i = period - i;
-    }
-    return i;
-}
-
 template <int KH_, int KW_, int S_, bool REFLECT_, int KC_, int TR_, int TC_>
 struct Cfg {
     static constexpr int KH = KH_, KW = KW_, S = S_, KC = KC_, TR = TR_, TC = TC_;
@@ -84,7 +70,7 @@ __device__ __forceinline__ void load_chunk(Stage<C> &st, const ConvSeg &sg, int 
             const int row = idx / (C::WK / 4), c4 = idx % (C::WK / 4);
             const int co = m0 + row;
             if (co < M)
-                v = *reinterpret_cast<const float4 *>(sg.wt + (long)co * sg.wrow + (long)ck * C::WK + c4 * 4);
+                v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(sg.wt) + (long)co * sg.wrow + (long)ck * C::WK + c4 * 4);
         }
         st.w[it] = v;
     }
@@ -101,9 +87,9 @@ __device__ __forceinline__ void load_chunk(Stage<C> &st, const ConvSeg &sg, int 
             const int iy = oy0 * C::S - C::PAD + r, ix = ox0 * C::S - C::PAD + c;
             if (ci < sg.C) {
                 if (C::REFLECT) {
-                    v = sg.src[(long)ci * plane + (long)reflect_idx(iy, sg.IH) * sg.IW + reflect_idx(ix, sg.IW)];
+                    v = gp(sg.src)[(long)ci * plane + (long)reflect1(iy, sg.IH) * sg.IW + reflect1(ix, sg.IW)];
                 } else if (iy >= 0 && ix >= 0 && iy < sg.IH && ix < sg.IW) {
-                    v = sg.src[(long)ci * plane + (long)iy * sg.IW + ix];
+                    v = gp(sg.src)[(long)ci * plane + (long)iy * sg.IW + ix];
                 }
             }
         }
@@ -205,12 +191,12 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const ConvProblem &P
         const int co = m0 + wm * 32 + i;
         if (co < P.M) {
             float v = acc[r];
-            if (P.bias) v += P.bias[co];
-            if (P.scale) v = v * P.scale[co] + P.shift[co];
+            if (P.bias) v += gp(P.bias)[co];
+            if (P.scale) v = v * gp(P.scale)[co] + gp(P.shift)[co];
             if (P.relu) v = fmaxf(v, 0.f);
             const long o = (long)co * P.out_cstride + pix;
-            if (P.res) v += P.res[o];
-            P.out[o] = v;
+            if (P.res) v += gp(P.res)[o];
+            gp(P.out)[o] = v;
         }
     }
 }

@@ -123,7 +123,7 @@ __device__ __forceinline__ void split_idx(const Pass &P, int m, int idx, int &b,
 }
 
 template <int R>
-__device__ void pass_fixed(const Pass &P)
+__device__ __forceinline__ void pass_fixed(const Pass &P)
 {
     const int m = P.n / R, twstep = P.n / (P.Ns * R), total = P.count * m;
     for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
@@ -147,7 +147,7 @@ __device__ void pass_fixed(const Pass &P)
 }
 
 // Any other radix: a direct DFT per butterfly.
-__device__ void pass_generic(const Pass &P, int R)
+__device__ __forceinline__ void pass_generic(const Pass &P, int R)
 {
     const int m = P.n / R, twstep = P.n / (P.Ns * R), total = P.count * m, unit = P.n / R;
     for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
@@ -170,9 +170,10 @@ __device__ void pass_generic(const Pass &P, int R)
 }
 
 // All passes of one length over a batch; returns the buffer with the result.
-__device__ float2 *stockham(const FftLen &L, float2 *a, float2 *b, int count, int bstride, int estride, int sign)
+__device__ __forceinline__ float2 *stockham(const FftLen &L, const float2 *tw, float2 *a, float2 *b, int count, int bstride,
+                           int estride, int sign)
 {
-    Pass P{a, b, L.n, 1, count, bstride, estride, sign, reinterpret_cast<const float2 *>(L.tw)};
+    Pass P{a, b, L.n, 1, count, bstride, estride, sign, tw};
     for (int s = 0; s < L.nstages; ++s) {
         const int R = L.radix[s];
         switch (R) {
@@ -191,6 +192,15 @@ __device__ float2 *stockham(const FftLen &L, float2 *a, float2 *b, int count, in
     return const_cast<float2 *>(P.in);
 }
 
+// Both twiddle tables into LDS (row table first), ahead of the first pass.
+__device__ __forceinline__ void load_twiddles(const FftArgs &A, float2 *twr, float2 *twc)
+{
+    const LAMA_GLOBAL float2 *gr = gp(reinterpret_cast<const float2 *>(A.row.tw));
+    const LAMA_GLOBAL float2 *gc = gp(reinterpret_cast<const float2 *>(A.col.tw));
+    for (int i = threadIdx.x; i < A.W; i += blockDim.x) twr[i] = gr[i];
+    for (int i = threadIdx.x; i < A.H; i += blockDim.x) twc[i] = gc[i];
+}
+
 }  // namespace
 
 // One block per channel: real [C][H][W] -> stacked [2C][H][W/2+1], ortho.
@@ -200,8 +210,9 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
     const int NB = max(HP * W, H * Wh);
-    float2 *b0 = sm, *b1 = sm + NB;
-    const float *src = A.in + (long)c * H * W;
+    float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
+    load_twiddles(A, twr, twc);
+    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
     for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
         const int p = idx / W, x = idx - p * W;
         const float a = src[(2 * p) * W + x];
@@ -209,7 +220,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *
         b0[idx] = make_float2(a, b);
     }
     __syncthreads();
-    float2 *r = stockham(A.row, b0, b1, HP, W, 1, A.row.sign_fwd);
+    float2 *r = stockham(A.row, twr, b0, b1, HP, W, 1, A.row.sign_fwd);
     float2 *o = r == b0 ? b1 : b0;
     // split each row pair into the two half spectra
     for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) {
@@ -219,8 +230,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *
                          : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
     }
     __syncthreads();
-    float2 *q = stockham(A.col, o, r, Wh, 1, Wh, A.col.sign_fwd);
-    float *dre = A.out + (long)(2 * c) * H * Wh, *dim = dre + (long)H * Wh;
+    float2 *q = stockham(A.col, twc, o, r, Wh, 1, Wh, A.col.sign_fwd);
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh, *dim = dre + (long)H * Wh;
     for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) {
         const float2 v = q[idx];
         dre[idx] = v.x * A.scale;
@@ -236,11 +247,12 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_irfft2(const FftArgs 
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
     const int NB = max(HP * W, H * Wh);
-    float2 *b0 = sm, *b1 = sm + NB;
-    const float *sre = A.in + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
+    float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
+    load_twiddles(A, twr, twc);
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
     for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) b0[idx] = make_float2(sre[idx], sim[idx]);
     __syncthreads();
-    float2 *r = stockham(A.col, b0, b1, Wh, 1, Wh, -A.col.sign_fwd);
+    float2 *r = stockham(A.col, twc, b0, b1, Wh, 1, Wh, -A.col.sign_fwd);
     float2 *o = r == b0 ? b1 : b0;
     // Hermitian rows, two per complex transform: z = Ga + i Gb
     for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
@@ -264,9 +276,9 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_irfft2(const FftArgs 
         o[idx] = make_float2(g[0].x - g[1].y, g[0].y + g[1].x);
     }
     __syncthreads();
-    float2 *q = stockham(A.row, o, r, HP, W, 1, -A.row.sign_fwd);
-    const float *f = A.feat + (long)c * H * W;
-    float *d = A.out + (long)c * H * W;
+    float2 *q = stockham(A.row, twr, o, r, HP, W, 1, -A.row.sign_fwd);
+    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    LAMA_GLOBAL float *d = gp(A.out) + (long)c * H * W;
     for (int idx = threadIdx.x; idx < H * W; idx += blockDim.x) {
         const int y = idx / W, x = idx - y * W;
         const float2 v = q[(y >> 1) * W + x];

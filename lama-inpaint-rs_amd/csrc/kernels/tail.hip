@@ -14,17 +14,6 @@ namespace {
 constexpr int TROWS = 8, TCOLS = 64, PX = 2;
 constexpr int PR = TROWS + 6, PC = TCOLS + 6;
 
-__device__ __forceinline__ int reflect_t(int i, int n)
-{
-    if (n == 1) return 0;
-    if (i < 0) i = -i;
-    if (i >= n) {
-        int period = 2 * n - 2;
-        i %= period;
-        if (i >= n) i = period - i;
-    }
-    return i;
-}
 }  // namespace
 
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
@@ -46,7 +35,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
         const float *src = A.src + (long)ci * plane;
         for (int idx = threadIdx.x; idx < PR * PC; idx += LAMA_NT) {
             const int r = idx / PC, c = idx - r * PC;
-            dst[idx] = src[(long)reflect_t(oy0 - 3 + r, H) * W + reflect_t(ox0 - 3 + c, W)];
+            dst[idx] = gp(src)[(long)reflect1(oy0 - 3 + r, H) * W + reflect1(ox0 - 3 + c, W)];
         }
     };
     stage(0, patch[0]);
@@ -65,7 +54,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
             for (int kx = 0; kx < 7; ++kx) {
 #pragma unroll
                 for (int co = 0; co < 3; ++co) {
-                    const float wv = w0[co * wstride + ky * 7 + kx];
+                    const float wv = gp(w0)[co * wstride + ky * 7 + kx];
 #pragma unroll
                     for (int p = 0; p < PX; ++p) acc[co][p] += wv * row[p + kx];
                 }
@@ -80,8 +69,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
         for (int p = 0; p < PX; ++p) {
             const int ox = ox0 + tc + p;
             if (ox < W) {
-                const float v = acc[co][p] + A.bias[co];
-                A.out[co * plane + (long)oy * W + ox] = 1.0f / (1.0f + expf(-v));
+                const float v = acc[co][p] + gp(A.bias)[co];
+                gp(A.out)[co * plane + (long)oy * W + ox] = 1.0f / (1.0f + expf(-v));
             }
         }
 }

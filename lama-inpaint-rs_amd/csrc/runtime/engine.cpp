@@ -385,7 +385,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
     std::vector<float> twr, twc;
     if (!fft_len(W8, frow, twr, err) || !fft_len(H8, fcol, twc, err)) return false;
     const int HP = (H8 + 1) / 2;
-    const size_t fft_lds = 2 * std::max((size_t)HP * W8, PS) * 8;
+    const size_t fft_lds = (2 * std::max((size_t)HP * W8, PS) + H8 + W8) * 8;
     if (fft_lds > 160 * 1024) {
         err = "bottleneck plane " + std::to_string(W8) + "x" + std::to_string(H8) +
               " exceeds the LDS-resident FFT (input up to about 1024x1024)";
@@ -911,7 +911,7 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
     std::vector<float> twr, twc;
     if (!fft_len(w, fr, twr, err) || !fft_len(h, fc, twc, err)) return false;
     const int Wh = w / 2 + 1, HP = (h + 1) / 2;
-    const size_t lds = 2 * std::max((size_t)HP * w, (size_t)h * Wh) * 8;
+    const size_t lds = (2 * std::max((size_t)HP * w, (size_t)h * Wh) + h + w) * 8;
     if (lds > 160 * 1024) {
         err = "plane too large for the LDS-resident FFT";
         return false;
