@@ -48,12 +48,13 @@ struct ConvSeg {
 // One output problem: out[co][oy'][ox'] for co < M, (oy, ox) on the OH x OW
 // GEMM grid, stored at oy' = oy*oy_mul + oy_off, ox' = ox*ox_mul + ox_off
 // (the conv-transpose phases interleave four grids into one plane).
-// Epilogue: v = acc (+bias) -> *scale + shift -> ReLU -> (+res) -> store.
+// Epilogue: v = acc (+bias) (+addend) -> *scale + shift -> ReLU -> (+res)
+// -> store; `addend` and `res` are indexed like `out`.
 struct ConvProblem {
     ConvSeg s0, s1;  // s1.nchunk == 0 when absent; s1 is always 1x1
     int M, OH, OW;
     int tiles_x, tiles_y, mblocks, nblocks;
-    const float *bias, *scale, *shift;
+    const float *bias, *addend, *scale, *shift;
     int relu;
     const float *res;
     float *out;

@@ -8,15 +8,18 @@
 // K is walked in chunks of KC input channels.  Per chunk the block stages, in
 // LDS: the packed weights [64 co][taps][KC] (rows padded to a stride = 4 mod
 // 8 floats, so the 16-byte reads of 16 lanes fall on distinct banks) and the
-// input patch [KC][PR][PC] that covers the tile's receptive field, gathered
-// with PyTorch 'reflect' index mapping (or zero fill for the transposed
+// input patch that covers the tile's receptive field, pixel-major
+// [PR][PC][KC+4] (again 16-byte reads on distinct banks), gathered with
+// PyTorch 'reflect' index mapping (or zero fill for the transposed
 // convolution phases).  im2col is never materialised.  The next chunk's
-// global loads are issued into registers before the MFMAs of the current one.
+// global loads are issued into registers before the MFMAs of the current one
+// and land in the second of two LDS stages (one barrier per chunk).
 //
 // MFMA operand mapping (32x32x2, one block): lane l supplies A[l%32][l/32] and
 // B[l/32][l%32]; the two K slots of every MFMA are given to the two lane
 // halves as channels ci = g*KC/2 + c (g = lane/32) of the same tap, so each
-// lane reads its KC/2 weights for a tap with one vector LDS read.  D[i][j]
+// lane reads its KC/2 weights and its KC/2 inputs for a tap with one vector
+// LDS read each.  D[i][j]
 // lands in lane j + 32*((i/4)%2), register (i/8)*4 + i%4.
 #include <hip/hip_runtime.h>
 
@@ -36,89 +39,116 @@ struct Cfg {
     static constexpr int PC = (TC - 1) * S + KW;
     static constexpr int WK = T * KC;
     static constexpr int WSTR = WK + ((12 - WK % 8) % 8);  // = 4 (mod 8)
-    static constexpr int W_LDS = 64 * WSTR;
-    static constexpr int P_LDS = KC * PR * PC;
+    static constexpr int KCP = KC + 4;                       // patch pixel stride
     static constexpr int W4 = 64 * WK / 4;
     static constexpr int WITER = (W4 + LAMA_NT - 1) / LAMA_NT;
-    static constexpr int PITER = (P_LDS + LAMA_NT - 1) / LAMA_NT;
+    static constexpr int P_ELEM = KC * PR * PC;
+    static constexpr int PITER = (P_ELEM + LAMA_NT - 1) / LAMA_NT;
+    // staging is branch-free: slots past the data land in a dummy tail
+    static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT - W4) * 4;
+    static constexpr int P_LDS = PR * PC * KCP + (PITER * LAMA_NT - P_ELEM);
     static constexpr int LDS = W_LDS + P_LDS;
     static_assert(TR * TC == 64, "pixel tile must hold 64 pixels");
-    static_assert(WK % 4 == 0, "weight chunk must be float4 aligned");
-    static_assert(KC % 4 == 0 || KC == 4, "KC must be a multiple of 4");
+    static_assert(KC % 4 == 0, "KC must be a multiple of 4");
 };
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-// Registers holding one chunk on its way from global memory to LDS.
+// Per-thread staging addresses, fixed for a block: each chunk only adds its
+// channel / K offset.  Staging is branch-free (a divergent branch around a
+// load makes the compiler wait for every outstanding load, which would
+// serialise the prefetch): rows past M and channels past C read clamped, valid
+// addresses (their weights are zero or their outputs are dropped), positions
+// outside the plane of a transposed-convolution phase are zeroed by a select,
+// and slots past the tile are written to a dummy LDS tail.
 template <class C>
-struct Stage {
-    float4 w[C::WITER];
-    float p[C::PITER];
+struct Slots {
+    int wg[C::WITER];  // weights: float offset of the float4 within the rows
+    int wl[C::WITER];  // weights: LDS float offset
+    int pg[C::PITER];  // patch: spatial offset in the input plane (clamped)
+    int pl[C::PITER];  // patch: LDS float offset
+    int pc[C::PITER];  // patch: channel within the chunk; < 0 marks a zero slot
 };
 
-// Issue the global loads of chunk `ck` of segment `sg`.
 template <class C>
-__device__ __forceinline__ void load_chunk(Stage<C> &st, const ConvSeg &sg, int ck, int m0, int M,
-                                           int oy0, int ox0)
+__device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int m0, int M, int oy0, int ox0)
 {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int it = 0; it < C::WITER; ++it) {
         const int idx = tid + it * LAMA_NT;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (idx < C::W4) {
-            const int row = idx / (C::WK / 4), c4 = idx % (C::WK / 4);
-            const int co = m0 + row;
-            if (co < M)
-                v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(sg.wt) + (long)co * sg.wrow + (long)ck * C::WK + c4 * 4);
-        }
-        st.w[it] = v;
+        const int row = idx / (C::WK / 4), c4 = idx % (C::WK / 4);
+        const bool in = idx < C::W4;
+        sl.wl[it] = in ? row * C::WSTR + c4 * 4 : 64 * C::WSTR + (idx - C::W4) * 4;
+        sl.wg[it] = in ? min(m0 + row, M - 1) * sg.wrow + c4 * 4 : 0;
     }
-    const long plane = (long)sg.IH * sg.IW;
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) {
         const int idx = tid + it * LAMA_NT;
-        float v = 0.f;
-        if (idx < C::P_LDS) {
-            const int cl = idx / (C::PR * C::PC);
-            const int rem = idx - cl * (C::PR * C::PC);
-            const int r = rem / C::PC, c = rem - r * C::PC;
-            const int ci = ck * C::KC + cl;
-            const int iy = oy0 * C::S - C::PAD + r, ix = ox0 * C::S - C::PAD + c;
-            if (ci < sg.C) {
-                if (C::REFLECT) {
-                    v = gp(sg.src)[(long)ci * plane + (long)reflect1(iy, sg.IH) * sg.IW + reflect1(ix, sg.IW)];
-                } else if (iy >= 0 && ix >= 0 && iy < sg.IH && ix < sg.IW) {
-                    v = gp(sg.src)[(long)ci * plane + (long)iy * sg.IW + ix];
-                }
-            }
+        const int cl = idx / (C::PR * C::PC);
+        const int rem = idx - cl * (C::PR * C::PC);
+        const int r = rem / C::PC, c = rem - r * C::PC;
+        const int iy = oy0 * C::S - C::PAD + r, ix = ox0 * C::S - C::PAD + c;
+        const bool in = idx < C::P_ELEM;
+        bool zero = false;
+        int g;
+        if (C::REFLECT) {
+            g = reflect1(iy, sg.IH) * sg.IW + reflect1(ix, sg.IW);
+        } else {
+            zero = !(iy >= 0 && ix >= 0 && iy < sg.IH && ix < sg.IW);
+            g = zero ? 0 : iy * sg.IW + ix;
         }
-        st.p[it] = v;
+        sl.pl[it] = in ? (r * C::PC + c) * C::KCP + cl : C::PR * C::PC * C::KCP + (idx - C::P_ELEM);
+        sl.pg[it] = g;
+        sl.pc[it] = (in && !zero) ? cl : -1;
+    }
+}
+
+// Registers holding one chunk on its way from global memory to LDS.
+template <class C>
+struct Stage {
+    float w[4 * C::WITER];
+    float p[C::PITER];
+};
+
+// Issue the global loads of chunk `ck`.
+template <class C>
+__device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, const ConvSeg &sg, int ck)
+{
+    const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::WK;
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it) {
+        const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(wt + sl.wg[it]);
+        st.w[4 * it] = v.x;
+        st.w[4 * it + 1] = v.y;
+        st.w[4 * it + 2] = v.z;
+        st.w[4 * it + 3] = v.w;
+    }
+    const long plane = (long)sg.IH * sg.IW;
+    const int c0 = ck * C::KC, clast = sg.C - 1 - c0;  // last valid channel within the chunk
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
+#pragma unroll
+    for (int it = 0; it < C::PITER; ++it) {
+        const float v = src[(long)min(max(sl.pc[it], 0), clast) * plane + sl.pg[it]];
+        st.p[it] = sl.pc[it] >= 0 ? v : 0.f;
     }
 }
 
 template <class C>
-__device__ __forceinline__ void store_chunk(const Stage<C> &st, float *wl, float *pl)
+__device__ __forceinline__ void store_chunk(const Stage<C> &st, const Slots<C> &sl, float *wl, float *pl)
 {
-    const int tid = threadIdx.x;
 #pragma unroll
-    for (int it = 0; it < C::WITER; ++it) {
-        const int idx = tid + it * LAMA_NT;
-        if (idx < C::W4) {
-            const int row = idx / (C::WK / 4), c4 = idx % (C::WK / 4);
-            *reinterpret_cast<float4 *>(wl + row * C::WSTR + c4 * 4) = st.w[it];
-        }
-    }
+    for (int it = 0; it < C::WITER; ++it)
+        *reinterpret_cast<float4 *>(wl + sl.wl[it]) =
+            make_float4(st.w[4 * it], st.w[4 * it + 1], st.w[4 * it + 2], st.w[4 * it + 3]);
 #pragma unroll
-    for (int it = 0; it < C::PITER; ++it) {
-        const int idx = tid + it * LAMA_NT;
-        if (idx < C::P_LDS) pl[idx] = st.p[it];
-    }
+    for (int it = 0; it < C::PITER; ++it) pl[sl.pl[it]] = st.p[it];
 }
 
 template <int N>
 __device__ __forceinline__ void lds_vec(float (&a)[N], const float *p)
 {
+    static_assert(N % 2 == 0, "vector of 2 or 4k floats");
     if constexpr (N % 4 == 0) {
 #pragma unroll
         for (int q = 0; q < N / 4; ++q) {
@@ -128,16 +158,16 @@ __device__ __forceinline__ void lds_vec(float (&a)[N], const float *p)
             a[4 * q + 2] = v.z;
             a[4 * q + 3] = v.w;
         }
-    } else if constexpr (N == 2) {
+    } else {
         float2 v = *reinterpret_cast<const float2 *>(p);
         a[0] = v.x;
         a[1] = v.y;
-    } else {
-#pragma unroll
-        for (int q = 0; q < N; ++q) a[q] = p[q];
     }
 }
 
+// MFMAs of one chunk.  Both operands of a tap are KC/2 consecutive floats per
+// lane (weights [co][tap][ci], patch [pixel][ci]); the reads of tap t+1 are
+// issued before the MFMAs of tap t.
 template <class C>
 __device__ __forceinline__ void compute_chunk(f32x16 &acc, const float *wl, const float *pl)
 {
@@ -146,33 +176,69 @@ __device__ __forceinline__ void compute_chunk(f32x16 &acc, const float *wl, cons
     const int p = wn * 32 + j;
     const int pr = p / C::TC, pc = p % C::TC;
     const float *wrow = wl + (wm * 32 + j) * C::WSTR + g * (C::KC / 2);
-    const float *prow = pl + g * (C::KC / 2) * C::PR * C::PC + pr * C::S * C::PC + pc * C::S;
+    const float *prow = pl + ((pr * C::S) * C::PC + pc * C::S) * C::KCP + g * (C::KC / 2);
+    constexpr int H = C::KC / 2;
+    float a[2][H], b[2][H];
+    lds_vec<H>(a[0], wrow);
+    lds_vec<H>(b[0], prow);
 #pragma unroll
     for (int t = 0; t < C::T; ++t) {
-        const int ky = t / C::KW, kx = t % C::KW;
-        float a[C::KC / 2];
-        lds_vec<C::KC / 2>(a, wrow + t * C::KC);
-#pragma unroll
-        for (int c = 0; c < C::KC / 2; ++c) {
-            const float bv = prow[c * C::PR * C::PC + ky * C::PC + kx];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c], bv, acc, 0, 0, 0);
+        const int cur = t & 1;
+        if (t + 1 < C::T) {
+            const int ky = (t + 1) / C::KW, kx = (t + 1) % C::KW;
+            lds_vec<H>(a[cur ^ 1], wrow + (t + 1) * C::KC);
+            lds_vec<H>(b[cur ^ 1], prow + (ky * C::PC + kx) * C::KCP);
         }
+#pragma unroll
+        for (int c = 0; c < H; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][c], b[cur][c], acc, 0, 0, 0);
     }
 }
 
-template <class C>
+// K loop of one segment.  NBUF = 2: two LDS stages and two register stages,
+// one barrier per chunk.  Chunk k's global loads are issued two chunks ahead
+// (during chunk k-2's MFMAs), written to LDS after chunk k-1's MFMAs and
+// consumed at step k, so each load has two chunks of MFMA time to land.
+// NBUF = 1 (single-chunk segments such as the 4-channel head) stages once.
+template <class C, int NBUF>
 __device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg, int m0, int M, int oy0, int ox0,
                                             float *lds)
 {
-    float *wl = lds, *pl = lds + C::W_LDS;
-    Stage<C> st;
-    load_chunk<C>(st, sg, 0, m0, M, oy0, ox0);
-    for (int ck = 0; ck < sg.nchunk; ++ck) {
+    const int n = sg.nchunk;
+    if (n <= 0) return;
+    Slots<C> sl;
+    make_slots<C>(sl, sg, m0, M, oy0, ox0);
+    if constexpr (NBUF == 1) {
+        Stage<C> st;
+        for (int ck = 0; ck < n; ++ck) {
+            load_chunk<C>(st, sl, sg, ck);
+            __syncthreads();
+            store_chunk<C>(st, sl, lds, lds + C::W_LDS);
+            __syncthreads();
+            compute_chunk<C>(acc, lds, lds + C::W_LDS);
+        }
+    } else {
+        // prefetches past the last chunk re-read it (uniform control flow)
+        float *l0 = lds, *l1 = lds + C::LDS;
+        const int last = n - 1;
+        Stage<C> r0, r1;
+        load_chunk<C>(r0, sl, sg, 0);
+        load_chunk<C>(r1, sl, sg, min(1, last));
+        store_chunk<C>(r0, sl, l0, l0 + C::W_LDS);
+        load_chunk<C>(r0, sl, sg, min(2, last));
         __syncthreads();
-        store_chunk<C>(st, wl, pl);
-        __syncthreads();
-        if (ck + 1 < sg.nchunk) load_chunk<C>(st, sg, ck + 1, m0, M, oy0, ox0);
-        compute_chunk<C>(acc, wl, pl);
+        for (int ck = 0; ck < n; ck += 2) {
+            // even step: compute stage 0, stage chunk ck+1 (r1), refill r1 with ck+3
+            compute_chunk<C>(acc, l0, l0 + C::W_LDS);
+            store_chunk<C>(r1, sl, l1, l1 + C::W_LDS);
+            load_chunk<C>(r1, sl, sg, min(ck + 3, last));
+            __syncthreads();
+            if (ck + 1 >= n) break;
+            // odd step: compute stage 1, stage chunk ck+2 (r0), refill r0 with ck+4
+            compute_chunk<C>(acc, l1, l1 + C::W_LDS);
+            store_chunk<C>(r0, sl, l0, l0 + C::W_LDS);
+            load_chunk<C>(r0, sl, sg, min(ck + 4, last));
+            __syncthreads();
+        }
     }
 }
 
@@ -191,19 +257,20 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const ConvProblem &P
         const int co = m0 + wm * 32 + i;
         if (co < P.M) {
             float v = acc[r];
+            const long o = (long)co * P.out_cstride + pix;
             if (P.bias) v += gp(P.bias)[co];
+            if (P.addend) v += gp(P.addend)[o];
             if (P.scale) v = v * gp(P.scale)[co] + gp(P.shift)[co];
             if (P.relu) v = fmaxf(v, 0.f);
-            const long o = (long)co * P.out_cstride + pix;
             if (P.res) v += gp(P.res)[o];
             gp(P.out)[o] = v;
         }
     }
 }
 
-// One 64 x 64 output tile of problem P: segment 0 with the template geometry,
-// then (SEG1) the optional 1x1 segment over a second source.
-template <class C0, bool SEG1>
+// One 64 x 64 output tile of problem P: segment 0 with the template
+// geometry, then (SEG1) the optional 1x1 segment over a second source.
+template <class C0, bool SEG1, int NBUF = 2>
 __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *lds)
 {
     const int mb = b % P.mblocks, t = b / P.mblocks;
@@ -212,10 +279,10 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    run_segment<C0>(acc, P.s0, m0, P.M, oy0, ox0, lds);
+    run_segment<C0, NBUF>(acc, P.s0, m0, P.M, oy0, ox0, lds);
     if constexpr (SEG1) {
         using C1 = Cfg<1, 1, 1, false, C0::KC, C0::TR, C0::TC>;
-        if (P.s1.nchunk > 0) run_segment<C1>(acc, P.s1, m0, P.M, oy0, ox0, lds);
+        if (P.s1.nchunk > 0) run_segment<C1, NBUF>(acc, P.s1, m0, P.M, oy0, ox0, lds);
     }
     epilogue<C0::TR, C0::TC>(acc, P, m0, oy0, ox0);
 }
@@ -249,13 +316,13 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvPro
     __shared__ __attribute__((aligned(16))) float lds[CfgHead::LDS];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
-    conv_tile<CfgHead, false>(probs[pi], b, lds);
+    conv_tile<CfgHead, false, 1>(probs[pi], b, lds);
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvProblem *__restrict__ probs, int nprob)
 {
-    __shared__ __attribute__((aligned(16))) float lds[CfgDown::LDS];
+    __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
     conv_tile<CfgDown, false>(probs[pi], b, lds);
@@ -265,7 +332,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvP
 // second K segment (the SpectralTransform's conv2, summed before BN_g).
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvProblem *__restrict__ probs, int nprob)
 {
-    __shared__ __attribute__((aligned(16))) float lds[cmax(CfgFfc::LDS, CfgFfc1::LDS)];
+    __shared__ __attribute__((aligned(16))) float lds[2 * cmax(CfgFfc::LDS, CfgFfc1::LDS)];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
     conv_tile<CfgFfc, true>(probs[pi], b, lds);
@@ -274,7 +341,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit conv).
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvProblem *__restrict__ probs, int nprob)
 {
-    __shared__ __attribute__((aligned(16))) float lds[Cfg1x1::LDS];
+    __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
     conv_tile<Cfg1x1, false>(probs[pi], b, lds);
@@ -285,7 +352,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvPro
 // (1+py) x (1+px) convolution with zero fill at the bottom/right edge.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(const ConvProblem *__restrict__ probs, int nprob)
 {
-    __shared__ __attribute__((aligned(16))) float lds[cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
+    __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
     switch (pi) {

@@ -170,6 +170,9 @@ Engine::~Engine()
         hip_->hipEventDestroy(p.b);
     }
     for (auto e : event_pool_) hip_->hipEventDestroy(e);
+    for (auto e : ev_)
+        if (e) hip_->hipEventDestroy(e);
+    if (side_) hip_->hipStreamDestroy(side_);
     if (stream_) hip_->hipStreamDestroy(stream_);
     if (module_) hip_->hipModuleUnload(module_);
 }
@@ -212,7 +215,12 @@ bool Engine::open(std::string &err)
     if (!check(hip_->hipModuleLoadData(&module_, lama_hsaco_start), "hipModuleLoadData", err)) return false;
     for (int f = 0; f < F_COUNT; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
-    return check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err);
+    if (!check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err) ||
+        !check(hip_->hipStreamCreate(&side_), "hipStreamCreate", err))
+        return false;
+    for (auto &e : ev_)
+        if (!check(hip_->hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate", err)) return false;
+    return true;
 }
 
 bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_info *t, size_t n, std::string &err)
@@ -260,7 +268,7 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
                 return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
             });
             F.l2g = pack(A, 384, 128, 9, 8, [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; });
-            F.conv2 = pack(A, 384, 192, 1, 8, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
+            F.conv2 = pack(A, 384, 192, 1, 32, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
             F.conv1 = pack(A, 192, 384, 1, 32, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
             F.fu = pack(A, 384, 384, 1, 32, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
             if (!fold_bns(A, S, {{pf + ".convg2g.conv1.1", 192}}, F.bn1, err) ||
@@ -402,16 +410,18 @@ bool Engine::build_plan(Plan &p, std::string &err)
     const size_t o_in = take(4 * P * 4), o_a1 = take(64 * P * 4), o_a2 = take(128 * P2 * 4), o_a3 = take(256 * P4 * 4);
     const size_t o_x = take(512 * P8 * 4), o_y = take(512 * P8 * 4), o_f = take(192 * P8 * 4), o_g = take(192 * P8 * 4);
     const size_t o_s = take(384 * PS * 4), o_s2 = take(384 * PS * 4), o_out = take(3 * P * 4);
+    const size_t o_gc = take(384 * P8 * 4);
+
     const size_t o_twr = take(twr.size() * 4), o_twc = take(twc.size() * 4);
-    const size_t n_conv = 4 + 36 * 4 + 4 * 3;
-    const size_t n_puts = 4 + 36 * 3 + 3 + 3;  // descriptor uploads, each 256-byte aligned
+    const size_t n_conv = 4 + 36 * 4 + 4 * 3;  // problems
+    const size_t n_puts = 4 + 36 * 4 + 3 + 3;  // descriptor uploads, each 256-byte aligned
     const size_t o_desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
     p.arena_bytes = off;
     if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
     char *base = (char *)p.arena;
     auto F = [&](size_t o) { return (float *)(base + o); };
     float *in = F(o_in), *a1 = F(o_a1), *a2 = F(o_a2), *a3 = F(o_a3), *X = F(o_x), *Y = F(o_y), *Fb = F(o_f),
-          *G = F(o_g), *Sb = F(o_s), *S2 = F(o_s2), *out = F(o_out);
+          *G = F(o_g), *Sb = F(o_s), *S2 = F(o_s2), *out = F(o_out), *GC = F(o_gc);
     p.in = in;
     p.out = out;
     frow.tw = F(o_twr);
@@ -459,12 +469,21 @@ bool Engine::build_plan(Plan &p, std::string &err)
         q.oy_mul = q.ox_mul = 1;
         return q;
     };
-    auto conv_launch = [&](int family, std::vector<ConvProblem> probs, int step, double flops, double bytes) {
+    bool bad_problem = false;
+    auto conv_launch = [&](int family, std::vector<ConvProblem> probs, int step, double flops, double bytes,
+                           int stream = S_MAIN, int wait_ev = -1, int record_ev = -1) {
         Launch L{};
         L.fn = fn_[family];
         L.family = family;
+        L.stream = stream;
+        L.wait_ev = wait_ev;
+        L.record_ev = record_ev;
         unsigned nb = 0;
-        for (auto &q : probs) nb += (unsigned)q.nblocks;
+        for (auto &q : probs) {
+            nb += (unsigned)q.nblocks;
+            if (q.nblocks != q.tiles_x * q.tiles_y * q.mblocks)
+                bad_problem = true;
+        }
         L.grid = nb;
         L.shmem = 0;
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
@@ -486,7 +505,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
     conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a2, down_[1], 128, H2, W2), 256, H4, W4, down_bn_[1], 256, a3, P4, W4, nullptr)},
                 3, 2.0 * 128 * 256 * 9 * P4, f4 * (128 * P2 + 256 * P4 + 256 * 128 * 9));
     conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a3, down_[2], 256, H4, W4), 512, H8, W8, down_bn_[2], 512, X, P8, W8, nullptr)},
-                4, 2.0 * 256 * 512 * 9 * P8, f4 * (256 * P4 + 512 * P8 + 512 * 256 * 9));
+                4, 2.0 * 256 * 512 * 9 * P8, f4 * (256 * P4 + 512 * P8 + 512 * 256 * 9), S_MAIN, -1, EV_FORK);
 
     // FFT descriptors (the same buffers serve all 36 spectral transforms)
     FftArgs fa{};
@@ -506,19 +525,42 @@ bool Engine::build_plan(Plan &p, std::string &err)
     void *d_irfft = put(&fa, sizeof fa);
     const double fft_bytes = f4 * 192 * P8 + 8.0 * 192 * PS;  // real plane + half spectrum (re, im)
 
-    // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual)
+    // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual).
+    // Main stream: one grouped launch of the local GEMM, BN_l(l2l(x_l) +
+    // g2l(x_g)), and the raw l2g(x_l) partial.  Side stream, concurrently: the
+    // SpectralTransform chain, then conv2(f + ifft) whose epilogue adds the
+    // l2g partial before BN_g.  The next FFC's main launch waits for the side
+    // stream (its input's global half); the side stream's conv2 waits for the
+    // main launch (the partial).
     for (int r = 0; r < 18; ++r)
         for (int s = 0; s < 2; ++s) {
-            const FfcW &Fw = ffc_[r * 2 + s];
+            const int k = r * 2 + s;
+            const FfcW &Fw = ffc_[k];
             float *src = s == 0 ? X : Y, *dst = s == 0 ? Y : X;
             const float *res = s == 0 ? nullptr : X;
+            const int step = s == 1 ? 5 + r : -1;
+            ConvProblem ql = problem(F_CONV3, seg(src, Fw.local, 512, H8, W8), 128, H8, W8, Fw.bn_l, 128, dst, P8, W8, res);
+            ConvProblem qg = problem(F_CONV3, seg(src, Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, GC, P8, W8, nullptr);
+            qg.scale = qg.shift = nullptr;
+            qg.relu = 0;
+            const double fl = 2.0 * P8 * (128.0 * 512 * 9 + 384.0 * 128 * 9);
+            const double by = f4 * (512 * P8 + 128 * P8 * (res ? 2 : 1) + 384 * P8 + 128 * 512 * 9 + 384 * 128 * 9);
+            static const bool split_launch = getenv("LAMA_SPLIT_LAUNCH") != nullptr;  // profiling aid
+            if (split_launch) {
+                conv_launch(F_CONV3, {ql}, -1, 2.0 * P8 * 128.0 * 512 * 9, by, S_MAIN, k == 0 ? -1 : EV_SIDE, -1);
+                conv_launch(F_CONV3, {qg}, -1, 2.0 * P8 * 384.0 * 128 * 9, by, S_MAIN, -1, EV_MAIN);
+            } else {
+                conv_launch(F_CONV3, {ql, qg}, -1, fl, by, S_MAIN, k == 0 ? -1 : EV_SIDE, EV_MAIN);
+            }
             // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
             conv_launch(F_CONV1,
                         {problem(F_CONV1, seg(src + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1, 192, Fb, P8, (int)P8, nullptr)},
-                        -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384));
+                        -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384), S_SIDE, k == 0 ? EV_FORK : -1);
             Launch L{};
             L.fn = fn_[F_RFFT];
             L.family = F_RFFT;
+            L.stream = S_SIDE;
+            L.wait_ev = L.record_ev = -1;
             L.grid = 192;
             L.shmem = (unsigned)fft_lds;
             L.arg = d_rfft;
@@ -530,20 +572,18 @@ bool Engine::build_plan(Plan &p, std::string &err)
             // FourierUnit conv over the stacked spectrum + BN + ReLU
             conv_launch(F_CONV1,
                         {problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS, (int)PS, nullptr)},
-                        -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384));
+                        -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384), S_SIDE);
             L.fn = fn_[F_IRFFT];
             L.family = F_IRFFT;
             L.arg = d_irfft;
             L.bytes = fft_bytes + f4 * 192 * P8;  // + the fused feat read
             p.launches.push_back(L);
-            // local: BN_l(l2l(x_l) + g2l(x_g)); global: BN_g(l2g(x_l) + conv2(f + ifft))
-            ConvProblem ql = problem(F_CONV3, seg(src, Fw.local, 512, H8, W8), 128, H8, W8, Fw.bn_l, 128, dst, P8, W8, res);
-            ConvProblem qg = problem(F_CONV3, seg(src, Fw.l2g, 128, H8, W8), 384, H8, W8, Fw.bn_g, 384, dst + 128 * P8, P8,
-                                     W8, res ? res + 128 * P8 : nullptr);
-            qg.s1 = seg(G, Fw.conv2, 192, H8, W8);
-            const double fl = 2.0 * P8 * (128.0 * 512 * 9 + 384.0 * 128 * 9 + 384.0 * 192);
-            const double by = f4 * (512 * P8 + 192 * P8 + 512 * P8 * (res ? 2 : 1) + 128 * 512 * 9 + 384 * 128 * 9 + 384 * 192);
-            conv_launch(F_CONV3, {ql, qg}, s == 1 ? 5 + r : -1, fl, by);
+            // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
+            ConvProblem q2 = problem(F_CONV1, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
+                                     dst + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
+            q2.addend = GC;
+            conv_launch(F_CONV1, {q2}, step, 2.0 * 192 * 384 * P8,
+                        f4 * (192 * P8 + 384 * P8 * (res ? 3 : 2) + 384 * 192), S_SIDE, EV_MAIN, EV_SIDE);
         }
     // step 23 (concat) is the same buffer as step 22; steps 24-26 the upsamplers
     const float *usrc[3] = {X, a3, a2};
@@ -564,7 +604,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         }
         const double pin = (double)uh[u] * uw[u];
         conv_launch(F_CONVT, ph, 24 + u, 2.0 * U.cin * U.cout * 9 * pin,
-                    f4 * (U.cin * pin + U.cout * 4 * pin + U.cin * U.cout * 9));
+                    f4 * (U.cin * pin + U.cout * 4 * pin + U.cin * U.cout * 9), S_MAIN, u == 0 ? EV_SIDE : -1);
     }
     // step 28: model.34 + sigmoid (ReflectionPad2d(3) folded into the indexing)
     TailArgs ta{};
@@ -579,6 +619,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
         Launch L{};
         L.fn = fn_[F_TAIL];
         L.family = F_TAIL;
+        L.stream = S_MAIN;
+        L.wait_ev = L.record_ev = -1;
         L.grid = (unsigned)(((W + 63) / 64) * ((H + 7) / 8));
         L.arg = put(&ta, sizeof ta);
         L.nparams = 1;
@@ -586,6 +628,10 @@ bool Engine::build_plan(Plan &p, std::string &err)
         L.flops = 2.0 * 64 * 3 * 49 * P;
         L.bytes = f4 * (64 * P + 3 * P);
         p.launches.push_back(L);
+    }
+    if (bad_problem) {
+        err = "internal: inconsistent launch descriptor";
+        return false;
     }
     if (desc.size() > p.arena_bytes - o_desc) {
         err = "internal: descriptor region overflow";
@@ -604,6 +650,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
 
     if (!check(hip_->hipMemcpy(base + o_desc, desc.data(), desc.size(), hipMemcpyHostToDevice), "hipMemcpy(descriptors)", err))
         return false;
+
     if (!check(hip_->hipMemcpy((void *)frow.tw, twr.data(), twr.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err))
         return false;
     return check(hip_->hipMemcpy((void *)fcol.tw, twc.data(), twc.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err);
@@ -654,25 +701,35 @@ static void host_reflect_pad(const float *src, int c, int h, int w, int pad, flo
 
 bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
 {
+    // LAMA_STREAMS=1 puts the side-stream work on the main stream (profiling)
+    static const bool single = getenv("LAMA_STREAMS") && atoi(getenv("LAMA_STREAMS")) == 1;
+    hipStream_t st[2] = {s, single ? s : side_};
     for (const Launch &L : p.launches) {
-        if (!launch(L, s, err)) return false;
+        hipStream_t ls = st[L.stream];
+        if (L.wait_ev >= 0 && !check(hip_->hipStreamWaitEvent(ls, ev_[L.wait_ev], 0), "hipStreamWaitEvent", err))
+            return false;
+        if (!launch(L, ls, err)) return false;
+        if (L.record_ev >= 0 && !check(hip_->hipEventRecord(ev_[L.record_ev], ls), "hipEventRecord", err)) return false;
         if (!steps || L.step_end < 0) continue;
         int done[2] = {L.step_end, L.step_end == 22 ? 23 : -1};
-        for (int st : done) {
-            if (st < 0) continue;
-            const bool want = steps[st] || (st == 26 && steps[27]);
+        for (int stp : done) {
+            if (stp < 0) continue;
+            const bool want = steps[stp] || (stp == 26 && steps[27]);
             if (!want) continue;
-            auto src = p.step_src[st];
+            auto src = p.step_src[stp];
             std::vector<float> tmp;
-            float *dst = steps[st];
+            float *dst = steps[stp];
             if (!dst) {
                 tmp.resize(src.second);
                 dst = tmp.data();
             }
-            if (!check(hip_->hipMemcpyAsync(dst, src.first, src.second * 4, hipMemcpyDeviceToHost, s), "hipMemcpy(dump)", err) ||
+            // a step is complete when both streams have drained
+            if (!check(hip_->hipStreamSynchronize(st[0]), "hipStreamSynchronize", err) ||
+                !check(hip_->hipStreamSynchronize(st[1]), "hipStreamSynchronize", err) ||
+                !check(hip_->hipMemcpyAsync(dst, src.first, src.second * 4, hipMemcpyDeviceToHost, s), "hipMemcpy(dump)", err) ||
                 !check(hip_->hipStreamSynchronize(s), "hipStreamSynchronize", err))
                 return false;
-            if (st == 26 && steps[27]) host_reflect_pad(dst, 64, p.H, p.W, 3, steps[27]);
+            if (stp == 26 && steps[27]) host_reflect_pad(dst, 64, p.H, p.W, 3, steps[27]);
         }
     }
     return true;

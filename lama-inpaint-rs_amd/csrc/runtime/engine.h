@@ -26,9 +26,18 @@ struct Packed {
     int M = 0, C = 0, T = 0, KC = 0, nchunk = 0, wrow = 0;
 };
 
+// Streams of a forward: the main one (the caller's) and a side stream that
+// carries the SpectralTransform chain of every FFC concurrently with the
+// FFC's spatial GEMM.  Cross-stream order is kept with the engine's events.
+enum { S_MAIN = 0, S_SIDE = 1 };
+enum { EV_FORK = 0, EV_MAIN = 1, EV_SIDE = 2, EV_COUNT = 3 };
+
 struct Launch {
     hipFunction_t fn;
     int family;
+    int stream;     // S_MAIN or S_SIDE
+    int wait_ev;    // event the stream waits for before the launch, or -1
+    int record_ev;  // event recorded on the stream after the launch, or -1
     unsigned grid;
     unsigned shmem;
     void *arg;   // device pointer to this launch's descriptor(s)
@@ -96,7 +105,8 @@ private:
     int device_ = 0;
     hipModule_t module_ = nullptr;
     hipFunction_t fn_[F_COUNT] = {};
-    hipStream_t stream_ = nullptr;
+    hipStream_t stream_ = nullptr, side_ = nullptr;
+    hipEvent_t ev_[EV_COUNT] = {};
 
     // weights
     bool have_weights_ = false;
