@@ -88,6 +88,15 @@ struct FftArgs {
     int pad_;
 };
 
+// Sum of K-partials + BN + ReLU (+ residual) over [C][plane].
+struct FinalizeArgs {
+    const float *part[4];
+    int nparts, C;
+    long plane;
+    const float *scale, *shift, *res;
+    float *out;
+};
+
 // The 7x7 output convolution (64 -> 3, reflect pad 3, bias, sigmoid).
 struct TailArgs {
     const float *src;  // [Cin][H][W]

@@ -3,3 +3,4 @@
 #include "kernels/conv.hip"
 #include "kernels/fft.hip"
 #include "kernels/tail.hip"
+#include "kernels/eltwise.hip"

@@ -22,8 +22,8 @@
 
 namespace lama {
 
-const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3", "conv1x1",
-                                          "convt",   "rfft2",     "irfft2",  "tail"};
+const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt",
+                                          "rfft2",   "irfft2",    "tail",    "finalize"};
 
 size_t step_numel(int step, int h, int w)
 {
@@ -45,7 +45,8 @@ size_t step_numel(int step, int h, int w)
 namespace {
 
 const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lama_conv3x3", "lama_conv1x1",
-                                          "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail"};
+                                          "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail",
+                                          "lama_finalize"};
 
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 void tile_shape(int family, int &tr, int &tc)
@@ -411,17 +412,19 @@ bool Engine::build_plan(Plan &p, std::string &err)
     const size_t o_x = take(512 * P8 * 4), o_y = take(512 * P8 * 4), o_f = take(192 * P8 * 4), o_g = take(192 * P8 * 4);
     const size_t o_s = take(384 * PS * 4), o_s2 = take(384 * PS * 4), o_out = take(3 * P * 4);
     const size_t o_gc = take(384 * P8 * 4);
+    // the FFC local GEMM runs as four K quarters with raw partial outputs
+    const size_t o_lq = take(4 * 128 * P8 * 4);
 
     const size_t o_twr = take(twr.size() * 4), o_twc = take(twc.size() * 4);
-    const size_t n_conv = 4 + 36 * 4 + 4 * 3;  // problems
-    const size_t n_puts = 4 + 36 * 4 + 3 + 3;  // descriptor uploads, each 256-byte aligned
+    const size_t n_conv = 4 + 36 * 7 + 4 * 3;  // problems
+    const size_t n_puts = 4 + 36 * 5 + 3 + 3;  // descriptor uploads, each 256-byte aligned
     const size_t o_desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
     p.arena_bytes = off;
     if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
     char *base = (char *)p.arena;
     auto F = [&](size_t o) { return (float *)(base + o); };
     float *in = F(o_in), *a1 = F(o_a1), *a2 = F(o_a2), *a3 = F(o_a3), *X = F(o_x), *Y = F(o_y), *Fb = F(o_f),
-          *G = F(o_g), *Sb = F(o_s), *S2 = F(o_s2), *out = F(o_out), *GC = F(o_gc);
+          *G = F(o_g), *Sb = F(o_s), *S2 = F(o_s2), *out = F(o_out), *GC = F(o_gc), *LQ = F(o_lq);
     p.in = in;
     p.out = out;
     frow.tw = F(o_twr);
@@ -539,18 +542,45 @@ bool Engine::build_plan(Plan &p, std::string &err)
             float *src = s == 0 ? X : Y, *dst = s == 0 ? Y : X;
             const float *res = s == 0 ? nullptr : X;
             const int step = s == 1 ? 5 + r : -1;
-            ConvProblem ql = problem(F_CONV3, seg(src, Fw.local, 512, H8, W8), 128, H8, W8, Fw.bn_l, 128, dst, P8, W8, res);
+            // local: four K quarters (input channels 128q..128q+127), raw partials
+            std::vector<ConvProblem> probs;
+            for (int q = 0; q < 4; ++q) {
+                ConvSeg sq = seg(src + (size_t)128 * q * P8, Fw.local, 128, H8, W8);
+                sq.wt = wp(Fw.local.off) + (size_t)q * 16 * 72;  // chunks 16q.. of the packed rows
+                sq.nchunk = 16;
+                ConvProblem pq = problem(F_CONV3, sq, 128, H8, W8, 0, 0, LQ + (size_t)q * 128 * P8, P8, W8, nullptr);
+                pq.scale = pq.shift = nullptr;
+                pq.relu = 0;
+                probs.push_back(pq);
+            }
             ConvProblem qg = problem(F_CONV3, seg(src, Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, GC, P8, W8, nullptr);
             qg.scale = qg.shift = nullptr;
             qg.relu = 0;
+            probs.push_back(qg);
             const double fl = 2.0 * P8 * (128.0 * 512 * 9 + 384.0 * 128 * 9);
-            const double by = f4 * (512 * P8 + 128 * P8 * (res ? 2 : 1) + 384 * P8 + 128 * 512 * 9 + 384 * 128 * 9);
-            static const bool split_launch = getenv("LAMA_SPLIT_LAUNCH") != nullptr;  // profiling aid
-            if (split_launch) {
-                conv_launch(F_CONV3, {ql}, -1, 2.0 * P8 * 128.0 * 512 * 9, by, S_MAIN, k == 0 ? -1 : EV_SIDE, -1);
-                conv_launch(F_CONV3, {qg}, -1, 2.0 * P8 * 384.0 * 128 * 9, by, S_MAIN, -1, EV_MAIN);
-            } else {
-                conv_launch(F_CONV3, {ql, qg}, -1, fl, by, S_MAIN, k == 0 ? -1 : EV_SIDE, EV_MAIN);
+            const double by = f4 * (512 * P8 + 4 * 128 * P8 + 384 * P8 + 128 * 512 * 9 + 384 * 128 * 9);
+            conv_launch(F_CONV3, probs, -1, fl, by, S_MAIN, k == 0 ? -1 : EV_SIDE, EV_MAIN);
+            {
+                FinalizeArgs fa2{};
+                for (int q = 0; q < 4; ++q) fa2.part[q] = LQ + (size_t)q * 128 * P8;
+                fa2.nparts = 4;
+                fa2.C = 128;
+                fa2.plane = (long)P8;
+                fa2.scale = wp(Fw.bn_l);
+                fa2.shift = wp(Fw.bn_l + 128);
+                fa2.res = res;
+                fa2.out = dst;
+                Launch L{};
+                L.fn = fn_[F_FINAL];
+                L.family = F_FINAL;
+                L.stream = S_MAIN;
+                L.wait_ev = L.record_ev = -1;
+                L.grid = (unsigned)(((128 * P8 + 3) / 4 + LAMA_NT - 1) / LAMA_NT);
+                L.arg = put(&fa2, sizeof fa2);
+                L.nparams = 1;
+                L.step_end = -1;
+                L.bytes = f4 * 128 * P8 * (4 + 1 + (res ? 1 : 0));
+                p.launches.push_back(L);
             }
             // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
             conv_launch(F_CONV1,

@@ -12,7 +12,7 @@
 
 namespace lama {
 
-enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_COUNT };
+enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_COUNT };
 extern const char *const kFamilyName[F_COUNT];
 
 // Number of plan steps of the reference (model.rs:135-207) and the size in

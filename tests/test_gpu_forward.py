@@ -74,5 +74,6 @@ def test_forward_repeatable_and_shapes(pkg, engine):
     b = engine.forward(x)
     assert a.shape == (3, 64, 128)
     assert np.array_equal(a, b)
-    # head, 3 downsamplers, 36 FFCs x (grouped GEMM, conv1, rfft2, FU conv, irfft2, conv2), 3 upsamplers, tail
-    assert engine.launch_count(64, 128) == 1 + 3 + 36 * 6 + 3 + 1
+    # head, 3 downsamplers, 36 FFCs x (grouped GEMM, finalize, conv1, rfft2, FU conv, irfft2, conv2),
+    # 3 upsamplers, tail
+    assert engine.launch_count(64, 128) == 1 + 3 + 36 * 7 + 3 + 1
