@@ -104,7 +104,7 @@ def main():
         with open(args.traffic) as fh:
             traffic = json.load(fh).get(dom)
 
-    conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt"]
+    conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt", "conv1x1res"]
     conv_ms = sum(fam[f]["ms"] for f in conv_fams) / 3
     conv_flops = sum(fam[f]["flops"] for f in conv_fams) / 3
     fft_ms = sum(fam[f]["ms"] for f in ("rfft2", "irfft2")) / 3
@@ -149,7 +149,7 @@ def main():
         "data": "synthetic (seeded random-init Big-LaMa weights, blurred-noise image, brush-stroke mask)",
         "config": {"workload": f"Big-LaMa generator whole-image pass {S}x{S}, batch 1 (BASELINE configs[3])",
                    "h": S, "w": S, "mask_coverage": round(coverage, 4), "launches_per_pass": eng.launch_count(S, S)},
-        "roofline": {"bound": "mfma", "kernel": "lama_conv3x3 (FFC 3x3 implicit GEMM + conv2 segment)",
+        "roofline": {"bound": "mfma", "kernel": "lama_conv3x3 (FFC 3x3 implicit GEMMs: local in 4 K-quarters + l2g, one launch)",
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
                      "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5)},

@@ -4,7 +4,10 @@
 #pragma once
 #include <stdint.h>
 
-#define LAMA_NT 256  // threads per block (4 waves of 64)
+#define LAMA_NT 256      // threads per block (4 waves of 64)
+#define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
+#define LAMA_TAIL_ROWS 8 // output tile of the 7x7 tail kernel (rows x columns)
+#define LAMA_TAIL_COLS 64
 
 #ifdef __HIP_DEVICE_COMPILE__
 // Pointers read out of descriptors are generic; casting them to the global

@@ -39,7 +39,9 @@ struct Cfg {
     static constexpr int PC = (TC - 1) * S + KW;
     static constexpr int WK = T * KC;
     static constexpr int WSTR = WK + ((12 - WK % 8) % 8);  // = 4 (mod 8)
-    static constexpr int KCP = KC + 4;                       // patch pixel stride
+    // patch pixel stride: the 16-byte per-lane reads of 16 lanes land on
+    // distinct banks
+    static constexpr int KCP = KC + 4;
     static constexpr int W4 = 64 * WK / 4;
     static constexpr int WITER = (W4 + LAMA_NT - 1) / LAMA_NT;
     static constexpr int P_ELEM = KC * PR * PC;
@@ -50,6 +52,7 @@ struct Cfg {
     static constexpr int LDS = W_LDS + P_LDS;
     static_assert(TR * TC == 64, "pixel tile must hold 64 pixels");
     static_assert(KC % 4 == 0, "KC must be a multiple of 4");
+    static_assert((KC / 2) % 4 != 0 || KCP % 4 == 0, "b128 operand reads need 16-byte pixel stride");
 };
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -242,8 +245,32 @@ __device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg, int 
     }
 }
 
+// Epilogue operands read from memory (addend, residual) are fetched before
+// the K loop so their latency hides behind it.
+struct EpiPre {
+    float add[16], res[16];
+};
+
 template <int TR, int TC>
-__device__ __forceinline__ void epilogue(const f32x16 &acc, const ConvProblem &P, int m0, int oy0, int ox0)
+__device__ __forceinline__ void epilogue_prefetch(EpiPre &e, const ConvProblem &P, int m0, int oy0, int ox0)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
+    const int p = wn * 32 + j;
+    const int oy = min(oy0 + p / TC, P.OH - 1), ox = min(ox0 + p % TC, P.OW - 1);
+    const long pix = (long)(oy * P.oy_mul + P.oy_off) * P.outW + (long)ox * P.ox_mul + P.ox_off;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int co = min(m0 + wm * 32 + 8 * (r >> 2) + 4 * g + (r & 3), P.M - 1);
+        const long o = (long)co * P.out_cstride + pix;
+        e.add[r] = P.addend ? gp(P.addend)[o] : 0.f;
+        e.res[r] = P.res ? gp(P.res)[o] : 0.f;
+    }
+}
+
+template <int TR, int TC, bool PREFETCH>
+__device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, const ConvProblem &P, int m0, int oy0,
+                                         int ox0)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
@@ -259,10 +286,16 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const ConvProblem &P
             float v = acc[r];
             const long o = (long)co * P.out_cstride + pix;
             if (P.bias) v += gp(P.bias)[co];
-            if (P.addend) v += gp(P.addend)[o];
+            if (PREFETCH)
+                v += e.add[r];
+            else if (P.addend)
+                v += gp(P.addend)[o];
             if (P.scale) v = v * gp(P.scale)[co] + gp(P.shift)[co];
             if (P.relu) v = fmaxf(v, 0.f);
-            if (P.res) v += gp(P.res)[o];
+            if (PREFETCH)
+                v += e.res[r];
+            else if (P.res)
+                v += gp(P.res)[o];
             gp(P.out)[o] = v;
         }
     }
@@ -270,12 +303,19 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const ConvProblem &P
 
 // One 64 x 64 output tile of problem P: segment 0 with the template
 // geometry, then (SEG1) the optional 1x1 segment over a second source.
-template <class C0, bool SEG1, int NBUF = 2>
+template <class C0, bool SEG1, int NBUF = 2, bool PREFETCH = false>
 __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *lds)
 {
     const int mb = b % P.mblocks, t = b / P.mblocks;
     const int tx = t % P.tiles_x, ty = t / P.tiles_x;
     const int m0 = mb * 64, oy0 = ty * C0::TR, ox0 = tx * C0::TC;
+    EpiPre pre;
+    if constexpr (PREFETCH) {
+        epilogue_prefetch<C0::TR, C0::TC>(pre, P, m0, oy0, ox0);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pre.add[r] = pre.res[r] = 0.f;
+    }
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -284,7 +324,7 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
         using C1 = Cfg<1, 1, 1, false, C0::KC, C0::TR, C0::TC>;
         if (P.s1.nchunk > 0) run_segment<C1, NBUF>(acc, P.s1, m0, P.M, oy0, ox0, lds);
     }
-    epilogue<C0::TR, C0::TC>(acc, P, m0, oy0, ox0);
+    epilogue<C0::TR, C0::TC, PREFETCH>(acc, pre, P, m0, oy0, ox0);
 }
 
 __device__ __forceinline__ int find_problem(const ConvProblem *probs, int nprob, int &b)
@@ -345,6 +385,17 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvPro
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
     conv_tile<Cfg1x1, false>(probs[pi], b, lds);
+}
+
+// The same with addend / residual fetched before the K loop (the
+// SpectralTransform conv2, whose epilogue adds the l2g partial and the
+// residual).
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1_res(const ConvProblem *__restrict__ probs, int nprob)
+{
+    __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
+    int b = blockIdx.x;
+    int pi = find_problem(probs, nprob, b);
+    conv_tile<Cfg1x1, false, 2, true>(probs[pi], b, lds);
 }
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions

@@ -204,7 +204,7 @@ __device__ __forceinline__ void load_twiddles(const FftArgs &A, float2 *twr, flo
 }  // namespace
 
 // One block per channel: real [C][H][W] -> stacked [2C][H][W/2+1], ortho.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftArgs *__restrict__ args)
 {
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
@@ -213,11 +213,25 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *
     float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
     load_twiddles(A, twr, twc);
     const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
-    for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
-        const int p = idx / W, x = idx - p * W;
-        const float a = src[(2 * p) * W + x];
-        const float b = 2 * p + 1 < H ? src[(2 * p + 1) * W + x] : 0.f;
-        b0[idx] = make_float2(a, b);
+    if ((W & 3) == 0 && (H & 1) == 0) {  // row pairs as float4 quads
+        const int W4 = W >> 2;
+        for (int q = threadIdx.x; q < HP * W4; q += blockDim.x) {
+            const int p = q / W4, x = (q - p * W4) * 4;
+            const float4 a = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
+            const float4 b = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
+            float2 *d = b0 + p * W + x;
+            d[0] = make_float2(a.x, b.x);
+            d[1] = make_float2(a.y, b.y);
+            d[2] = make_float2(a.z, b.z);
+            d[3] = make_float2(a.w, b.w);
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
+            const int p = idx / W, x = idx - p * W;
+            const float a = src[(2 * p) * W + x];
+            const float b = 2 * p + 1 < H ? src[(2 * p + 1) * W + x] : 0.f;
+            b0[idx] = make_float2(a, b);
+        }
     }
     __syncthreads();
     float2 *r = stockham(A.row, twr, b0, b1, HP, W, 1, A.row.sign_fwd);
@@ -241,7 +255,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_rfft2(const FftArgs *
 
 // One block per channel: stacked [2C][H][W/2+1] -> real [C][H][W], ortho,
 // plus feat: out = feat + irfft2(in).
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_irfft2(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftArgs *__restrict__ args)
 {
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
@@ -279,9 +293,27 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_irfft2(const FftArgs 
     float2 *q = stockham(A.row, twr, o, r, HP, W, 1, -A.row.sign_fwd);
     const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
     LAMA_GLOBAL float *d = gp(A.out) + (long)c * H * W;
-    for (int idx = threadIdx.x; idx < H * W; idx += blockDim.x) {
-        const int y = idx / W, x = idx - y * W;
-        const float2 v = q[(y >> 1) * W + x];
-        d[idx] = ((y & 1) ? v.y : v.x) * A.scale + f[idx];
+    if ((W & 3) == 0) {
+        for (int i4 = threadIdx.x; i4 < (H * W) >> 2; i4 += blockDim.x) {
+            const int idx = i4 * 4, y = idx / W, x = idx - y * W;
+            const float2 *v = q + (y >> 1) * W + x;
+            const float4 fv = *reinterpret_cast<const LAMA_GLOBAL float4 *>(f + idx);
+            float4 o;
+            if (y & 1)
+                o = make_float4(v[0].y, v[1].y, v[2].y, v[3].y);
+            else
+                o = make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
+            o.x = o.x * A.scale + fv.x;
+            o.y = o.y * A.scale + fv.y;
+            o.z = o.z * A.scale + fv.z;
+            o.w = o.w * A.scale + fv.w;
+            *reinterpret_cast<LAMA_GLOBAL float4 *>(d + idx) = o;
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < H * W; idx += blockDim.x) {
+            const int y = idx / W, x = idx - y * W;
+            const float2 v = q[(y >> 1) * W + x];
+            d[idx] = ((y & 1) ? v.y : v.x) * A.scale + f[idx];
+        }
     }
 }

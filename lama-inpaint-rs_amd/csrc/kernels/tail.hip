@@ -3,15 +3,16 @@
 //
 // With only three output channels an MFMA tile would be >90% padding, so this
 // is VALU work: a block covers 8 rows x 64 columns, each thread two adjacent
-// pixels x 3 channels (6 accumulators).  Per input channel the block stages
-// the reflect-padded 14 x 70 patch in LDS; the channel's 147 weights are
-// wave-uniform and read through the scalar cache.
+// pixels x 3 channels (6 accumulators).  All 3 x Cin x 49 weights are staged
+// in LDS once (wave-uniform broadcast reads); per input channel the block
+// stages the reflect-padded 14 x 70 patch, one channel ahead.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
 
 namespace {
-constexpr int TROWS = 8, TCOLS = 64, PX = 2;
+constexpr int TROWS = LAMA_TAIL_ROWS, TCOLS = LAMA_TAIL_COLS, PX = 2;
+static_assert(TROWS * TCOLS / PX == LAMA_NT, "one thread per PX pixels of the tile");
 constexpr int PR = TROWS + 6, PC = TCOLS + 6;
 
 }  // namespace
@@ -19,6 +20,7 @@ constexpr int PR = TROWS + 6, PC = TCOLS + 6;
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
 {
     __shared__ float patch[2][PR * PC];
+    __shared__ __attribute__((aligned(16))) float wl[3 * 64 * 49];
     const TailArgs &A = *args;
     const int H = A.H, W = A.W;
     const int tiles_x = (W + TCOLS - 1) / TCOLS;
@@ -38,13 +40,15 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
             dst[idx] = gp(src)[(long)reflect1(oy0 - 3 + r, H) * W + reflect1(ox0 - 3 + c, W)];
         }
     };
+    const int nw = 3 * A.Cin * 49;  // Cin <= 64
+    for (int i = threadIdx.x; i < nw; i += LAMA_NT) wl[i] = gp(A.wt)[i];
     stage(0, patch[0]);
     for (int ci = 0; ci < A.Cin; ++ci) {
         __syncthreads();
         if (ci + 1 < A.Cin) stage(ci + 1, patch[(ci + 1) & 1]);
         const float *pp = patch[ci & 1] + tr * PC + tc;
-        const float *w0 = A.wt + (long)ci * 49;
-        const long wstride = (long)A.Cin * 49;
+        const float *w0 = wl + ci * 49;
+        const int wstride = A.Cin * 49;
 #pragma unroll
         for (int ky = 0; ky < 7; ++ky) {
             float row[PX + 6];
@@ -54,7 +58,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
             for (int kx = 0; kx < 7; ++kx) {
 #pragma unroll
                 for (int co = 0; co < 3; ++co) {
-                    const float wv = gp(w0)[co * wstride + ky * 7 + kx];
+                    const float wv = w0[co * wstride + ky * 7 + kx];
 #pragma unroll
                     for (int p = 0; p < PX; ++p) acc[co][p] += wv * row[p + kx];
                 }

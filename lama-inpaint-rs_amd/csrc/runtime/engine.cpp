@@ -23,7 +23,7 @@
 namespace lama {
 
 const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt",
-                                          "rfft2",   "irfft2",    "tail",    "finalize"};
+                                          "rfft2",   "irfft2",    "tail",    "finalize", "conv1x1res"};
 
 size_t step_numel(int step, int h, int w)
 {
@@ -46,12 +46,12 @@ namespace {
 
 const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lama_conv3x3", "lama_conv1x1",
                                           "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail",
-                                          "lama_finalize"};
+                                          "lama_finalize", "lama_conv1x1_res"};
 
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 void tile_shape(int family, int &tr, int &tc)
 {
-    if (family == F_CONV1) {
+    if (family == F_CONV1 || family == F_CONV1R) {
         tr = 1;
         tc = 64;
     } else {
@@ -589,6 +589,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
             Launch L{};
             L.fn = fn_[F_RFFT];
             L.family = F_RFFT;
+            L.block = LAMA_FFT_NT;
             L.stream = S_SIDE;
             L.wait_ev = L.record_ev = -1;
             L.grid = 192;
@@ -609,10 +610,10 @@ bool Engine::build_plan(Plan &p, std::string &err)
             L.bytes = fft_bytes + f4 * 192 * P8;  // + the fused feat read
             p.launches.push_back(L);
             // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
-            ConvProblem q2 = problem(F_CONV1, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
+            ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
                                      dst + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
             q2.addend = GC;
-            conv_launch(F_CONV1, {q2}, step, 2.0 * 192 * 384 * P8,
+            conv_launch(F_CONV1R, {q2}, step, 2.0 * 192 * 384 * P8,
                         f4 * (192 * P8 + 384 * P8 * (res ? 3 : 2) + 384 * 192), S_SIDE, EV_MAIN, EV_SIDE);
         }
     // step 23 (concat) is the same buffer as step 22; steps 24-26 the upsamplers
@@ -651,7 +652,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         L.family = F_TAIL;
         L.stream = S_MAIN;
         L.wait_ev = L.record_ev = -1;
-        L.grid = (unsigned)(((W + 63) / 64) * ((H + 7) / 8));
+        L.grid = (unsigned)(((W + LAMA_TAIL_COLS - 1) / LAMA_TAIL_COLS) * ((H + LAMA_TAIL_ROWS - 1) / LAMA_TAIL_ROWS));
         L.arg = put(&ta, sizeof ta);
         L.nparams = 1;
         L.step_end = 28;
@@ -707,7 +708,8 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err)
         pe.bytes = L.bytes;
         if (!check(hip_->hipEventRecord(pe.a, s), "hipEventRecord", err)) return false;
     }
-    if (!check(hip_->hipModuleLaunchKernel(L.fn, L.grid, 1, 1, LAMA_NT, 1, 1, L.shmem, s, params, nullptr),
+    const unsigned block = L.block ? L.block : LAMA_NT;
+    if (!check(hip_->hipModuleLaunchKernel(L.fn, L.grid, 1, 1, block, 1, 1, L.shmem, s, params, nullptr),
                kFamilyName[L.family], err))
         return false;
     if (prof) {
@@ -1034,6 +1036,7 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
     Launch L{};
     L.fn = fn_[inverse ? F_IRFFT : F_RFFT];
     L.family = inverse ? F_IRFFT : F_RFFT;
+    L.block = LAMA_FFT_NT;
     L.grid = (unsigned)c;
     L.shmem = (unsigned)lds;
     L.arg = da;
@@ -1045,6 +1048,10 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
 bool Engine::op_tail(const float *x, int cin, int h, int w, const float *wt, const float *bias, float *out,
                      std::string &err)
 {
+    if (cin < 1 || cin > 64) {
+        err = "op_tail: the tail kernel stages at most 64 input channels of weights";
+        return false;
+    }
     Scratch sc{hip_, {}};
     UPLOAD(dx, x, (size_t)cin * h * w);
     UPLOAD(dw, wt, (size_t)3 * cin * 49);
@@ -1063,7 +1070,7 @@ bool Engine::op_tail(const float *x, int cin, int h, int w, const float *wt, con
     Launch L{};
     L.fn = fn_[F_TAIL];
     L.family = F_TAIL;
-    L.grid = (unsigned)(((w + 63) / 64) * ((h + 7) / 8));
+    L.grid = (unsigned)(((w + LAMA_TAIL_COLS - 1) / LAMA_TAIL_COLS) * ((h + LAMA_TAIL_ROWS - 1) / LAMA_TAIL_ROWS));
     L.arg = da;
     L.nparams = 1;
     if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;

@@ -12,7 +12,7 @@
 
 namespace lama {
 
-enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_COUNT };
+enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_CONV1R, F_COUNT };
 extern const char *const kFamilyName[F_COUNT];
 
 // Number of plan steps of the reference (model.rs:135-207) and the size in
@@ -39,6 +39,7 @@ struct Launch {
     int wait_ev;    // event the stream waits for before the launch, or -1
     int record_ev;  // event recorded on the stream after the launch, or -1
     unsigned grid;
+    unsigned block;  // threads per block (0 = LAMA_NT)
     unsigned shmem;
     void *arg;   // device pointer to this launch's descriptor(s)
     int nprob;   // conv kernels: number of problems (second parameter)
