@@ -1170,3 +1170,13 @@ OR_EXPORT int or_net_bn(void *p, int i, char *prefix, int prefix_len, float *mea
     if (var && b->cal_var) memcpy(var, b->cal_var, sizeof(float) * b->n);
     return b->n;
 }
+
+/* Thread count of the OpenMP regions (tests check thread-count independence). */
+OR_EXPORT void or_set_threads(int n)
+{
+#ifdef _OPENMP
+    omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
