@@ -89,6 +89,7 @@ class Store:
     """WeightStore (weights.rs:80-139): the mapped container and its tensor table."""
 
     def __init__(self, path, map=True):
+        self.handle = None
         err = ctypes.create_string_buffer(1024)
         h = ctypes.c_void_p()
         if lib().lama_store_open(os.fsencode(path), 1 if map else 0, ctypes.byref(h), err, 1024):

@@ -14,7 +14,7 @@ import torch.nn.functional as F
 
 def forward(W, x):
     """W: {name: np.ndarray}; x: [4][h][w] -> (out [3][h][w], {step: activation})."""
-    t = lambda n: torch.from_numpy(np.ascontiguousarray(W[n], np.float32))  # noqa: E731
+    t = lambda n: torch.from_numpy(np.array(W[n], np.float32))  # noqa: E731
     steps = {}
 
     def bn(y, p):
