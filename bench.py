@@ -36,8 +36,11 @@ def main():
     ap.add_argument("--size", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-size", type=int, default=0, help="CPU sample size (default: the workload size)")
-    ap.add_argument("--traffic", type=str, default=None,
-                    help="JSON file with measured HBM bytes per launch of the dominant kernel")
+    ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "traffic_conv3x3_512.json"),
+                    help="JSON with the measured HBM bytes per launch of the dominant kernel")
+    ap.add_argument("--copy-probe", type=int, default=0,
+                    help="MiB of one untimed device-to-device copy made before the warmup: the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs one forward on one GPU; multi-GPU runs are not part of this build "
@@ -64,6 +67,14 @@ def main():
     d_in = eng.malloc(x.nbytes)
     d_out = eng.malloc(3 * S * S * 4)
     eng.upload(d_in, x)
+
+    if args.copy_probe:
+        nb = args.copy_probe << 20
+        a, b = eng.malloc(nb), eng.malloc(nb)
+        eng.copy_d2d(b, a, nb)
+        eng.synchronize()
+        eng.free(a)
+        eng.free(b)
 
     for _ in range(args.warmup):
         eng.forward_device(d_in, S, S, d_out)
@@ -94,6 +105,14 @@ def main():
     eng.download(out, d_out)
     assert np.isfinite(out).all()
 
+    # PCIe-inclusive rate: host input -> host output through lama_hip_forward
+    n_io = max(3, min(10, args.steps))
+    t = time.perf_counter()
+    for _ in range(n_io):
+        host_out = eng.forward(x)
+    host_io = n_io / (time.perf_counter() - t)
+    assert np.array_equal(host_out, out)
+
     ms = elapsed * 1e3 / args.steps
     d = prof[dom]
     launch_ms = d["ms"] / max(1, d["launches"])
@@ -102,7 +121,9 @@ def main():
     traffic = None
     if args.traffic and os.path.exists(args.traffic):
         with open(args.traffic) as fh:
-            traffic = json.load(fh).get(dom)
+            t = json.load(fh)
+        if t.get("size") == S:
+            traffic = t["bytes_per_launch"]
 
     conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt", "conv1x1res"]
     conv_ms = sum(fam[f]["ms"] for f in conv_fams) / 3
@@ -157,6 +178,7 @@ def main():
         "conv_frac_of_peak": round(conv_flops / (conv_ms * 1e9) / PEAK_FP32_MFMA, 4),
         "fft_gbps": round(fft_bytes / (fft_ms * 1e6), 1) if fft_ms > 0 else None,
         "fft_frac_of_hbm": round(fft_bytes / (fft_ms * 1e6) / PEAK_HBM, 4) if fft_ms > 0 else None,
+        "host_io_passes_per_s": round(host_io, 3),
         "per_family": per_family,
         "cpu_baseline": cpu,
     }

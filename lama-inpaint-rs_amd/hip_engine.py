@@ -145,6 +145,9 @@ class Engine:
         self._check(lib().lama_hip_memcpy(self.ctx, a.ctypes.data, dptr, a.nbytes, 2, self._err, 4096))
         return a
 
+    def copy_d2d(self, dst, src, nbytes):
+        self._check(lib().lama_hip_memcpy(self.ctx, dst, src, nbytes, 3, self._err, 4096))
+
     def synchronize(self):
         self._check(lib().lama_hip_synchronize(self.ctx, self._err, 4096))
 
