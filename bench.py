@@ -168,7 +168,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded random-init Big-LaMa weights, blurred-noise image, brush-stroke mask)",
-        "config": {"workload": f"Big-LaMa generator whole-image pass {S}x{S}, batch 1 (BASELINE configs[3])",
+        "config": {"workload": f"Big-LaMa generator whole-image pass {S}x{S}, batch 1"
+                               + {512: " (BASELINE configs[3])", 2048: " (BASELINE configs[4])",
+                                  256: " (BASELINE configs[0] shape)"}.get(S, ""),
                    "h": S, "w": S, "mask_coverage": round(coverage, 4), "launches_per_pass": eng.launch_count(S, S)},
         "roofline": {"bound": "mfma", "kernel": "lama_conv3x3 (FFC 3x3 implicit GEMMs: local in 4 K-quarters + l2g, one launch)",
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",

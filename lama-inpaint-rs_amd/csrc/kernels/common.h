@@ -88,6 +88,13 @@ struct FftArgs {
     float *out;         // rfft: stacked [2C][H][Wh]; irfft: real [C][H][W]
     const float *feat;  // irfft only: added to the output (f + ifft)
     float scale;        // 1/sqrt(H*W)
+    // Split mode (planes too large for one block's LDS): the row and column
+    // transforms are separate launches and the half spectrum between them is
+    // interleaved complex [C][H][Wh] in `tmp`.  `rows_per_block` row pairs,
+    // `cols_per_block` columns per block.
+    int rows_per_block;
+    float *tmp;
+    int cols_per_block;
     int pad_;
 };
 

@@ -317,3 +317,147 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
         }
     }
 }
+
+// ---- split mode: row and column transforms as separate launches ----------
+//
+// For bottleneck planes whose two ping-pong buffers do not fit one block's
+// LDS (2048x2048 inputs give 256x256 planes), each 2-D transform becomes a
+// row launch and a column launch.  A row block transforms `rows_per_block`
+// row pairs of one channel, a column block `cols_per_block` adjacent columns
+// of one channel over all H rows; the half spectrum between the two launches
+// is interleaved complex [C][H][Wh] in A.tmp.  The butterflies, twiddles and
+// pass order are those of the single-block kernels above.
+
+namespace {
+
+__device__ __forceinline__ void load_table(const float *tw, int n, float2 *dst)
+{
+    const LAMA_GLOBAL float2 *g = gp(reinterpret_cast<const float2 *>(tw));
+    for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = g[i];
+}
+
+}  // namespace
+
+// real [C][H][W] -> tmp: x transforms of row pairs, split into half spectra.
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const FftArgs *__restrict__ args)
+{
+    extern __shared__ float2 sm[];
+    const FftArgs &A = *args;
+    const int H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2, PB = A.rows_per_block;
+    const int nchunk = (HP + PB - 1) / PB, c = blockIdx.x / nchunk;
+    const int p0 = (blockIdx.x - c * nchunk) * PB, np = min(PB, HP - p0);
+    float2 *b0 = sm, *b1 = sm + PB * W, *twr = sm + 2 * PB * W;
+    load_table(A.row.tw, W, twr);
+    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W + (long)(2 * p0) * W;
+    const int rows = min(2 * np, H - 2 * p0);  // real rows present in this block
+    for (int idx = threadIdx.x; idx < np * W; idx += blockDim.x) {
+        const int p = idx / W, x = idx - p * W;
+        const float a = src[(2 * p) * W + x];
+        const float b = 2 * p + 1 < rows ? src[(2 * p + 1) * W + x] : 0.f;
+        b0[idx] = make_float2(a, b);
+    }
+    __syncthreads();
+    const float2 *r = stockham(A.row, twr, b0, b1, np, W, 1, A.row.sign_fwd);
+    LAMA_GLOBAL float2 *t = gp(reinterpret_cast<float2 *>(A.tmp)) + (long)c * H * Wh + (long)(2 * p0) * Wh;
+    for (int idx = threadIdx.x; idx < rows * Wh; idx += blockDim.x) {
+        const int y = idx / Wh, k = idx - y * Wh, p = y >> 1;
+        const float2 z = r[p * W + k], zm = r[p * W + (W - k) % W];
+        t[idx] = (y & 1) ? make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x))
+                         : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+    }
+}
+
+// tmp -> stacked [2C][H][Wh]: y transforms of the kept columns, ortho scale.
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const FftArgs *__restrict__ args)
+{
+    extern __shared__ float2 sm[];
+    const FftArgs &A = *args;
+    const int H = A.H, Wh = A.Wh, CB = A.cols_per_block;
+    const int nchunk = (Wh + CB - 1) / CB, c = blockIdx.x / nchunk;
+    const int x0 = (blockIdx.x - c * nchunk) * CB, nc = min(CB, Wh - x0);
+    float2 *b0 = sm, *b1 = sm + H * CB, *twc = sm + 2 * H * CB;
+    load_table(A.col.tw, H, twc);
+    const LAMA_GLOBAL float2 *t = gp(reinterpret_cast<const float2 *>(A.tmp)) + (long)c * H * Wh + x0;
+    for (int idx = threadIdx.x; idx < H * nc; idx += blockDim.x) {
+        const int y = idx / nc, j = idx - y * nc;
+        b0[idx] = t[(long)y * Wh + j];
+    }
+    __syncthreads();
+    const float2 *q = stockham(A.col, twc, b0, b1, nc, 1, nc, A.col.sign_fwd);
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh + x0, *dim = dre + (long)H * Wh;
+    for (int idx = threadIdx.x; idx < H * nc; idx += blockDim.x) {
+        const int y = idx / nc, j = idx - y * nc;
+        const float2 v = q[idx];
+        dre[(long)y * Wh + j] = v.x * A.scale;
+        dim[(long)y * Wh + j] = v.y * A.scale;
+    }
+}
+
+// stacked [2C][H][Wh] -> tmp: inverse y transforms of the stored columns.
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const FftArgs *__restrict__ args)
+{
+    extern __shared__ float2 sm[];
+    const FftArgs &A = *args;
+    const int H = A.H, Wh = A.Wh, CB = A.cols_per_block;
+    const int nchunk = (Wh + CB - 1) / CB, c = blockIdx.x / nchunk;
+    const int x0 = (blockIdx.x - c * nchunk) * CB, nc = min(CB, Wh - x0);
+    float2 *b0 = sm, *b1 = sm + H * CB, *twc = sm + 2 * H * CB;
+    load_table(A.col.tw, H, twc);
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh + x0, *sim = sre + (long)H * Wh;
+    for (int idx = threadIdx.x; idx < H * nc; idx += blockDim.x) {
+        const int y = idx / nc, j = idx - y * nc;
+        b0[idx] = make_float2(sre[(long)y * Wh + j], sim[(long)y * Wh + j]);
+    }
+    __syncthreads();
+    const float2 *q = stockham(A.col, twc, b0, b1, nc, 1, nc, -A.col.sign_fwd);
+    LAMA_GLOBAL float2 *t = gp(reinterpret_cast<float2 *>(A.tmp)) + (long)c * H * Wh + x0;
+    for (int idx = threadIdx.x; idx < H * nc; idx += blockDim.x) {
+        const int y = idx / nc, j = idx - y * nc;
+        t[(long)y * Wh + j] = q[idx];
+    }
+}
+
+// tmp -> real [C][H][W]: complex-to-real x transforms of row pairs, ortho
+// scale, plus feat.
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const FftArgs *__restrict__ args)
+{
+    extern __shared__ float2 sm[];
+    const FftArgs &A = *args;
+    const int H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2, PB = A.rows_per_block;
+    const int nchunk = (HP + PB - 1) / PB, c = blockIdx.x / nchunk;
+    const int p0 = (blockIdx.x - c * nchunk) * PB, np = min(PB, HP - p0);
+    float2 *b0 = sm, *b1 = sm + PB * W, *twr = sm + 2 * PB * W;
+    load_table(A.row.tw, W, twr);
+    const int rows = min(2 * np, H - 2 * p0);
+    const LAMA_GLOBAL float2 *t = gp(reinterpret_cast<const float2 *>(A.tmp)) + (long)c * H * Wh + (long)(2 * p0) * Wh;
+    for (int idx = threadIdx.x; idx < np * W; idx += blockDim.x) {
+        const int p = idx / W, x = idx - p * W;
+        float2 g[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int y = 2 * p + h;
+            float2 v = make_float2(0.f, 0.f);
+            if (y < rows) {
+                if (x < Wh) {
+                    v = t[y * Wh + x];
+                    if (x == 0 || 2 * x == W) v.y = 0.f;
+                } else {
+                    v = t[y * Wh + (W - x)];
+                    v.y = -v.y;
+                }
+            }
+            g[h] = v;
+        }
+        b0[idx] = make_float2(g[0].x - g[1].y, g[0].y + g[1].x);
+    }
+    __syncthreads();
+    const float2 *q = stockham(A.row, twr, b0, b1, np, W, 1, -A.row.sign_fwd);
+    const long base = (long)c * H * W + (long)(2 * p0) * W;
+    const LAMA_GLOBAL float *f = gp(A.feat) + base;
+    LAMA_GLOBAL float *d = gp(A.out) + base;
+    for (int idx = threadIdx.x; idx < rows * W; idx += blockDim.x) {
+        const int y = idx / W, x = idx - y * W;
+        const float2 v = q[(y >> 1) * W + x];
+        d[idx] = ((y & 1) ? v.y : v.x) * A.scale + f[idx];
+    }
+}

@@ -48,6 +48,8 @@ const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lam
                                           "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail",
                                           "lama_finalize", "lama_conv1x1_res"};
 
+const char *const kSplitName[4] = {"lama_rfft2_rows", "lama_rfft2_cols", "lama_irfft2_cols", "lama_irfft2_rows"};
+
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 void tile_shape(int family, int &tr, int &tc)
 {
@@ -216,6 +218,13 @@ bool Engine::open(std::string &err)
     if (!check(hip_->hipModuleLoadData(&module_, lama_hsaco_start), "hipModuleLoadData", err)) return false;
     for (int f = 0; f < F_COUNT; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
+    for (int f = 0; f < 4; ++f)
+        if (!check(hip_->hipModuleGetFunction(&fn_split_[f], module_, kSplitName[f]), kSplitName[f], err)) return false;
+    {
+        int lds = 0;
+        if (hip_->hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_) == hipSuccess && lds > 0)
+            max_lds_ = (size_t)lds;
+    }
     if (!check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err) ||
         !check(hip_->hipStreamCreate(&side_), "hipStreamCreate", err))
         return false;
@@ -360,6 +369,73 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
     return true;
 }
 
+// Single-block mode keeps a whole plane (two ping-pong buffers + both
+// twiddle tables) in one block's LDS; it is used while that fits in 64 KB.
+// Larger planes (or LAMA_FFT_SPLIT=1) use the row/column launches, each
+// block holding at most 64 KB of ping-pong buffers.
+bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
+{
+    const int Wh = W / 2 + 1, HP = (H + 1) / 2;
+    const size_t f2 = 8;  // bytes per complex value
+    g = FftGeom{};
+    g.lds = (2 * std::max((size_t)HP * W, (size_t)H * Wh) + H + W) * f2;
+    const char *env = getenv("LAMA_FFT_SPLIT");
+    const bool force = env && atoi(env) == 1;
+    if (!force && g.lds <= std::min<size_t>(max_lds_, 64 * 1024)) {
+        g.grid_rows = g.grid_cols = (unsigned)C;  // one block per plane
+        return true;
+    }
+    // complex values the two ping-pong buffers may hold next to the twiddles
+    const size_t cap = max_lds_ / f2, buf = 64 * 1024 / f2;
+    const size_t avail_r = cap > (size_t)W ? std::min(buf, cap - W) : 0;
+    const size_t avail_c = cap > (size_t)H ? std::min(buf, cap - H) : 0;
+    g.split = true;
+    g.rows_per_block = (int)std::max<size_t>(1, std::min<size_t>(HP, avail_r / (2 * (size_t)W)));
+    g.cols_per_block = (int)std::max<size_t>(1, std::min<size_t>(Wh, avail_c / (2 * (size_t)H)));
+    g.lds_rows = (2 * (size_t)g.rows_per_block * W + W) * f2;
+    g.lds_cols = (2 * (size_t)g.cols_per_block * H + H) * f2;
+    if (g.lds_rows > max_lds_ || g.lds_cols > max_lds_) {
+        err = "FFT plane " + std::to_string(W) + "x" + std::to_string(H) + " needs more LDS per block than the device has";
+        return false;
+    }
+    g.grid_rows = (unsigned)(C * ((HP + g.rows_per_block - 1) / g.rows_per_block));
+    g.grid_cols = (unsigned)(C * ((Wh + g.cols_per_block - 1) / g.cols_per_block));
+    g.tmp_bytes = (size_t)C * H * Wh * f2;
+    return true;
+}
+
+// The launches of one rfft2 (inverse = false) or irfft2 over the descriptor
+// `arg`: one in single-block mode, row + column launches in split mode (the
+// inverse runs columns first).  bytes_a / bytes_b: algorithmic bytes of the
+// input and output sides, for the profile.
+void Engine::push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int stream, double bytes_a, double bytes_b)
+{
+    Launch L{};
+    L.family = inverse ? F_IRFFT : F_RFFT;
+    L.block = LAMA_FFT_NT;
+    L.stream = stream;
+    L.wait_ev = L.record_ev = -1;
+    L.arg = arg;
+    L.nparams = 1;
+    L.step_end = -1;
+    if (!g.split) {
+        L.fn = fn_[L.family];
+        L.grid = g.grid_rows;
+        L.shmem = (unsigned)g.lds;
+        L.bytes = bytes_a + bytes_b;
+        p.launches.push_back(L);
+        return;
+    }
+    for (int k = 0; k < 2; ++k) {
+        const bool rows = inverse ? k == 1 : k == 0;
+        L.fn = fn_split_[inverse ? 2 + k : k];
+        L.grid = rows ? g.grid_rows : g.grid_cols;
+        L.shmem = (unsigned)(rows ? g.lds_rows : g.lds_cols);
+        L.bytes = k == 0 ? bytes_a : bytes_b;
+        p.launches.push_back(L);
+    }
+}
+
 Plan *Engine::plan_for(int h, int w, std::string &err)
 {
     if (!have_weights_) {
@@ -393,13 +469,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
     FftLen frow, fcol;
     std::vector<float> twr, twc;
     if (!fft_len(W8, frow, twr, err) || !fft_len(H8, fcol, twc, err)) return false;
-    const int HP = (H8 + 1) / 2;
-    const size_t fft_lds = (2 * std::max((size_t)HP * W8, PS) + H8 + W8) * 8;
-    if (fft_lds > 160 * 1024) {
-        err = "bottleneck plane " + std::to_string(W8) + "x" + std::to_string(H8) +
-              " exceeds the LDS-resident FFT (input up to about 1024x1024)";
-        return false;
-    }
+    FftGeom fg;
+    if (!fft_geom(192, H8, W8, fg, err)) return false;
 
     // arena layout
     size_t off = 0;
@@ -414,10 +485,11 @@ bool Engine::build_plan(Plan &p, std::string &err)
     const size_t o_gc = take(384 * P8 * 4);
     // the FFC local GEMM runs as four K quarters with raw partial outputs
     const size_t o_lq = take(4 * 128 * P8 * 4);
+    const size_t o_tmp = take(fg.split ? fg.tmp_bytes : 0);
 
     const size_t o_twr = take(twr.size() * 4), o_twc = take(twc.size() * 4);
     const size_t n_conv = 4 + 36 * 7 + 4 * 3;  // problems
-    const size_t n_puts = 4 + 36 * 5 + 3 + 3;  // descriptor uploads, each 256-byte aligned
+    const size_t n_puts = 4 + 36 * 2 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
     const size_t o_desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
     p.arena_bytes = off;
     if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
@@ -519,6 +591,9 @@ bool Engine::build_plan(Plan &p, std::string &err)
     fa.W = W8;
     fa.Wh = Wh;
     fa.scale = (float)(1.0 / std::sqrt((double)H8 * W8));
+    fa.rows_per_block = fg.rows_per_block;
+    fa.cols_per_block = fg.cols_per_block;
+    fa.tmp = fg.split ? (float *)(base + o_tmp) : nullptr;
     fa.in = Fb;
     fa.out = Sb;
     void *d_rfft = put(&fa, sizeof fa);
@@ -526,7 +601,6 @@ bool Engine::build_plan(Plan &p, std::string &err)
     fa.out = G;
     fa.feat = Fb;
     void *d_irfft = put(&fa, sizeof fa);
-    const double fft_bytes = f4 * 192 * P8 + 8.0 * 192 * PS;  // real plane + half spectrum (re, im)
 
     // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual).
     // Main stream: one grouped launch of the local GEMM, BN_l(l2l(x_l) +
@@ -586,29 +660,12 @@ bool Engine::build_plan(Plan &p, std::string &err)
             conv_launch(F_CONV1,
                         {problem(F_CONV1, seg(src + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1, 192, Fb, P8, (int)P8, nullptr)},
                         -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384), S_SIDE, k == 0 ? EV_FORK : -1);
-            Launch L{};
-            L.fn = fn_[F_RFFT];
-            L.family = F_RFFT;
-            L.block = LAMA_FFT_NT;
-            L.stream = S_SIDE;
-            L.wait_ev = L.record_ev = -1;
-            L.grid = 192;
-            L.shmem = (unsigned)fft_lds;
-            L.arg = d_rfft;
-            L.nparams = 1;
-            L.step_end = -1;
-            L.flops = 0;
-            L.bytes = fft_bytes;
-            p.launches.push_back(L);
+            push_fft(p, false, fg, d_rfft, S_SIDE, f4 * 192 * P8, 8.0 * 192 * PS);
             // FourierUnit conv over the stacked spectrum + BN + ReLU
             conv_launch(F_CONV1,
                         {problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS, (int)PS, nullptr)},
                         -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384), S_SIDE);
-            L.fn = fn_[F_IRFFT];
-            L.family = F_IRFFT;
-            L.arg = d_irfft;
-            L.bytes = fft_bytes + f4 * 192 * P8;  // + the fused feat read
-            p.launches.push_back(L);
+            push_fft(p, true, fg, d_irfft, S_SIDE, 8.0 * 192 * PS, 2 * f4 * 192 * P8);  // + the fused feat read
             // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
             ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
                                      dst + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
@@ -999,12 +1056,9 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
     FftLen fr, fc;
     std::vector<float> twr, twc;
     if (!fft_len(w, fr, twr, err) || !fft_len(h, fc, twc, err)) return false;
-    const int Wh = w / 2 + 1, HP = (h + 1) / 2;
-    const size_t lds = (2 * std::max((size_t)HP * w, (size_t)h * Wh) + h + w) * 8;
-    if (lds > 160 * 1024) {
-        err = "plane too large for the LDS-resident FFT";
-        return false;
-    }
+    FftGeom g;
+    if (!fft_geom(c, h, w, g, err)) return false;
+    const int Wh = w / 2 + 1;
     const size_t nin = inverse ? 2ul * c * h * Wh : (size_t)c * h * w;
     const size_t nout = inverse ? (size_t)c * h * w : 2ul * c * h * Wh;
     std::vector<float> zeros;
@@ -1018,6 +1072,7 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
     UPLOAD(dtr, twr.data(), twr.size());
     UPLOAD(dtc, twc.data(), twc.size());
     UPLOAD(dfeat, inverse ? feat : nullptr, inverse ? (size_t)c * h * w : 1);
+    UPLOAD(dtmp, nullptr, g.split ? g.tmp_bytes / 4 : 1);
     FftArgs a{};
     a.row = fr;
     a.col = fc;
@@ -1031,17 +1086,16 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
     a.out = dout;
     a.feat = inverse ? dfeat : nullptr;
     a.scale = (float)(1.0 / std::sqrt((double)h * w));
+    a.rows_per_block = g.rows_per_block;
+    a.cols_per_block = g.cols_per_block;
+    a.tmp = g.split ? dtmp : nullptr;
     UPLOAD(da, nullptr, (sizeof a + 3) / 4);
     if (!check(hip_->hipMemcpy(da, &a, sizeof a, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
-    Launch L{};
-    L.fn = fn_[inverse ? F_IRFFT : F_RFFT];
-    L.family = inverse ? F_IRFFT : F_RFFT;
-    L.block = LAMA_FFT_NT;
-    L.grid = (unsigned)c;
-    L.shmem = (unsigned)lds;
-    L.arg = da;
-    L.nparams = 1;
-    if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
+    Plan tmp;
+    push_fft(tmp, inverse, g, da, S_MAIN, 0, 0);
+    for (const Launch &L : tmp.launches)
+        if (!launch(L, stream_, err)) return false;
+    if (!check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
     return check(hip_->hipMemcpy(out, dout, nout * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);
 }
 

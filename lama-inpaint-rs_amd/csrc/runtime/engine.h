@@ -48,6 +48,16 @@ struct Launch {
     double flops, bytes;
 };
 
+// How the rfft2/irfft2 of one [C][H][W] batch of planes are launched.
+struct FftGeom {
+    bool split = false;
+    size_t lds = 0;                 // single-block mode: bytes per block
+    int rows_per_block = 0, cols_per_block = 0;
+    size_t lds_rows = 0, lds_cols = 0;
+    unsigned grid_rows = 0, grid_cols = 0;
+    size_t tmp_bytes = 0;           // interleaved complex [C][H][W/2+1]
+};
+
 struct Plan {
     int H = 0, W = 0;
     void *arena = nullptr;
@@ -100,12 +110,17 @@ private:
     bool run(Plan &p, hipStream_t s, float *const *steps, std::string &err);
     bool launch(const Launch &L, hipStream_t s, std::string &err);
     bool fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err);
+    bool fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const;
+    void push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int stream, double bytes_a, double bytes_b);
     void collect_events();
 
     const HipApi *hip_ = nullptr;
     int device_ = 0;
     hipModule_t module_ = nullptr;
     hipFunction_t fn_[F_COUNT] = {};
+    // split-mode FFT kernels: rfft2 rows, rfft2 cols, irfft2 cols, irfft2 rows
+    hipFunction_t fn_split_[4] = {};
+    size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};
 

@@ -77,3 +77,57 @@ def test_forward_repeatable_and_shapes(pkg, engine):
     # head, 3 downsamplers, 36 FFCs x (grouped GEMM, finalize, conv1, rfft2, FU conv, irfft2, conv2),
     # 3 upsamplers, tail
     assert engine.launch_count(64, 128) == 1 + 3 + 36 * 7 + 3 + 1
+
+
+def test_forward_split_fft_1024(pkg, engine, oracle_cal):
+    """1024x1024: the 128x128 bottleneck planes exceed one block's 64 KB LDS
+    budget, so every rfft2/irfft2 runs as row + column launches."""
+    h = w = 1024
+    img, mask = _case(pkg, h, w, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    print(f"case {h}x{w} strokes (split FFT)", flush=True)
+    got, got_steps = engine.forward_steps(x, list(range(29)))
+    assert engine.launch_count(h, w) == 1 + 3 + 36 * 9 + 3 + 1
+    ref, ref_steps = oracle_cal.forward(x, steps=True)
+    for s in range(29):
+        e = rel_err(got_steps[s], ref_steps[s])
+        assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+    u8g = pkg.host_api.composite(img, mask, got, 0, 0)
+    u8r = pkg.host_api.composite(img, mask, ref, 0, 0)
+    d = np.abs(u8g.astype(int) - u8r.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
+
+
+def test_forward_split_forced_matches_single(pkg, engine, monkeypatch):
+    """The split launches compute the same transform as the single-block
+    kernels: at 128x96 the whole forward agrees to float rounding."""
+    img, mask = _case(pkg, 128, 96, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    a = engine.forward(x)
+    monkeypatch.setenv("LAMA_FFT_SPLIT", "1")
+    eng2 = pkg.hip_engine.Engine()
+    eng2.load_weights(engine._store)
+    b = eng2.forward(x)
+    assert eng2.launch_count(128, 96) == 1 + 3 + 36 * 9 + 3 + 1
+    eng2.close()
+    assert rel_err(b, a) < 1e-5
+
+
+def test_forward_2048_whole_image(pkg, engine):
+    """configs[4] at its full size (bottleneck 512 x 256 x 256): checked by
+    size-independent properties -- finite, bitwise repeatable, sigmoid range,
+    unmasked pixels of the composite bit-exact."""
+    h = w = 2048
+    H = pkg.host_api
+    img = H.synth_image(h, w, 1)
+    mask, _ = H.synth_mask_rect(h, w, 300, 300, 2)
+    x = H.build_input(img, mask)
+    print(f"case {h}x{w} rect 300", flush=True)
+    a = engine.forward(x)
+    b = engine.forward(x)
+    assert np.array_equal(a, b)
+    assert np.isfinite(a).all() and a.min() >= 0 and a.max() <= 1
+    u8 = H.composite(img, mask, a, 0, 0)
+    keep = mask == 0
+    assert np.array_equal(u8[keep], img[keep])
+    assert engine.launch_count(h, w) == 1 + 3 + 36 * 9 + 3 + 1

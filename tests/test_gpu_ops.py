@@ -72,8 +72,24 @@ def test_conv_transpose(engine, cin, cout, h, w):
 SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), (64, 33), (16, 12), (38, 19)]
 
 
-@pytest.mark.parametrize("h,w", SIZES)
-def test_rfft2(engine, h, w):
+# planes too large for one block's LDS take the row/column split launches
+LARGE = [(256, 256), (200, 130), (150, 90)]
+
+
+@pytest.fixture(params=["single", "split"])
+def fft_mode(request, monkeypatch):
+    """'split' forces the row/column launches (LAMA_FFT_SPLIT=1) at every size."""
+    if request.param == "split":
+        monkeypatch.setenv("LAMA_FFT_SPLIT", "1")
+    else:
+        monkeypatch.delenv("LAMA_FFT_SPLIT", raising=False)
+    return request.param
+
+
+@pytest.mark.parametrize("h,w", SIZES + LARGE)
+def test_rfft2(engine, fft_mode, h, w):
+    if fft_mode == "single" and (h, w) in LARGE:
+        pytest.skip("large planes always split")
     rng = np.random.default_rng(h * 100 + w)
     c = 3
     x = rng.standard_normal((c, h, w), np.float32)
@@ -83,8 +99,10 @@ def test_rfft2(engine, h, w):
     assert rel_err(got, ref) < TOL
 
 
-@pytest.mark.parametrize("h,w", SIZES)
-def test_irfft2(engine, h, w):
+@pytest.mark.parametrize("h,w", SIZES + LARGE)
+def test_irfft2(engine, fft_mode, h, w):
+    if fft_mode == "single" and (h, w) in LARGE:
+        pytest.skip("large planes always split")
     rng = np.random.default_rng(h * 100 + w + 1)
     c = 3
     wh = w // 2 + 1
