@@ -10,6 +10,18 @@
 #define LAMA_TAIL_COLS 64
 
 #ifdef __HIP_DEVICE_COMPILE__
+// Wave priority of the SpectralTransform chain (conv1, rfft2, FU conv,
+// irfft2, conv2).  It runs on a second stream beside the FFC 3x3 GEMM and is
+// the critical path of every FFC; when its workgroups share a CU with the
+// GEMM's, a higher priority lets their instructions issue first.
+#ifndef LAMA_SIDE_PRIO
+#define LAMA_SIDE_PRIO 3
+#endif
+__device__ __forceinline__ void side_priority()
+{
+    if (LAMA_SIDE_PRIO > 0) __builtin_amdgcn_s_setprio(LAMA_SIDE_PRIO);
+}
+
 // Pointers read out of descriptors are generic; casting them to the global
 // address space lets the compiler emit global_load/global_store instead of
 // flat accesses (which also count against lgkmcnt and so serialise with LDS

@@ -381,6 +381,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit conv).
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvProblem *__restrict__ probs, int nprob)
 {
+    side_priority();
     __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
@@ -392,6 +393,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvPro
 // residual).
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1_res(const ConvProblem *__restrict__ probs, int nprob)
 {
+    side_priority();
     __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);

@@ -206,6 +206,7 @@ __device__ __forceinline__ void load_twiddles(const FftArgs &A, float2 *twr, flo
 // One block per channel: real [C][H][W] -> stacked [2C][H][W/2+1], ortho.
 extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftArgs *__restrict__ args)
 {
+    side_priority();
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
@@ -257,6 +258,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
 // plus feat: out = feat + irfft2(in).
 extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftArgs *__restrict__ args)
 {
+    side_priority();
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
@@ -341,6 +343,7 @@ __device__ __forceinline__ void load_table(const float *tw, int n, float2 *dst)
 // real [C][H][W] -> tmp: x transforms of row pairs, split into half spectra.
 extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const FftArgs *__restrict__ args)
 {
+    side_priority();
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2, PB = A.rows_per_block;
@@ -370,6 +373,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const 
 // tmp -> stacked [2C][H][Wh]: y transforms of the kept columns, ortho scale.
 extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const FftArgs *__restrict__ args)
 {
+    side_priority();
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, Wh = A.Wh, CB = A.cols_per_block;
@@ -396,6 +400,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const 
 // stacked [2C][H][Wh] -> tmp: inverse y transforms of the stored columns.
 extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const FftArgs *__restrict__ args)
 {
+    side_priority();
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, Wh = A.Wh, CB = A.cols_per_block;
@@ -421,6 +426,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const
 // scale, plus feat.
 extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const FftArgs *__restrict__ args)
 {
+    side_priority();
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2, PB = A.rows_per_block;
