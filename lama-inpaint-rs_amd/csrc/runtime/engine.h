@@ -65,6 +65,8 @@ struct Plan {
     float *in = nullptr, *out = nullptr;
     std::vector<std::pair<const float *, size_t>> step_src;  // per step (nullptr: host-derived)
     std::vector<Launch> launches;
+    hipGraphExec_t graph = nullptr;  // the launch list captured once, replayed per forward
+    bool graph_failed = false;
 };
 
 class Engine {
@@ -108,6 +110,9 @@ private:
     Plan *plan_for(int h, int w, std::string &err);
     bool build_plan(Plan &p, std::string &err);
     bool run(Plan &p, hipStream_t s, float *const *steps, std::string &err);
+    bool replay(Plan &p, hipStream_t s, std::string &err);
+    bool use_graph() const;
+    void free_plan(Plan &p);
     bool launch(const Launch &L, hipStream_t s, std::string &err);
     bool fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err);
     bool fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const;

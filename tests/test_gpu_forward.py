@@ -131,3 +131,36 @@ def test_forward_2048_whole_image(pkg, engine):
     keep = mask == 0
     assert np.array_equal(u8[keep], img[keep])
     assert engine.launch_count(h, w) == 1 + 3 + 36 * 9 + 3 + 1
+
+
+def test_graph_replays_match_eager(pkg, engine, monkeypatch):
+    """The forward captured as one HIP graph and replayed: every replay, with
+    eager work and synchronisations in between, equals the per-launch path
+    bit for bit."""
+    img, mask = _case(pkg, 128, 96, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    monkeypatch.setenv("LAMA_GRAPH", "0")
+    eng0 = pkg.hip_engine.Engine()
+    eng0.load_weights(engine._store)
+    eager = eng0.forward(x)
+    eng0.close()
+    monkeypatch.setenv("LAMA_GRAPH", "1")
+    eng1 = pkg.hip_engine.Engine()
+    eng1.load_weights(engine._store)
+    rng = np.random.default_rng(3)
+    d_in = eng1.malloc(x.nbytes)
+    d_out = eng1.malloc(3 * 128 * 96 * 4)
+    eng1.upload(d_in, x)
+    for i in range(4):
+        out = eng1.forward(x) if i % 2 == 0 else None
+        if out is None:
+            eng1.forward_device(d_in, 128, 96, d_out)
+            eng1.synchronize()
+            out = np.empty((3, 128, 96), np.float32)
+            eng1.download(out, d_out)
+        assert np.array_equal(out, eager), f"replay {i}"
+        # eager work between replays
+        eng1.op_conv2d(rng.standard_normal((8, 9, 11), np.float32), rng.standard_normal((16, 8, 3, 3), np.float32))
+    eng1.free(d_in)
+    eng1.free(d_out)
+    eng1.close()
