@@ -268,9 +268,23 @@ __device__ __forceinline__ void epilogue_prefetch(EpiPre &e, const ConvProblem &
     }
 }
 
+// Per-channel epilogue operands (bias, BN scale, BN shift) of the block's 64
+// output channels: one value per thread for threads 0..191, loaded into a
+// register before the K loop and parked in LDS after it, so the epilogue
+// reads them from LDS instead of making dependent global round trips after
+// its first store (which the compiler may not reorder loads above).
+__device__ __forceinline__ float epi_param_load(const ConvProblem &P, int m0)
+{
+    const int t = threadIdx.x, row = t >> 6, c = min(m0 + (t & 63), P.M - 1);
+    if (t >= 192) return 0.f;
+    if (row == 0) return P.bias ? gp(P.bias)[c] : 0.f;
+    if (row == 1) return P.scale ? gp(P.scale)[c] : 1.f;
+    return P.scale ? gp(P.shift)[c] : 0.f;
+}
+
 template <int TR, int TC, bool PREFETCH>
-__device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, const ConvProblem &P, int m0, int oy0,
-                                         int ox0)
+__device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, const ConvProblem &P, const float *epl,
+                                         int m0, int oy0, int ox0)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
@@ -278,25 +292,35 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, con
     const int oy = oy0 + p / TC, ox = ox0 + p % TC;
     if (oy >= P.OH || ox >= P.OW) return;
     const long pix = (long)(oy * P.oy_mul + P.oy_off) * P.outW + (long)ox * P.ox_mul + P.ox_off;
+    float v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const int i = 8 * (r >> 2) + 4 * g + (r & 3);
-        const int co = m0 + wm * 32 + i;
-        if (co < P.M) {
-            float v = acc[r];
-            const long o = (long)co * P.out_cstride + pix;
-            if (P.bias) v += gp(P.bias)[co];
-            if (PREFETCH)
-                v += e.add[r];
-            else if (P.addend)
-                v += gp(P.addend)[o];
-            if (P.scale) v = v * gp(P.scale)[co] + gp(P.shift)[co];
-            if (P.relu) v = fmaxf(v, 0.f);
-            if (PREFETCH)
-                v += e.res[r];
-            else if (P.res)
-                v += gp(P.res)[o];
-            gp(P.out)[o] = v;
+        const int cl = wm * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const long o = (long)min(m0 + cl, P.M - 1) * P.out_cstride + pix;
+        float x = acc[r];
+        if (P.bias) x += epl[cl];
+        if (PREFETCH)
+            x += e.add[r];
+        else if (P.addend)
+            x += gp(P.addend)[o];
+        if (P.scale) x = x * epl[64 + cl] + epl[128 + cl];
+        if (P.relu) x = fmaxf(x, 0.f);
+        if (PREFETCH)
+            x += e.res[r];
+        else if (P.res)
+            x += gp(P.res)[o];
+        v[r] = x;
+    }
+    LAMA_GLOBAL float *out = gp(P.out);
+    const int cbase = m0 + wm * 32 + 4 * g;
+    if (m0 + 64 <= P.M) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) out[(long)(cbase + 8 * (r >> 2) + (r & 3)) * P.out_cstride + pix] = v[r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = cbase + 8 * (r >> 2) + (r & 3);
+            if (co < P.M) out[(long)co * P.out_cstride + pix] = v[r];
         }
     }
 }
@@ -304,11 +328,12 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, con
 // One 64 x 64 output tile of problem P: segment 0 with the template
 // geometry, then (SEG1) the optional 1x1 segment over a second source.
 template <class C0, bool SEG1, int NBUF = 2, bool PREFETCH = false>
-__device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *lds)
+__device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *lds, float *epl)
 {
     const int mb = b % P.mblocks, t = b / P.mblocks;
     const int tx = t % P.tiles_x, ty = t / P.tiles_x;
     const int m0 = mb * 64, oy0 = ty * C0::TR, ox0 = tx * C0::TC;
+    const float ep = epi_param_load(P, m0);
     EpiPre pre;
     if constexpr (PREFETCH) {
         epilogue_prefetch<C0::TR, C0::TC>(pre, P, m0, oy0, ox0);
@@ -324,7 +349,9 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
         using C1 = Cfg<1, 1, 1, false, C0::KC, C0::TR, C0::TC>;
         if (P.s1.nchunk > 0) run_segment<C1, NBUF>(acc, P.s1, m0, P.M, oy0, ox0, lds);
     }
-    epilogue<C0::TR, C0::TC, PREFETCH>(acc, pre, P, m0, oy0, ox0);
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    __syncthreads();
+    epilogue<C0::TR, C0::TC, PREFETCH>(acc, pre, P, epl, m0, oy0, ox0);
 }
 
 __device__ __forceinline__ int find_problem(const ConvProblem *probs, int nprob, int &b)
@@ -354,18 +381,20 @@ using CfgT11 = Cfg<2, 2, 1, false, 8, 2, 32>;
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvProblem *__restrict__ probs, int nprob)
 {
     __shared__ __attribute__((aligned(16))) float lds[CfgHead::LDS];
+    __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
-    conv_tile<CfgHead, false, 1>(probs[pi], b, lds);
+    conv_tile<CfgHead, false, 1>(probs[pi], b, lds, epl);
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvProblem *__restrict__ probs, int nprob)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
+    __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
-    conv_tile<CfgDown, false>(probs[pi], b, lds);
+    conv_tile<CfgDown, false>(probs[pi], b, lds, epl);
 }
 
 // FFC spatial convolutions: 3x3 stride 1 reflect pad 1, with an optional 1x1
@@ -373,9 +402,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvP
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvProblem *__restrict__ probs, int nprob)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(CfgFfc::LDS, CfgFfc1::LDS)];
+    __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
-    conv_tile<CfgFfc, true>(probs[pi], b, lds);
+    conv_tile<CfgFfc, true>(probs[pi], b, lds, epl);
 }
 
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit conv).
@@ -383,9 +413,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvPro
 {
     side_priority();
     __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
+    __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
-    conv_tile<Cfg1x1, false>(probs[pi], b, lds);
+    conv_tile<Cfg1x1, false>(probs[pi], b, lds, epl);
 }
 
 // The same with addend / residual fetched before the K loop (the
@@ -395,9 +426,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1_res(const Con
 {
     side_priority();
     __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
+    __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
-    conv_tile<Cfg1x1, false, 2, true>(probs[pi], b, lds);
+    conv_tile<Cfg1x1, false, 2, true>(probs[pi], b, lds, epl);
 }
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions
@@ -406,12 +438,13 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1_res(const Con
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(const ConvProblem *__restrict__ probs, int nprob)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
+    __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(probs, nprob, b);
     switch (pi) {
-    case 0: conv_tile<CfgT00, false>(probs[0], b, lds); break;
-    case 1: conv_tile<CfgT01, false>(probs[1], b, lds); break;
-    case 2: conv_tile<CfgT10, false>(probs[2], b, lds); break;
-    default: conv_tile<CfgT11, false>(probs[3], b, lds); break;
+    case 0: conv_tile<CfgT00, false>(probs[0], b, lds, epl); break;
+    case 1: conv_tile<CfgT01, false>(probs[1], b, lds, epl); break;
+    case 2: conv_tile<CfgT10, false>(probs[2], b, lds, epl); break;
+    default: conv_tile<CfgT11, false>(probs[3], b, lds, epl); break;
     }
 }

@@ -13,24 +13,47 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
     const long n = (long)A.C * A.plane;
     const long i = ((long)blockIdx.x * LAMA_NT + threadIdx.x) * 4;
     if (i >= n) return;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    const int m = n - i < 4 ? (int)(n - i) : 4;
-    if (m == 4) {  // [C][plane] is 16-byte aligned as a whole
-        for (int q = 0; q < A.nparts; ++q) {
-            const float4 u = *reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.part[q]) + i);
-            v[0] += u.x;
-            v[1] += u.y;
-            v[2] += u.z;
-            v[3] += u.w;
-        }
-    } else {
-        for (int q = 0; q < A.nparts; ++q)
-            for (int e = 0; e < m; ++e) v[e] += gp(A.part[q])[i + e];
+    // every load of the four elements is issued before any arithmetic or store
+    long idx[4];
+    int ch[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        idx[e] = min(i + e, n - 1);
+        ch[e] = (int)(idx[e] / A.plane);
     }
-    for (int e = 0; e < m; ++e) {
-        const int c = (int)((i + e) / A.plane);
-        float x = fmaxf(v[e] * gp(A.scale)[c] + gp(A.shift)[c], 0.f);
-        if (A.res) x += gp(A.res)[i + e];
-        gp(A.out)[i + e] = x;
+    float part[4][4], sc[4], sh[4], rs[4];
+    const int np = A.nparts;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const LAMA_GLOBAL float *pq = gp(A.part[min(q, np - 1)]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[q][e] = pq[idx[e]];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        sc[e] = gp(A.scale)[ch[e]];
+        sh[e] = gp(A.shift)[ch[e]];
+    }
+    if (A.res) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rs[e] = gp(A.res)[idx[e]];
+    }
+    float out[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (q < np) v += part[q][e];
+        float x = fmaxf(v * sc[e] + sh[e], 0.f);
+        if (A.res) x += rs[e];
+        out[e] = x;
+    }
+    LAMA_GLOBAL float *o = gp(A.out);
+    if (i + 4 <= n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[i + e] = out[e];
+    } else {
+        for (int e = 0; e < (int)(n - i); ++e) o[i + e] = out[e];
     }
 }

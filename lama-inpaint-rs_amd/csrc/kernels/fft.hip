@@ -266,6 +266,18 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
     load_twiddles(A, twr, twc);
     const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
+    // the `f +` addend of the output is fetched now, its latency hidden by the transforms
+    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    const bool vec = (W & 3) == 0;
+    const int n4 = (H * W) >> 2;
+    constexpr int FP = 2;
+    float4 fpre[FP];
+#pragma unroll
+    for (int k = 0; k < FP; ++k) {
+        const int i4 = min((int)threadIdx.x + k * (int)blockDim.x, max(n4 - 1, 0));
+        fpre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (vec) fpre[k] = reinterpret_cast<const LAMA_GLOBAL float4 *>(f)[i4];
+    }
     for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) b0[idx] = make_float2(sre[idx], sim[idx]);
     __syncthreads();
     float2 *r = stockham(A.col, twc, b0, b1, Wh, 1, Wh, -A.col.sign_fwd);
@@ -293,13 +305,11 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     }
     __syncthreads();
     float2 *q = stockham(A.row, twr, o, r, HP, W, 1, -A.row.sign_fwd);
-    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
     LAMA_GLOBAL float *d = gp(A.out) + (long)c * H * W;
-    if ((W & 3) == 0) {
-        for (int i4 = threadIdx.x; i4 < (H * W) >> 2; i4 += blockDim.x) {
+    if (vec) {
+        auto emit = [&](int i4, float4 fv) {
             const int idx = i4 * 4, y = idx / W, x = idx - y * W;
             const float2 *v = q + (y >> 1) * W + x;
-            const float4 fv = *reinterpret_cast<const LAMA_GLOBAL float4 *>(f + idx);
             float4 o;
             if (y & 1)
                 o = make_float4(v[0].y, v[1].y, v[2].y, v[3].y);
@@ -310,7 +320,14 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
             o.z = o.z * A.scale + fv.z;
             o.w = o.w * A.scale + fv.w;
             *reinterpret_cast<LAMA_GLOBAL float4 *>(d + idx) = o;
+        };
+#pragma unroll
+        for (int k = 0; k < FP; ++k) {
+            const int i4 = threadIdx.x + k * blockDim.x;
+            if (i4 < n4) emit(i4, fpre[k]);
         }
+        for (int i4 = threadIdx.x + FP * blockDim.x; i4 < n4; i4 += blockDim.x)
+            emit(i4, reinterpret_cast<const LAMA_GLOBAL float4 *>(f)[i4]);
     } else {
         for (int idx = threadIdx.x; idx < H * W; idx += blockDim.x) {
             const int y = idx / W, x = idx - y * W;

@@ -5,7 +5,8 @@
 // is VALU work: a block covers 8 rows x 64 columns, each thread two adjacent
 // pixels x 3 channels (6 accumulators).  All 3 x Cin x 49 weights are staged
 // in LDS once (wave-uniform broadcast reads); per input channel the block
-// stages the reflect-padded 14 x 70 patch, one channel ahead.
+// stages the reflect-padded 14 x 70 patch, its global loads issued one
+// channel ahead so they overlap the current channel's FMAs.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -19,7 +20,8 @@ constexpr int PR = TROWS + 6, PC = TCOLS + 6;
 
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
 {
-    __shared__ float patch[2][PR * PC];
+    constexpr int PE = PR * PC, PK = (PE + LAMA_NT - 1) / LAMA_NT;  // patch elements per thread
+    __shared__ float patch[2][PE];
     __shared__ __attribute__((aligned(16))) float wl[3 * 64 * 49];
     const TailArgs &A = *args;
     const int H = A.H, W = A.W;
@@ -32,20 +34,48 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
 #pragma unroll
         for (int p = 0; p < PX; ++p) acc[co][p] = 0.f;
 
+    // this thread's patch elements: the same reflect-mapped offsets in every channel
     const long plane = (long)H * W;
-    auto stage = [&](int ci, float *dst) {
-        const float *src = A.src + (long)ci * plane;
-        for (int idx = threadIdx.x; idx < PR * PC; idx += LAMA_NT) {
-            const int r = idx / PC, c = idx - r * PC;
-            dst[idx] = gp(src)[(long)reflect1(oy0 - 3 + r, H) * W + reflect1(ox0 - 3 + c, W)];
-        }
+    long off[PK];
+#pragma unroll
+    for (int k = 0; k < PK; ++k) {
+        const int idx = min((int)threadIdx.x + k * LAMA_NT, PE - 1);
+        const int r = idx / PC, c = idx - r * PC;
+        off[k] = (long)reflect1(oy0 - 3 + r, H) * W + reflect1(ox0 - 3 + c, W);
+    }
+    const LAMA_GLOBAL float *src = gp(A.src);
+    float nxt[PK];
+    auto fetch = [&](int ci) {
+#pragma unroll
+        for (int k = 0; k < PK; ++k) nxt[k] = src[(long)ci * plane + off[k]];
     };
-    const int nw = 3 * A.Cin * 49;  // Cin <= 64
-    for (int i = threadIdx.x; i < nw; i += LAMA_NT) wl[i] = gp(A.wt)[i];
-    stage(0, patch[0]);
+    auto put = [&](float *dst) {
+#pragma unroll
+        for (int k = 0; k < PK; ++k)
+            if ((int)threadIdx.x + k * LAMA_NT < PE) dst[threadIdx.x + k * LAMA_NT] = nxt[k];
+    };
+
+    // weights (3 x Cin x 49 <= 9408 floats), four float4 loads in flight per round
+    {
+        const int nw = 3 * A.Cin * 49, n4 = nw >> 2;
+        const LAMA_GLOBAL float4 *w4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.wt));
+        fetch(0);
+        for (int b = threadIdx.x; b < n4; b += 4 * LAMA_NT) {
+            float4 wv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) wv[k] = w4[min(b + k * LAMA_NT, n4 - 1)];
+            // lanes past the end rewrite the last float4 with the same value
+#pragma unroll
+            for (int k = 0; k < 4; ++k) reinterpret_cast<float4 *>(wl)[min(b + k * LAMA_NT, n4 - 1)] = wv[k];
+        }
+        for (int i = 4 * n4 + threadIdx.x; i < nw; i += LAMA_NT) wl[i] = gp(A.wt)[i];
+    }
+    put(patch[0]);
+    // one barrier per channel: channel ci+1's loads are in flight during
+    // channel ci's FMAs and land in the other patch buffer afterwards
     for (int ci = 0; ci < A.Cin; ++ci) {
+        if (ci + 1 < A.Cin) fetch(ci + 1);
         __syncthreads();
-        if (ci + 1 < A.Cin) stage(ci + 1, patch[(ci + 1) & 1]);
         const float *pp = patch[ci & 1] + tr * PC + tc;
         const float *w0 = wl + ci * 49;
         const int wstride = A.Cin * 49;
@@ -64,16 +94,20 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
                 }
             }
         }
+        if (ci + 1 < A.Cin) put(patch[(ci + 1) & 1]);
     }
     const int oy = oy0 + tr;
     if (oy >= H) return;
+    float bias[3];
+#pragma unroll
+    for (int co = 0; co < 3; ++co) bias[co] = gp(A.bias)[co];
 #pragma unroll
     for (int co = 0; co < 3; ++co)
 #pragma unroll
         for (int p = 0; p < PX; ++p) {
             const int ox = ox0 + tc + p;
             if (ox < W) {
-                const float v = acc[co][p] + gp(A.bias)[co];
+                const float v = acc[co][p] + bias[co];
                 gp(A.out)[co * plane + (long)oy * W + ox] = 1.0f / (1.0f + expf(-v));
             }
         }
