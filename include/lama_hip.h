@@ -83,6 +83,12 @@ int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, 
                           double *ms, double *flops, double *bytes);
 /* print_stats (cuda.rs:1785-1806): a summary to stderr. */
 void lama_hip_print_stats(lama_hip_ctx *ctx);
+/* Device memory one forward at h x w needs, for the --gpu capacity guard
+ * (the role of mem.rs:26-36 estimated_bytes, exact for this engine): the
+ * activation arena of that shape, from its layout, and the resident weights
+ * (0 before lama_hip_load_weights).  h, w multiples of 8. */
+int lama_hip_plan_bytes(lama_hip_ctx *ctx, int h, int w, uint64_t *arena_bytes, uint64_t *weight_bytes,
+                        char *err, size_t errlen);
 /* Launches per forward at h x w (after a plan exists for that shape). */
 int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w);
 

@@ -139,6 +139,18 @@ extern "C" void lama_hip_print_stats(lama_hip_ctx *ctx)
     }
 }
 
+extern "C" int lama_hip_plan_bytes(lama_hip_ctx *ctx, int h, int w, uint64_t *arena_bytes, uint64_t *weight_bytes,
+                                   char *err, size_t errlen)
+{
+    GUARD(([&] {
+        uint64_t a = 0, wb = 0;
+        if (!ctx->eng.plan_bytes(h, w, a, wb, e_)) return false;
+        if (arena_bytes) *arena_bytes = a;
+        if (weight_bytes) *weight_bytes = wb;
+        return true;
+    })());
+}
+
 extern "C" int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w) { return ctx->eng.launch_count(h, w); }
 
 extern "C" int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size_t errlen)

@@ -325,6 +325,7 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
         warena_ = nullptr;
     }
     if (!check(hip_->hipMalloc((void **)&warena_, A.h.size() * 4), "hipMalloc(weights)", err)) return false;
+    warena_bytes_ = A.h.size() * 4;
     if (!check(hip_->hipMemcpy(warena_, A.h.data(), A.h.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(weights)",
                err))
         return false;
@@ -457,6 +458,62 @@ Plan *Engine::plan_for(int h, int w, std::string &err)
     return &(plans_[key] = p);
 }
 
+// Byte offsets of every buffer of the per-shape activation arena (each
+// 256-byte aligned) and its total size.
+size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, ArenaLayout &L)
+{
+    const size_t P = (size_t)H * W, P2 = (size_t)(H / 2) * (W / 2), P4 = (size_t)(H / 4) * (W / 4);
+    const size_t P8 = (size_t)(H / 8) * (W / 8), PS = (size_t)(H / 8) * ((W / 8) / 2 + 1);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off = (off + bytes + 255) / 256 * 256;
+        return o;
+    };
+    L.in = take(4 * P * 4);
+    L.a1 = take(64 * P * 4);
+    L.a2 = take(128 * P2 * 4);
+    L.a3 = take(256 * P4 * 4);
+    L.x = take(512 * P8 * 4);
+    L.y = take(512 * P8 * 4);
+    L.f = take(192 * P8 * 4);
+    L.g = take(192 * P8 * 4);
+    L.s = take(384 * PS * 4);
+    L.s2 = take(384 * PS * 4);
+    L.out = take(3 * P * 4);
+    L.gc = take(384 * P8 * 4);
+    L.lq = take(4 * 128 * P8 * 4);  // the FFC local GEMM's four K-quarter partials
+    L.tmp = take(fg.split ? fg.tmp_bytes : 0);
+    L.twr = take(ntwr * 4);
+    L.twc = take(ntwc * 4);
+    const size_t n_conv = 4 + 36 * 7 + 4 * 3;      // problems
+    const size_t n_puts = 4 + 36 * 2 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
+    L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
+    return off;
+}
+
+bool Engine::plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::string &err)
+{
+    if (h < 8 || w < 8 || h % 8 || w % 8) {
+        err = "input size must be a multiple of 8 and at least 8";
+        return false;
+    }
+    auto it = plans_.find({h, w});
+    weights = warena_bytes_;
+    if (it != plans_.end()) {
+        arena = it->second.arena_bytes;
+        return true;
+    }
+    FftLen fr, fc;
+    std::vector<float> twr, twc;
+    FftGeom fg;
+    if (!fft_len(w / 8, fr, twr, err) || !fft_len(h / 8, fc, twc, err) || !fft_geom(192, h / 8, w / 8, fg, err))
+        return false;
+    ArenaLayout lay;
+    arena = arena_layout(h, w, fg, twr.size(), twc.size(), lay);
+    return true;
+}
+
 bool Engine::build_plan(Plan &p, std::string &err)
 {
     const int H = p.H, W = p.W, H2 = H / 2, W2 = W / 2, H4 = H / 4, W4 = W / 4, H8 = H / 8, W8 = W / 8;
@@ -470,26 +527,11 @@ bool Engine::build_plan(Plan &p, std::string &err)
     FftGeom fg;
     if (!fft_geom(192, H8, W8, fg, err)) return false;
 
-    // arena layout
-    size_t off = 0;
-    auto take = [&](size_t bytes) {
-        size_t o = off;
-        off = (off + bytes + 255) / 256 * 256;
-        return o;
-    };
-    const size_t o_in = take(4 * P * 4), o_a1 = take(64 * P * 4), o_a2 = take(128 * P2 * 4), o_a3 = take(256 * P4 * 4);
-    const size_t o_x = take(512 * P8 * 4), o_y = take(512 * P8 * 4), o_f = take(192 * P8 * 4), o_g = take(192 * P8 * 4);
-    const size_t o_s = take(384 * PS * 4), o_s2 = take(384 * PS * 4), o_out = take(3 * P * 4);
-    const size_t o_gc = take(384 * P8 * 4);
-    // the FFC local GEMM runs as four K quarters with raw partial outputs
-    const size_t o_lq = take(4 * 128 * P8 * 4);
-    const size_t o_tmp = take(fg.split ? fg.tmp_bytes : 0);
-
-    const size_t o_twr = take(twr.size() * 4), o_twc = take(twc.size() * 4);
-    const size_t n_conv = 4 + 36 * 7 + 4 * 3;  // problems
-    const size_t n_puts = 4 + 36 * 2 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
-    const size_t o_desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
-    p.arena_bytes = off;
+    ArenaLayout lay;
+    p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), lay);
+    const size_t o_in = lay.in, o_a1 = lay.a1, o_a2 = lay.a2, o_a3 = lay.a3, o_x = lay.x, o_y = lay.y, o_f = lay.f,
+                 o_g = lay.g, o_s = lay.s, o_s2 = lay.s2, o_out = lay.out, o_gc = lay.gc, o_lq = lay.lq, o_tmp = lay.tmp,
+                 o_twr = lay.twr, o_twc = lay.twc, o_desc = lay.desc;
     if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
     char *base = (char *)p.arena;
     auto F = [&](size_t o) { return (float *)(base + o); };

@@ -58,6 +58,10 @@ struct FftGeom {
     size_t tmp_bytes = 0;           // interleaved complex [C][H][W/2+1]
 };
 
+struct ArenaLayout {
+    size_t in, a1, a2, a3, x, y, f, g, s, s2, out, gc, lq, tmp, twr, twc, desc;
+};
+
 struct Plan {
     int H = 0, W = 0;
     void *arena = nullptr;
@@ -82,6 +86,9 @@ public:
     void profile_reset();
     bool profile_read(int i, std::string &name, uint64_t &launches, double &ms, double &flops, double &bytes);
     int launch_count(int h, int w);
+    // Device bytes of one forward at h x w: the activation arena of that shape
+    // (exact, from its layout) and the resident weights (0 before loading).
+    bool plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::string &err);
 
     // single kernel families (parity tests)
     bool op_conv2d(const float *x, int cin, int h, int w, const float *wt, const float *bias, int cout, int k,
@@ -111,6 +118,7 @@ private:
     bool build_plan(Plan &p, std::string &err);
     bool run(Plan &p, hipStream_t s, float *const *steps, std::string &err);
     bool replay(Plan &p, hipStream_t s, std::string &err);
+    static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, ArenaLayout &L);
     bool use_graph() const;
     void free_plan(Plan &p);
     bool launch(const Launch &L, hipStream_t s, std::string &err);
@@ -137,6 +145,7 @@ private:
     FfcW ffc_[36];
     UpW up_[3];
     size_t tail_w_ = 0, tail_b_ = 0;
+    size_t warena_bytes_ = 0;
     const float *wp(size_t off) const { return warena_ + off; }
 
     std::map<std::pair<int, int>, Plan> plans_;

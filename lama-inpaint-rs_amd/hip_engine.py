@@ -45,6 +45,8 @@ def lib():
                                             ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_print_stats.argtypes = [vp]
         L.lama_hip_launch_count.argtypes = [vp, ctypes.c_int, ctypes.c_int]
+        L.lama_hip_plan_bytes.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
+                                          ctypes.POINTER(ctypes.c_uint64), cp, sz]
         L.lama_hip_malloc.argtypes = [vp, sz, ctypes.POINTER(vp), cp, sz]
         L.lama_hip_free.argtypes = [vp, vp]
         L.lama_hip_memcpy.argtypes = [vp, vp, vp, sz, ctypes.c_int, cp, sz]
@@ -178,6 +180,12 @@ class Engine:
 
     def launch_count(self, h, w):
         return lib().lama_hip_launch_count(self.ctx, h, w)
+
+    def plan_bytes(self, h, w):
+        """(activation arena bytes at h x w, resident weight bytes)."""
+        a, wb = ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(lib().lama_hip_plan_bytes(self.ctx, h, w, ctypes.byref(a), ctypes.byref(wb), self._err, 4096))
+        return a.value, wb.value
 
     # single kernel families (parity tests)
     def op_conv2d(self, x, wt, bias=None, stride=1, scale=None, shift=None, relu=False):

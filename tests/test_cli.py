@@ -1,0 +1,211 @@
+"""The lama-inpaint command line (lama-inpaint-rs_amd/bin/lama-inpaint), the
+reference's CLI (lama-rs/src/main.rs:49-566) over the MI355X engine.
+
+CPU tests cover argument handling and the error policy (no CPU engine in
+this build, so --cpu and a failed GPU are errors with a message).  GPU tests
+run the whole-image, --tile and --sections flows end to end and compare them
+bit for bit with the same flows restated in Python over the engine
+(main.rs:213-313, 378-443, 465-566) -- including the reference's own claim
+that --tile equals cropping the window out, running it and pasting the hole
+back -- and the whole-image output with the CPU oracle."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "lama-inpaint-rs_amd", "bin", "lama-inpaint")
+
+
+def run_cli(*args, stdin=None, timeout=300):
+    return subprocess.run([CLI, *args], capture_output=True, timeout=timeout, input=stdin)
+
+
+@pytest.fixture(scope="module")
+def H(pkg):
+    return pkg.host_api
+
+
+def write_case(H, d, img, mask):
+    ip, mp = os.path.join(d, "in.png"), os.path.join(d, "mask.png")
+    H.png_write_rgb(ip, img)
+    H.png_write_rgb(mp, np.repeat(mask[..., None], 3, -1))
+    return ip, mp
+
+
+# ------------------------------------------------------------------ CPU
+
+def test_help_and_usage_errors():
+    r = run_cli("--help")
+    assert r.returncode == 0 and b"usage: lama-inpaint" in r.stdout
+    for args, msg in [((), b"--image is required"), (("--image", "a"), b"--mask is required"),
+                      (("--image", "a", "--mask", "b"), b"--output is required"),
+                      (("--bogus",), b"unknown argument --bogus"), (("--image",), b"--image needs a value"),
+                      (("--image", "-", "--mask", "-", "--output", "o"), b"cannot both be '-'"),
+                      (("--image", "a", "--mask", "b", "--output", "o", "--tile", "--sections"),
+                       b"mutually exclusive")]:
+        r = run_cli(*args)
+        assert r.returncode == 2, args
+        assert msg in r.stderr and b"usage:" in r.stderr, (args, r.stderr)
+
+
+def test_input_errors(H, tmp_path):
+    img = H.synth_image(24, 32, 1)
+    ip = str(tmp_path / "i.png")
+    H.png_write_rgb(ip, img)
+    mp = str(tmp_path / "m.png")
+    H.png_write_rgb(mp, np.zeros((16, 32, 3), np.uint8))
+    r = run_cli("--image", ip, "--mask", mp, "--output", str(tmp_path / "o.png"))
+    assert r.returncode == 1 and b"mask is 32x16 but image is 32x24" in r.stderr
+    r = run_cli("--image", str(tmp_path / "nope.png"), "--mask", mp, "--output", str(tmp_path / "o.png"))
+    assert r.returncode == 1 and b"error:" in r.stderr
+    H.png_write_rgb(mp, np.zeros((24, 32, 3), np.uint8))
+    r = run_cli("--image", ip, "--mask", mp, "--output", str(tmp_path / "o.png"), "--weights", "/nonexistent.st")
+    assert r.returncode == 1 and b"/nonexistent.st" in r.stderr
+
+
+def test_cpu_flag_is_refused_without_fallback(H, tmp_path, weights_dir):
+    img = H.synth_image(24, 32, 1)
+    mask, _ = H.synth_mask_rect(24, 32, 8, 8, 2)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    r = run_cli("--image", ip, "--mask", mp, "--output", str(tmp_path / "o.png"), "--weights", weights_dir["plain"],
+                "--cpu")
+    assert r.returncode == 1 and b"no CPU engine" in r.stderr
+    assert not (tmp_path / "o.png").exists()
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd") and os.access("/dev/kfd", os.R_OK | os.W_OK),
+                    reason="a GPU is present")
+def test_gpu_failure_is_an_error_not_a_fallback(H, tmp_path, weights_dir):
+    img = H.synth_image(24, 32, 1)
+    mask, _ = H.synth_mask_rect(24, 32, 8, 8, 2)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    r = run_cli("--image", ip, "--mask", mp, "--output", str(tmp_path / "o.png"), "--weights", weights_dir["plain"])
+    assert r.returncode == 1 and b"gpu unavailable" in r.stderr and b"no CPU engine" in r.stderr
+    r = run_cli("--image", ip, "--mask", mp, "--output", str(tmp_path / "o.png"), "--weights", weights_dir["plain"],
+                "--gpu")
+    assert r.returncode == 1 and b"gpu inference failed" in r.stderr
+
+
+def test_empty_mask_tile_and_sections_copy_the_input(H, tmp_path, weights_dir):
+    # main.rs:393-398, 486-490: an empty mask needs no network at all
+    img = H.synth_image(600, 640, 3)
+    ip, mp = write_case(H, str(tmp_path), img, np.zeros((600, 640), np.uint8))
+    for flag in ("--tile", "--sections"):
+        out = str(tmp_path / f"o{flag}.png")
+        r = run_cli("--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["plain"], flag)
+        assert r.returncode == 0, r.stderr
+        assert b"mask is empty" in r.stderr
+        assert np.array_equal(H.png_read_rgb(out), img)
+
+
+# ------------------------------------------------------------------ GPU
+
+def _tile_by_hand(H, engine, img, mask):
+    t = H.tile_rect(mask)
+    s = t.side
+    sub, sm = img[t.y0:t.y0 + s, t.x0:t.x0 + s], mask[t.y0:t.y0 + s, t.x0:t.x0 + s]
+    pad = (8 - s % 8) % 8
+    out = engine.forward(H.build_input(sub, sm, pad, pad))
+    res = img.copy()
+    u8 = H.composite(sub, sm, out, pad, pad)
+    hole = sm > 0
+    res[t.y0:t.y0 + s, t.x0:t.x0 + s][hole] = u8[hole]
+    return res
+
+
+def _sections_by_hand(H, engine, img, mask):
+    h, w = mask.shape
+    side = max(1, min(512, w, h))
+    pad = (8 - side % 8) % 8
+    work = img.copy()
+    for x0, y0, x1, y1 in H.section_rects(mask):
+        wx = H.window_origin((x0 + x1) // 2, side, w)
+        wy = H.window_origin((y0 + y1) // 2, side, h)
+        sub = work[wy:wy + side, wx:wx + side]
+        sm = mask[wy:wy + side, wx:wx + side].copy()
+        own = np.zeros_like(sm, bool)
+        own[y0 - wy:y1 - wy, x0 - wx:x1 - wx] = True
+        sm[~own] = 0
+        out = engine.forward(H.build_input(sub, sm, pad, pad))
+        u8 = H.composite(sub, sm, out, pad, pad)
+        # the section's own hole pixels, which lie inside the window
+        sel = np.zeros((h, w), bool)
+        sel[y0:y1, x0:x1] = mask[y0:y1, x0:x1] > 0
+        work[sel] = u8[sel[wy:wy + side, wx:wx + side]]
+    return work
+
+
+@pytest.mark.gpu
+def test_cli_whole_image_matches_engine_and_oracle(H, engine, tmp_path, weights_dir):
+    import oracle_api as O
+    img = H.synth_image(76, 100, 1)  # pads to 80 x 104
+    mask, _ = H.synth_mask_rect(76, 100, 30, 20, 2)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    out = str(tmp_path / "o.png")
+    r = run_cli("--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["cal"], "--gpu")
+    assert r.returncode == 0, r.stderr
+    got = H.png_read_rgb(out)
+    x = H.build_input(img, mask)
+    want = H.composite(img, mask, engine.forward(x), 4, 4)
+    assert np.array_equal(got, want)
+    ref = H.composite(img, mask, O.OracleNet(O.read_safetensors(weights_dir["cal"])).forward(x), 4, 4)
+    d = np.abs(got.astype(int) - ref.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1
+    assert np.array_equal(got[mask == 0], img[mask == 0])
+
+
+@pytest.mark.gpu
+def test_cli_tile_equals_crop_run_paste(H, engine, tmp_path, weights_dir):
+    img = H.synth_image(900, 1100, 4)
+    mask, _ = H.synth_mask_rect(900, 1100, 120, 90, 5)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    out = str(tmp_path / "o.png")
+    r = run_cli("--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["cal"], "--tile")
+    assert r.returncode == 0, r.stderr
+    assert b"tile: 512x512 window" in r.stderr
+    assert np.array_equal(H.png_read_rgb(out), _tile_by_hand(H, engine, img, mask))
+
+
+@pytest.mark.gpu
+def test_cli_sections_equal_the_restated_pass_loop(H, engine, tmp_path, weights_dir):
+    img = H.synth_image(1000, 1100, 6)
+    mask = np.zeros((1000, 1100), np.uint8)
+    mask[200:800, 300:900] = 255  # 600 x 600 -> 3 x 3 sections
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    out = str(tmp_path / "o.png")
+    dump = tmp_path / "dump"
+    dump.mkdir()
+    env = dict(os.environ, LAMA_DUMP_SECTIONS=str(dump))
+    r = subprocess.run([CLI, "--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["cal"],
+                        "--sections"], capture_output=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr
+    assert b"sections: 9 passes, 512x512 window each" in r.stderr
+    got = H.png_read_rgb(out)
+    assert np.array_equal(got, _sections_by_hand(H, engine, img, mask))
+    assert np.array_equal(got[mask == 0], img[mask == 0])
+    assert len(list(dump.iterdir())) == 9
+
+
+@pytest.mark.gpu
+def test_cli_stdin_stdout(H, tmp_path, weights_dir):
+    img = H.synth_image(64, 72, 7)
+    mask, _ = H.synth_mask_rect(64, 72, 20, 12, 8)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    a = run_cli("--image", "-", "--mask", mp, "--output", "-", "--weights", weights_dir["cal"],
+                stdin=open(ip, "rb").read())
+    assert a.returncode == 0, a.stderr
+    b_out = str(tmp_path / "b.png")
+    b = run_cli("--image", ip, "--mask", mp, "--output", b_out, "--weights", weights_dir["cal"])
+    assert b.returncode == 0
+    assert a.stdout == open(b_out, "rb").read()
+
+
+@pytest.mark.gpu
+def test_plan_bytes_is_the_allocated_arena(pkg, engine):
+    x = np.zeros((4, 136, 200), np.float32)
+    predicted, weights = engine.plan_bytes(136, 200)
+    engine.forward(x)
+    actual, _ = engine.plan_bytes(136, 200)
+    assert predicted == actual > 0 and weights > 200e6
