@@ -4,6 +4,14 @@
 #pragma once
 #include <hip/hip_runtime_api.h>
 
+// AMD extension launch (hip_ext.h, which needs the device-side headers): the
+// start/stop events are recorded by the dispatch packet itself.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void **kernelParams, void **extra,
+                                               hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
+
 #include <string>
 
 namespace lama {

@@ -164,3 +164,22 @@ def test_graph_replays_match_eager(pkg, engine, monkeypatch):
     eng1.free(d_in)
     eng1.free(d_out)
     eng1.close()
+
+
+def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal):
+    """configs[4]'s --tile window: 600 x 600 (75 x 75 bottleneck, FFT lengths
+    75 and 38 through the reference's opposite-sign rule) against the oracle,
+    every step."""
+    img, mask = _case(pkg, 600, 600, "rect")
+    x = pkg.host_api.build_input(img, mask)
+    print("case 600x600 rect", flush=True)
+    got, got_steps = engine.forward_steps(x, list(range(29)))
+    ref, ref_steps = oracle_cal.forward(x, steps=True)
+    for s in range(29):
+        e = rel_err(got_steps[s], ref_steps[s])
+        assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+    u8g = pkg.host_api.composite(img, mask, got, 0, 0)
+    u8r = pkg.host_api.composite(img, mask, ref, 0, 0)
+    d = np.abs(u8g.astype(int) - u8r.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
+    assert np.array_equal(u8g[mask == 0], img[mask == 0])
