@@ -80,12 +80,15 @@ def main():
         eng.forward_device(d_in, S, S, d_out)
     eng.synchronize()
 
+    # The dominant kernel is timed with HIP events on its own stream during the
+    # timed region, on every fourth pass (the events ride in the dispatch
+    # packets; sampling keeps their cost out of `value`).
     dom = "conv3x3"
-    eng.profile([dom])
     eng.profile_reset()
     eng.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        eng.profile([dom] if i % 4 == 0 else ())
         eng.forward_device(d_in, S, S, d_out)
     eng.synchronize()
     elapsed = time.perf_counter() - t0
