@@ -481,13 +481,13 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.s = take(384 * PS * 4);
     L.s2 = take(384 * PS * 4);
     L.out = take(3 * P * 4);
-    L.gc = take(384 * P8 * 4);
+    L.gc = take(2 * 384 * P8 * 4);  // the l2g partial, double-buffered by FFC parity
     L.lq = take(4 * 128 * P8 * 4);  // the FFC local GEMM's four K-quarter partials
     L.tmp = take(fg.split ? fg.tmp_bytes : 0);
     L.twr = take(ntwr * 4);
     L.twc = take(ntwc * 4);
-    const size_t n_conv = 4 + 36 * 7 + 4 * 3;      // problems
-    const size_t n_puts = 4 + 36 * 2 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
+    const size_t n_conv = 4 + 36 * 8 + 4 * 3;      // problems
+    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
     L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
     return off;
 }
@@ -643,76 +643,103 @@ bool Engine::build_plan(Plan &p, std::string &err)
     void *d_irfft = put(&fa, sizeof fa);
 
     // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual).
-    // Main stream: one grouped launch of the local GEMM, BN_l(l2l(x_l) +
-    // g2l(x_g)), and the raw l2g(x_l) partial.  Side stream, concurrently: the
-    // SpectralTransform chain, then conv2(f + ifft) whose epilogue adds the
-    // l2g partial before BN_g.  The next FFC's main launch waits for the side
-    // stream (its input's global half); the side stream's conv2 waits for the
-    // main launch (the partial).
-    for (int r = 0; r < 18; ++r)
-        for (int s = 0; s < 2; ++s) {
-            const int k = r * 2 + s;
-            const FfcW &Fw = ffc_[k];
-            float *src = s == 0 ? X : Y, *dst = s == 0 ? Y : X;
-            const float *res = s == 0 ? nullptr : X;
-            const int step = s == 1 ? 5 + r : -1;
-            // local: four K quarters (input channels 128q..128q+127), raw partials
-            std::vector<ConvProblem> probs;
-            for (int q = 0; q < 4; ++q) {
-                ConvSeg sq = seg(src + (size_t)128 * q * P8, Fw.local, 128, H8, W8);
-                sq.wt = wp(Fw.local.off) + (size_t)q * 16 * 72;  // chunks 16q.. of the packed rows
-                sq.nchunk = 16;
-                ConvProblem pq = problem(F_CONV3, sq, 128, H8, W8, 0, 0, LQ + (size_t)q * 128 * P8, P8, W8, nullptr);
-                pq.scale = pq.shift = nullptr;
-                pq.relu = 0;
-                probs.push_back(pq);
-            }
-            ConvProblem qg = problem(F_CONV3, seg(src, Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, GC, P8, W8, nullptr);
-            qg.scale = qg.shift = nullptr;
-            qg.relu = 0;
-            probs.push_back(qg);
-            const double fl = 2.0 * P8 * (128.0 * 512 * 9 + 384.0 * 128 * 9);
-            const double by = f4 * (512 * P8 + 4 * 128 * P8 + 384 * P8 + 128 * 512 * 9 + 384 * 128 * 9);
-            conv_launch(F_CONV3, probs, -1, fl, by, S_MAIN, k == 0 ? -1 : EV_SIDE, EV_MAIN);
-            {
-                FinalizeArgs fa2{};
-                for (int q = 0; q < 4; ++q) fa2.part[q] = LQ + (size_t)q * 128 * P8;
-                fa2.nparts = 4;
-                fa2.C = 128;
-                fa2.plane = (long)P8;
-                fa2.scale = wp(Fw.bn_l);
-                fa2.shift = wp(Fw.bn_l + 128);
-                fa2.res = res;
-                fa2.out = dst;
-                Launch L{};
-                L.fn = fn_[F_FINAL];
-                L.family = F_FINAL;
-                L.stream = S_MAIN;
-                L.wait_ev = L.record_ev = -1;
-                L.grid = (unsigned)(((128 * P8 + 3) / 4 + LAMA_NT - 1) / LAMA_NT);
-                L.arg = put(&fa2, sizeof fa2);
-                L.nparams = 1;
-                L.step_end = -1;
-                L.bytes = f4 * 128 * P8 * (4 + 1 + (res ? 1 : 0));
-                p.launches.push_back(L);
-            }
-            // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
-            conv_launch(F_CONV1,
-                        {problem(F_CONV1, seg(src + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1, 192, Fb, P8, (int)P8, nullptr)},
-                        -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384), S_SIDE, k == 0 ? EV_FORK : -1);
-            push_fft(p, false, fg, d_rfft, S_SIDE, f4 * 192 * P8, 8.0 * 192 * PS);
-            // FourierUnit conv over the stacked spectrum + BN + ReLU
-            conv_launch(F_CONV1,
-                        {problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS, (int)PS, nullptr)},
-                        -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384), S_SIDE);
-            push_fft(p, true, fg, d_irfft, S_SIDE, 8.0 * 192 * PS, 2 * f4 * 192 * P8);  // + the fused feat read
-            // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
-            ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
-                                     dst + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
-            q2.addend = GC;
-            conv_launch(F_CONV1R, {q2}, step, 2.0 * 192 * 384 * P8,
-                        f4 * (192 * P8 + 384 * P8 * (res ? 3 : 2) + 384 * 192), S_SIDE, EV_MAIN, EV_SIDE);
-        }
+    // FFC k's 3x3 convolutions run on the main stream as two grouped launches:
+    //   A(k): the l2l K quarter (input x_l) and l2g (raw, into GC[k % 2]);
+    //   B(k): the three g2l K quarters (input x_g);
+    // then the local finalize.  The side stream runs the SpectralTransform
+    // chain and conv2, whose epilogue adds GC[k % 2] before BN_g.  A(k+1)
+    // needs only x_l(k+1), the main stream's own finalize output, so it is
+    // issued right after finalize(k) and overlaps conv2(k); only B(k+1) waits
+    // for the side stream (x_g(k+1) from conv2(k)), and conv2(k) waits for
+    // A(k), which finished long before.
+    auto ffc_src = [&](int k) { return k % 2 == 0 ? X : Y; };
+    auto ffc_dst = [&](int k) { return k % 2 == 0 ? Y : X; };
+    auto ffc_res = [&](int k) -> const float * { return k % 2 == 0 ? nullptr : X; };
+    auto gc_buf = [&](int k) { return GC + (size_t)(k % 2) * 384 * P8; };
+    auto raw = [](ConvProblem q) {
+        q.scale = q.shift = nullptr;
+        q.relu = 0;
+        return q;
+    };
+    // local K quarter q of FFC k (input channels 128q..128q+127), raw partial
+    auto quarter = [&](int k, int q) {
+        const FfcW &Fw = ffc_[k];
+        ConvSeg sq = seg(ffc_src(k) + (size_t)128 * q * P8, Fw.local, 128, H8, W8);
+        sq.wt = wp(Fw.local.off) + (size_t)q * 16 * 72;  // chunks 16q.. of the packed rows
+        sq.nchunk = 16;
+        return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, LQ + (size_t)q * 128 * P8, P8, W8, nullptr));
+    };
+    auto launch_a = [&](int k) {
+        const FfcW &Fw = ffc_[k];
+        std::vector<ConvProblem> probs{
+            quarter(k, 0), raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8,
+                                       W8, nullptr))};
+        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
+                    f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
+                    k % 2 ? EV_A1 : EV_A0);
+    };
+    auto launch_b = [&](int k) {
+        std::vector<ConvProblem> probs{quarter(k, 1), quarter(k, 2), quarter(k, 3)};
+        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9), f4 * (384 * P8 + 3 * 128 * P8 + 128 * 384 * 9),
+                    S_MAIN, k == 0 ? -1 : ((k - 1) % 2 ? EV_S1 : EV_S0));
+    };
+    auto launch_finalize = [&](int k) {
+        const FfcW &Fw = ffc_[k];
+        FinalizeArgs fa2{};
+        for (int q = 0; q < 4; ++q) fa2.part[q] = LQ + (size_t)q * 128 * P8;
+        fa2.nparts = 4;
+        fa2.C = 128;
+        fa2.plane = (long)P8;
+        fa2.scale = wp(Fw.bn_l);
+        fa2.shift = wp(Fw.bn_l + 128);
+        fa2.res = ffc_res(k);
+        fa2.out = ffc_dst(k);
+        Launch L{};
+        L.fn = fn_[F_FINAL];
+        L.family = F_FINAL;
+        L.stream = S_MAIN;
+        L.wait_ev = L.record_ev = -1;
+        L.grid = (unsigned)(((128 * P8 + 3) / 4 + LAMA_NT - 1) / LAMA_NT);
+        L.arg = put(&fa2, sizeof fa2);
+        L.nparams = 1;
+        L.step_end = -1;
+        L.bytes = f4 * 128 * P8 * (4 + 1 + (fa2.res ? 1 : 0));
+        p.launches.push_back(L);
+    };
+    auto launch_spectral = [&](int k) {
+        const FfcW &Fw = ffc_[k];
+        // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
+        conv_launch(F_CONV1,
+                    {problem(F_CONV1, seg(ffc_src(k) + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1,
+                             192, Fb, P8, (int)P8, nullptr)},
+                    -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384), S_SIDE, k == 0 ? EV_FORK : -1);
+        push_fft(p, false, fg, d_rfft, S_SIDE, f4 * 192 * P8, 8.0 * 192 * PS);
+        // FourierUnit conv over the stacked spectrum + BN + ReLU
+        conv_launch(F_CONV1,
+                    {problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS, (int)PS,
+                             nullptr)},
+                    -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384), S_SIDE);
+        push_fft(p, true, fg, d_irfft, S_SIDE, 8.0 * 192 * PS, 2 * f4 * 192 * P8);  // + the fused feat read
+    };
+    auto launch_conv2 = [&](int k) {
+        const FfcW &Fw = ffc_[k];
+        const float *res = ffc_res(k);
+        // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
+        ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
+                                 ffc_dst(k) + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
+        q2.addend = gc_buf(k);
+        conv_launch(F_CONV1R, {q2}, k % 2 == 1 ? 5 + k / 2 : -1, 2.0 * 192 * 384 * P8,
+                    f4 * (192 * P8 + 384 * P8 * (res ? 3 : 2) + 384 * 192), S_SIDE, k % 2 ? EV_A1 : EV_A0,
+                    k % 2 ? EV_S1 : EV_S0);
+    };
+    launch_a(0);
+    for (int k = 0; k < 36; ++k) {
+        launch_spectral(k);
+        launch_b(k);
+        launch_finalize(k);
+        if (k + 1 < 36) launch_a(k + 1);
+        launch_conv2(k);
+    }
     // step 23 (concat) is the same buffer as step 22; steps 24-26 the upsamplers
     const float *usrc[3] = {X, a3, a2};
     float *udst[3] = {a3, a2, a1};
@@ -732,7 +759,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         }
         const double pin = (double)uh[u] * uw[u];
         conv_launch(F_CONVT, ph, 24 + u, 2.0 * U.cin * U.cout * 9 * pin,
-                    f4 * (U.cin * pin + U.cout * 4 * pin + U.cin * U.cout * 9), S_MAIN, u == 0 ? EV_SIDE : -1);
+                    f4 * (U.cin * pin + U.cout * 4 * pin + U.cin * U.cout * 9), S_MAIN, u == 0 ? EV_S1 : -1);
     }
     // step 28: model.34 + sigmoid (ReflectionPad2d(3) folded into the indexing)
     TailArgs ta{};

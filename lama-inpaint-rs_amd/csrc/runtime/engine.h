@@ -30,7 +30,10 @@ struct Packed {
 // carries the SpectralTransform chain of every FFC concurrently with the
 // FFC's spatial GEMM.  Cross-stream order is kept with the engine's events.
 enum { S_MAIN = 0, S_SIDE = 1 };
-enum { EV_FORK = 0, EV_MAIN = 1, EV_SIDE = 2, EV_COUNT = 3 };
+// EV_FORK: model.4 done (the side stream's first input); EV_A0/1: FFC k's
+// l2l + l2g launch done (its GC partial), by parity of k; EV_S0/1: FFC k's
+// conv2 done (its global output half), by parity of k.
+enum { EV_FORK = 0, EV_A0 = 1, EV_A1 = 2, EV_S0 = 3, EV_S1 = 4, EV_COUNT = 5 };
 
 struct Launch {
     hipFunction_t fn;

@@ -74,9 +74,9 @@ def test_forward_repeatable_and_shapes(pkg, engine):
     b = engine.forward(x)
     assert a.shape == (3, 64, 128)
     assert np.array_equal(a, b)
-    # head, 3 downsamplers, 36 FFCs x (grouped GEMM, finalize, conv1, rfft2, FU conv, irfft2, conv2),
+    # head, 3 downsamplers, 36 FFCs x (2 grouped GEMMs, finalize, conv1, rfft2, FU conv, irfft2, conv2),
     # 3 upsamplers, tail
-    assert engine.launch_count(64, 128) == 1 + 3 + 36 * 7 + 3 + 1
+    assert engine.launch_count(64, 128) == 1 + 3 + 36 * 8 + 3 + 1
 
 
 def test_forward_split_fft_1024(pkg, engine, oracle_cal):
@@ -87,7 +87,7 @@ def test_forward_split_fft_1024(pkg, engine, oracle_cal):
     x = pkg.host_api.build_input(img, mask)
     print(f"case {h}x{w} strokes (split FFT)", flush=True)
     got, got_steps = engine.forward_steps(x, list(range(29)))
-    assert engine.launch_count(h, w) == 1 + 3 + 36 * 9 + 3 + 1
+    assert engine.launch_count(h, w) == 1 + 3 + 36 * 10 + 3 + 1
     ref, ref_steps = oracle_cal.forward(x, steps=True)
     for s in range(29):
         e = rel_err(got_steps[s], ref_steps[s])
@@ -108,7 +108,7 @@ def test_forward_split_forced_matches_single(pkg, engine, monkeypatch):
     eng2 = pkg.hip_engine.Engine()
     eng2.load_weights(engine._store)
     b = eng2.forward(x)
-    assert eng2.launch_count(128, 96) == 1 + 3 + 36 * 9 + 3 + 1
+    assert eng2.launch_count(128, 96) == 1 + 3 + 36 * 10 + 3 + 1
     eng2.close()
     assert rel_err(b, a) < 1e-5
 
@@ -130,7 +130,7 @@ def test_forward_2048_whole_image(pkg, engine):
     u8 = H.composite(img, mask, a, 0, 0)
     keep = mask == 0
     assert np.array_equal(u8[keep], img[keep])
-    assert engine.launch_count(h, w) == 1 + 3 + 36 * 9 + 3 + 1
+    assert engine.launch_count(h, w) == 1 + 3 + 36 * 10 + 3 + 1
 
 
 def test_graph_replays_match_eager(pkg, engine, monkeypatch):
