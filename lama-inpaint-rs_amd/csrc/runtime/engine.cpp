@@ -811,7 +811,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
     return check(hip_->hipMemcpy((void *)fcol.tw, twc.data(), twc.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err);
 }
 
-bool Engine::launch(const Launch &L, hipStream_t s, std::string &err)
+bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record)
 {
     void *arg = L.arg;
     int nprob = L.nprob;
@@ -842,6 +842,12 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err)
         pending_.push_back(pe);
         return true;
     }
+    if (record) {
+        // the cross-stream event is recorded by this kernel's dispatch packet
+        return check(hip_->hipExtModuleLaunchKernel(L.fn, L.grid * block, 1, 1, block, 1, 1, L.shmem, s, params,
+                                                    nullptr, nullptr, record, 0),
+                     kFamilyName[L.family], err);
+    }
     return check(hip_->hipModuleLaunchKernel(L.fn, L.grid, 1, 1, block, 1, 1, L.shmem, s, params, nullptr),
                  kFamilyName[L.family], err);
 }
@@ -867,8 +873,14 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
         hipStream_t ls = st[L.stream];
         if (L.wait_ev >= 0 && !check(hip_->hipStreamWaitEvent(ls, ev_[L.wait_ev], 0), "hipStreamWaitEvent", err))
             return false;
-        if (!launch(L, ls, err)) return false;
-        if (L.record_ev >= 0 && !check(hip_->hipEventRecord(ev_[L.record_ev], ls), "hipEventRecord", err)) return false;
+        // cross-stream events ride in the dispatch packet, unless the launch is
+        // being profiled (its packet then carries the timing events) or the
+        // stream is being captured (a graph edge needs an explicit record)
+        const bool explicit_rec = capturing_ || ((prof_mask_ >> L.family) & 1u);
+        if (!launch(L, ls, err, L.record_ev >= 0 && !explicit_rec ? ev_[L.record_ev] : nullptr)) return false;
+        if (L.record_ev >= 0 && explicit_rec &&
+            !check(hip_->hipEventRecord(ev_[L.record_ev], ls), "hipEventRecord", err))
+            return false;
         if (!steps || L.step_end < 0) continue;
         int done[2] = {L.step_end, L.step_end == 22 ? 23 : -1};
         for (int stp : done) {
@@ -915,7 +927,9 @@ bool Engine::replay(Plan &p, hipStream_t s, std::string &err)
         if (!check(hip_->hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture", err))
             return false;
         std::string rerr;
+        capturing_ = true;
         const bool ok = run(p, stream_, nullptr, rerr);
+        capturing_ = false;
         const hipError_t e = hip_->hipStreamEndCapture(stream_, &g);
         if (!ok) {
             if (g) hip_->hipGraphDestroy(g);

@@ -124,7 +124,7 @@ private:
     static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, ArenaLayout &L);
     bool use_graph() const;
     void free_plan(Plan &p);
-    bool launch(const Launch &L, hipStream_t s, std::string &err);
+    bool launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record = nullptr);
     bool fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err);
     bool fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const;
     void push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int stream, double bytes_a, double bytes_b);
@@ -139,6 +139,7 @@ private:
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};
+    bool capturing_ = false;  // run() is recording a graph
 
     // weights
     bool have_weights_ = false;
