@@ -15,7 +15,7 @@
 // the imaginary parts of the DC and Nyquist columns; two rows again share one
 // complex transform.  The output is scaled and added to `feat` (f + FU(f)).
 //
-// 1-D transforms are Stockham auto-sort passes with radix 4, 2, 3, 5 (or a
+// 1-D transforms are Stockham auto-sort passes with radix 8, 4, 2, 3, 5 (or a
 // direct DFT for other prime factors), ping-ponging between two LDS buffers.
 // Twiddles come from a per-length table exp(-2 pi i k/n) built in f64 on the
 // host.  The exponent sign per length follows the reference CPU engine: a
@@ -100,6 +100,28 @@ __device__ __forceinline__ void dft<5>(float2 (&v)[5], int s)
     v[3] = csub(m2, n2);
 }
 
+// Radix 8 as two radix-4 DFTs (even and odd inputs) joined by the powers of
+// w = exp(s 2 pi i / 8): X[q] = E[q%4] + w^q O[q%4], w^(q+4) = -w^q.
+template <>
+__device__ __forceinline__ void dft<8>(float2 (&v)[8], int s)
+{
+    const float h = 0.70710678118654752440f;
+    float2 e[4] = {v[0], v[2], v[4], v[6]}, o[4] = {v[1], v[3], v[5], v[7]};
+    dft<4>(e, s);
+    dft<4>(o, s);
+    const float2 o1 = make_float2(h * (o[1].x - s * o[1].y), h * (o[1].y + s * o[1].x));  // * (1 + s i)/sqrt 2
+    const float2 o2 = mul_si(o[2], s);                                                    // * s i
+    const float2 o3 = make_float2(h * (-o[3].x - s * o[3].y), h * (-o[3].y + s * o[3].x));  // * (-1 + s i)/sqrt 2
+    v[0] = cadd(e[0], o[0]);
+    v[4] = csub(e[0], o[0]);
+    v[1] = cadd(e[1], o1);
+    v[5] = csub(e[1], o1);
+    v[2] = cadd(e[2], o2);
+    v[6] = csub(e[2], o2);
+    v[3] = cadd(e[3], o3);
+    v[7] = csub(e[3], o3);
+}
+
 // Butterfly (b, j) of a radix-R Stockham pass over `count` transforms of
 // length n; element e of transform b sits at b*bstride + e*estride.
 struct Pass {
@@ -181,6 +203,7 @@ __device__ __forceinline__ float2 *stockham(const FftLen &L, const float2 *tw, f
         case 3: pass_fixed<3>(P); break;
         case 4: pass_fixed<4>(P); break;
         case 5: pass_fixed<5>(P); break;
+        case 8: pass_fixed<8>(P); break;
         default: pass_generic(P, R); break;
         }
         __syncthreads();

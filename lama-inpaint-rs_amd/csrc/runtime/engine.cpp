@@ -348,6 +348,8 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
         m /= r;
         return true;
     };
+    while (m % 8 == 0)
+        if (!push(8)) break;
     while (m % 4 == 0)
         if (!push(4)) break;
     while (m % 2 == 0)
