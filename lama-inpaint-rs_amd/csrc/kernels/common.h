@@ -111,8 +111,9 @@ struct FftArgs {
 };
 
 // Sum of K-partials + BN + ReLU (+ residual) over [C][plane].
+#define LAMA_FIN_PARTS 5  // K partials of the FFC local GEMM: l2l, then g2l in four K ranges
 struct FinalizeArgs {
-    const float *part[4];
+    const float *part[LAMA_FIN_PARTS];
     int nparts, C;
     long plane;
     const float *scale, *shift, *res;

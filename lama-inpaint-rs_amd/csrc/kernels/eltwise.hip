@@ -1,6 +1,7 @@
 // Elementwise finish of the FFC local branch: the local GEMM runs as K
-// quarters that write raw partial sums (one per group of 128 input
-// channels); this sums them in quarter order, then applies BN_l, ReLU and the
+// ranges that write raw partial sums (l2l over the 128 local input channels,
+// then g2l over the 384 global ones in four ranges of 96); this sums them in
+// that order, then applies BN_l, ReLU and the
 // residual (cpu.rs:650-653 and 508-512).  HBM-bound: reads the partials and
 // the residual once, writes the output once.
 #include <hip/hip_runtime.h>
@@ -21,10 +22,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
         idx[e] = min(i + e, n - 1);
         ch[e] = (int)(idx[e] / A.plane);
     }
-    float part[4][4], sc[4], sh[4], rs[4];
+    float part[LAMA_FIN_PARTS][4], sc[4], sh[4], rs[4];
     const int np = A.nparts;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < LAMA_FIN_PARTS; ++q) {
         const LAMA_GLOBAL float *pq = gp(A.part[min(q, np - 1)]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[q][e] = pq[idx[e]];
@@ -43,7 +44,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
     for (int e = 0; e < 4; ++e) {
         float v = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < LAMA_FIN_PARTS; ++q)
             if (q < np) v += part[q][e];
         float x = fmaxf(v * sc[e] + sh[e], 0.f);
         if (A.res) x += rs[e];

@@ -484,11 +484,11 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.s2 = take(384 * PS * 4);
     L.out = take(3 * P * 4);
     L.gc = take(2 * 384 * P8 * 4);  // the l2g partial, double-buffered by FFC parity
-    L.lq = take(4 * 128 * P8 * 4);  // the FFC local GEMM's four K-quarter partials
+    L.lq = take(LAMA_FIN_PARTS * 128 * P8 * 4);  // the FFC local GEMM's K-range partials
     L.tmp = take(fg.split ? fg.tmp_bytes : 0);
     L.twr = take(ntwr * 4);
     L.twc = take(ntwc * 4);
-    const size_t n_conv = 4 + 36 * 8 + 4 * 3;      // problems
+    const size_t n_conv = 4 + 36 * 9 + 4 * 3;      // problems
     const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
     L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
     return off;
@@ -646,8 +646,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
 
     // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual).
     // FFC k's 3x3 convolutions run on the main stream as two grouped launches:
-    //   A(k): the l2l K quarter (input x_l) and l2g (raw, into GC[k % 2]);
-    //   B(k): the three g2l K quarters (input x_g);
+    //   A(k): l2l (input x_l) and l2g (raw, into GC[k % 2]);
+    //   B(k): g2l in four K ranges (input x_g);
     // then the local finalize.  The side stream runs the SpectralTransform
     // chain and conv2, whose epilogue adds GC[k % 2] before BN_g.  A(k+1)
     // needs only x_l(k+1), the main stream's own finalize output, so it is
@@ -663,33 +663,37 @@ bool Engine::build_plan(Plan &p, std::string &err)
         q.relu = 0;
         return q;
     };
-    // local K quarter q of FFC k (input channels 128q..128q+127), raw partial
-    auto quarter = [&](int k, int q) {
+    // Local GEMM part q of FFC k, a raw partial into LQ plane q: part 0 is l2l
+    // (input channels 0..127, 16 chunks of 8), parts 1-4 are g2l over input
+    // channels 128 + 96 (q-1) .. +95 (12 chunks each), so the g2l launch is 512
+    // equal workgroups -- one per slot of two per CU.
+    auto part = [&](int k, int q) {
         const FfcW &Fw = ffc_[k];
-        ConvSeg sq = seg(ffc_src(k) + (size_t)128 * q * P8, Fw.local, 128, H8, W8);
-        sq.wt = wp(Fw.local.off) + (size_t)q * 16 * 72;  // chunks 16q.. of the packed rows
-        sq.nchunk = 16;
+        const int c0 = q == 0 ? 0 : 128 + 96 * (q - 1), nch = q == 0 ? 128 : 96;
+        ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8, Fw.local, nch, H8, W8);
+        sq.wt = wp(Fw.local.off) + (size_t)(c0 / 8) * 72;  // chunk c0/8 of the packed rows
+        sq.nchunk = nch / 8;
         return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, LQ + (size_t)q * 128 * P8, P8, W8, nullptr));
     };
     auto launch_a = [&](int k) {
         const FfcW &Fw = ffc_[k];
         std::vector<ConvProblem> probs{
-            quarter(k, 0), raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8,
-                                       W8, nullptr))};
+            part(k, 0), raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8,
+                                    W8, nullptr))};
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
                     k % 2 ? EV_A1 : EV_A0);
     };
     auto launch_b = [&](int k) {
-        std::vector<ConvProblem> probs{quarter(k, 1), quarter(k, 2), quarter(k, 3)};
-        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9), f4 * (384 * P8 + 3 * 128 * P8 + 128 * 384 * 9),
+        std::vector<ConvProblem> probs{part(k, 1), part(k, 2), part(k, 3), part(k, 4)};
+        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9), f4 * (384 * P8 + 4 * 128 * P8 + 128 * 384 * 9),
                     S_MAIN, k == 0 ? -1 : ((k - 1) % 2 ? EV_S1 : EV_S0));
     };
     auto launch_finalize = [&](int k) {
         const FfcW &Fw = ffc_[k];
         FinalizeArgs fa2{};
-        for (int q = 0; q < 4; ++q) fa2.part[q] = LQ + (size_t)q * 128 * P8;
-        fa2.nparts = 4;
+        for (int q = 0; q < LAMA_FIN_PARTS; ++q) fa2.part[q] = LQ + (size_t)q * 128 * P8;
+        fa2.nparts = LAMA_FIN_PARTS;
         fa2.C = 128;
         fa2.plane = (long)P8;
         fa2.scale = wp(Fw.bn_l);
@@ -705,7 +709,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         L.arg = put(&fa2, sizeof fa2);
         L.nparams = 1;
         L.step_end = -1;
-        L.bytes = f4 * 128 * P8 * (4 + 1 + (fa2.res ? 1 : 0));
+        L.bytes = f4 * 128 * P8 * (LAMA_FIN_PARTS + 1 + (fa2.res ? 1 : 0));
         p.launches.push_back(L);
     };
     auto launch_spectral = [&](int k) {
