@@ -215,13 +215,29 @@ __device__ __forceinline__ float2 *stockham(const FftLen &L, const float2 *tw, f
     return const_cast<float2 *>(P.in);
 }
 
-// Both twiddle tables into LDS (row table first), ahead of the first pass.
-__device__ __forceinline__ void load_twiddles(const FftArgs &A, float2 *twr, float2 *twc)
+// Both twiddle tables into LDS (row table first), ahead of the first pass:
+// thread t fetches entry t of the concatenated tables with an unconditional
+// (clamped) load, so the fetch can be issued together with the plane's.
+struct TwFetch {
+    float2 v;
+    __device__ __forceinline__ void issue(const FftArgs &A, int t)
+    {
+        const int n = A.W + A.H, i = min(t, n - 1);
+        const LAMA_GLOBAL float2 *p = i < A.W ? gp(reinterpret_cast<const float2 *>(A.row.tw)) + i
+                                              : gp(reinterpret_cast<const float2 *>(A.col.tw)) + (i - A.W);
+        v = *p;
+    }
+};
+
+__device__ __forceinline__ void put_twiddles(const FftArgs &A, const TwFetch &f, float2 *twr, float2 *twc)
 {
-    const LAMA_GLOBAL float2 *gr = gp(reinterpret_cast<const float2 *>(A.row.tw));
-    const LAMA_GLOBAL float2 *gc = gp(reinterpret_cast<const float2 *>(A.col.tw));
-    for (int i = threadIdx.x; i < A.W; i += blockDim.x) twr[i] = gr[i];
-    for (int i = threadIdx.x; i < A.H; i += blockDim.x) twc[i] = gc[i];
+    const int n = A.W + A.H, t = threadIdx.x;
+    if (t < n) (t < A.W ? twr[t] : twc[t - A.W]) = f.v;
+    for (int i = t + blockDim.x; i < n; i += blockDim.x) {  // tables longer than the block (rare shapes)
+        TwFetch g;
+        g.issue(A, i);
+        (i < A.W ? twr[i] : twc[i - A.W]) = g.v;
+    }
 }
 
 }  // namespace
@@ -235,26 +251,52 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
     const int NB = max(HP * W, H * Wh);
     float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
-    load_twiddles(A, twr, twc);
+    // Prologue: every global load (the twiddle entry, this block's plane) is
+    // issued before the first LDS write; the host keeps this kernel to planes
+    // of at most LAMA_FFT_NT * 8 row-pair elements (two quads per thread).
+    TwFetch tw;
+    tw.issue(A, threadIdx.x);
     const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
+    const int NT = LAMA_FFT_NT;
     if ((W & 3) == 0 && (H & 1) == 0) {  // row pairs as float4 quads
-        const int W4 = W >> 2;
-        for (int q = threadIdx.x; q < HP * W4; q += blockDim.x) {
+        const int W4 = W >> 2, nq = HP * W4;
+        constexpr int RQ = 2;
+        float4 qa[RQ], qb[RQ];
+#pragma unroll
+        for (int k = 0; k < RQ; ++k) {
+            const int q = min((int)threadIdx.x + k * NT, nq - 1), p = q / W4, x = (q - p * W4) * 4;
+            qa[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
+            qb[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
+        }
+        put_twiddles(A, tw, twr, twc);
+#pragma unroll
+        for (int k = 0; k < RQ; ++k) {
+            const int q = threadIdx.x + k * NT;
+            if (q >= nq) break;
             const int p = q / W4, x = (q - p * W4) * 4;
-            const float4 a = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
-            const float4 b = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
             float2 *d = b0 + p * W + x;
-            d[0] = make_float2(a.x, b.x);
-            d[1] = make_float2(a.y, b.y);
-            d[2] = make_float2(a.z, b.z);
-            d[3] = make_float2(a.w, b.w);
+            d[0] = make_float2(qa[k].x, qb[k].x);
+            d[1] = make_float2(qa[k].y, qb[k].y);
+            d[2] = make_float2(qa[k].z, qb[k].z);
+            d[3] = make_float2(qa[k].w, qb[k].w);
         }
     } else {
-        for (int idx = threadIdx.x; idx < HP * W; idx += blockDim.x) {
-            const int p = idx / W, x = idx - p * W;
-            const float a = src[(2 * p) * W + x];
-            const float b = 2 * p + 1 < H ? src[(2 * p + 1) * W + x] : 0.f;
-            b0[idx] = make_float2(a, b);
+        const int ne = HP * W;
+        constexpr int RS = 8;
+        float sa[RS], sb[RS];
+#pragma unroll
+        for (int k = 0; k < RS; ++k) {
+            const int idx = min((int)threadIdx.x + k * NT, ne - 1), p = idx / W, x = idx - p * W;
+            sa[k] = src[(2 * p) * W + x];
+            sb[k] = src[min(2 * p + 1, H - 1) * W + x];
+        }
+        put_twiddles(A, tw, twr, twc);
+#pragma unroll
+        for (int k = 0; k < RS; ++k) {
+            const int idx = threadIdx.x + k * NT;
+            if (idx >= ne) break;
+            const int p = idx / W;
+            b0[idx] = make_float2(sa[k], 2 * p + 1 < H ? sb[k] : 0.f);
         }
     }
     __syncthreads();
@@ -287,21 +329,37 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
     const int NB = max(HP * W, H * Wh);
     float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
-    load_twiddles(A, twr, twc);
+    // Prologue: the twiddle entry, this block's spectrum (at most
+    // LAMA_FFT_NT * 8 values per plane, as the host guarantees) and the `f +`
+    // addend of the output are all fetched before the first LDS write; the
+    // addend's latency then hides behind the transforms.
+    const int NT = LAMA_FFT_NT;
+    TwFetch tw;
+    tw.issue(A, threadIdx.x);
     const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
-    // the `f +` addend of the output is fetched now, its latency hidden by the transforms
     const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
     const bool vec = (W & 3) == 0;
-    const int n4 = (H * W) >> 2;
-    constexpr int FP = 2;
+    const int n4 = (H * W) >> 2, ns = H * Wh;
+    constexpr int FP = 2, RS = 8;
     float4 fpre[FP];
+    // unaligned planes (W % 4 != 0) fetch a harmless aligned dummy instead
+    const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(vec ? f : gp(A.feat));
 #pragma unroll
-    for (int k = 0; k < FP; ++k) {
-        const int i4 = min((int)threadIdx.x + k * (int)blockDim.x, max(n4 - 1, 0));
-        fpre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (vec) fpre[k] = reinterpret_cast<const LAMA_GLOBAL float4 *>(f)[i4];
+    for (int k = 0; k < FP; ++k) fpre[k] = f4[vec ? min((int)threadIdx.x + k * NT, max(n4 - 1, 0)) : 0];
+    float re[RS], im[RS];
+#pragma unroll
+    for (int k = 0; k < RS; ++k) {
+        const int idx = min((int)threadIdx.x + k * NT, ns - 1);
+        re[k] = sre[idx];
+        im[k] = sim[idx];
     }
-    for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) b0[idx] = make_float2(sre[idx], sim[idx]);
+    put_twiddles(A, tw, twr, twc);
+#pragma unroll
+    for (int k = 0; k < RS; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        if (idx >= ns) break;
+        b0[idx] = make_float2(re[k], im[k]);
+    }
     __syncthreads();
     float2 *r = stockham(A.col, twc, b0, b1, Wh, 1, Wh, -A.col.sign_fwd);
     float2 *o = r == b0 ? b1 : b0;

@@ -382,7 +382,9 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
     g.lds = (2 * std::max((size_t)HP * W, (size_t)H * Wh) + H + W) * f2;
     const char *env = getenv("LAMA_FFT_SPLIT");
     const bool force = env && atoi(env) == 1;
-    if (!force && g.lds <= std::min<size_t>(max_lds_, 64 * 1024)) {
+    // the single-block kernels fetch at most 8 plane values per thread
+    const bool fits = std::max((size_t)HP * W, (size_t)H * Wh) <= 8 * (size_t)LAMA_FFT_NT;
+    if (!force && fits && g.lds <= std::min<size_t>(max_lds_, 64 * 1024)) {
         g.grid_rows = g.grid_cols = (unsigned)C;  // one block per plane
         return true;
     }
