@@ -32,7 +32,7 @@ namespace {
 template <int KH_, int KW_, int S_, bool REFLECT_, int KC_, int TR_, int TC_>
 struct Cfg {
     static constexpr int KH = KH_, KW = KW_, S = S_, KC = KC_, TR = TR_, TC = TC_;
-    static constexpr bool REFLECT = REFLECT_;
+    static constexpr bool REFLECT = REFLECT_, PW = false;
     static constexpr int T = KH * KW;
     static constexpr int PAD = REFLECT ? (KH - 1) / 2 : 0;
     static constexpr int PR = (TR - 1) * S + KH;
@@ -245,6 +245,151 @@ __device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg, int 
     }
 }
 
+// Pointwise (1x1) convolution over flat planes of N pixels: the same 64 x 64
+// tile, 4 waves and two-stage pipeline, but the activations are staged
+// channel-major, [KC][64 px], as they lie in memory.  Every thread moves whole
+// runs of 4 pixels (one 16-byte global load and one 16-byte LDS store, no
+// transpose), and each MFMA's B operand is one 4-byte LDS read per lane: lane
+// half g reads 32 consecutive pixels of channel g*KC/2 + c.  The two halves'
+// rows sit in separate regions whose bases differ by 32 banks.  VEC: planes
+// are 16-byte aligned with N % 4 == 0 (float4 loads); otherwise each run is
+// four clamped scalar loads.
+template <int KC_, bool VEC_>
+struct PwCfg {
+    static constexpr bool PW = true, VEC = VEC_;
+    static constexpr int KC = KC_, TR = 1, TC = 64;
+    static constexpr int WSTR = KC + 4;             // weight row stride, = 4 (mod 8)
+    static constexpr int HALF = KC / 2 * 64 + 32;   // one lane half's channel rows
+    static constexpr int W_LDS = 64 * WSTR;
+    static constexpr int LDS = W_LDS + 2 * HALF;
+    static constexpr int WITER = 64 * KC / 4 / LAMA_NT;  // weight float4s per thread
+    static constexpr int XITER = KC * 64 / 4 / LAMA_NT;  // activation runs per thread
+    static_assert(WITER * LAMA_NT * 4 == 64 * KC && XITER * LAMA_NT * 4 == KC * 64, "whole float4 slots");
+    static_assert(KC % 8 == 0 && WSTR % 8 == 4 && HALF % 64 == 32, "bank placement");
+};
+
+template <class C>
+struct PwSlots {
+    int wg[C::WITER], wl[C::WITER];                // weights: global float offset in the row, LDS offset
+    int xc[C::XITER], xp[C::XITER], xl[C::XITER];  // activations: channel in chunk, first pixel, LDS offset
+};
+
+template <class C>
+struct PwStage {
+    float w[4 * C::WITER];
+    float x[4 * C::XITER];
+};
+
+template <class C>
+__device__ __forceinline__ void pw_make_slots(PwSlots<C> &sl, const ConvSeg &sg, int m0, int M, int ox0)
+{
+    const int tid = threadIdx.x, N = sg.IH * sg.IW;
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it) {
+        const int idx = tid + it * LAMA_NT, row = idx / (C::KC / 4), c4 = idx % (C::KC / 4);
+        sl.wl[it] = row * C::WSTR + c4 * 4;
+        sl.wg[it] = min(m0 + row, M - 1) * sg.wrow + c4 * 4;
+    }
+#pragma unroll
+    for (int it = 0; it < C::XITER; ++it) {
+        const int idx = tid + it * LAMA_NT, ci = idx / 16, q = idx % 16;
+        sl.xc[it] = ci;
+        sl.xl[it] = (ci / (C::KC / 2)) * C::HALF + (ci % (C::KC / 2)) * 64 + 4 * q;
+        // runs past the plane read the last whole run (VEC) or clamp per element
+        sl.xp[it] = C::VEC ? min(ox0 + 4 * q, N - 4) : ox0 + 4 * q;
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &sl, const ConvSeg &sg, int ck)
+{
+    const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::KC;
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it) {
+        const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(wt + sl.wg[it]);
+        st.w[4 * it] = v.x;
+        st.w[4 * it + 1] = v.y;
+        st.w[4 * it + 2] = v.z;
+        st.w[4 * it + 3] = v.w;
+    }
+    const int N = sg.IH * sg.IW;
+    const int c0 = ck * C::KC, clast = sg.C - 1 - c0;  // channels past C read a valid plane (zero weights)
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * N;
+#pragma unroll
+    for (int it = 0; it < C::XITER; ++it) {
+        const LAMA_GLOBAL float *q = src + (long)min(sl.xc[it], clast) * N;
+        if constexpr (C::VEC) {
+            const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(q + sl.xp[it]);
+            st.x[4 * it] = v.x;
+            st.x[4 * it + 1] = v.y;
+            st.x[4 * it + 2] = v.z;
+            st.x[4 * it + 3] = v.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st.x[4 * it + e] = q[min(sl.xp[it] + e, N - 1)];
+        }
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void pw_store_chunk(const PwStage<C> &st, const PwSlots<C> &sl, float *lds)
+{
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it)
+        *reinterpret_cast<float4 *>(lds + sl.wl[it]) =
+            make_float4(st.w[4 * it], st.w[4 * it + 1], st.w[4 * it + 2], st.w[4 * it + 3]);
+#pragma unroll
+    for (int it = 0; it < C::XITER; ++it)
+        *reinterpret_cast<float4 *>(lds + C::W_LDS + sl.xl[it]) =
+            make_float4(st.x[4 * it], st.x[4 * it + 1], st.x[4 * it + 2], st.x[4 * it + 3]);
+}
+
+template <class C>
+__device__ __forceinline__ void pw_compute_chunk(f32x16 &acc, const float *lds)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
+    constexpr int H = C::KC / 2;
+    const float *wrow = lds + (wm * 32 + j) * C::WSTR + g * H;
+    const float *xrow = lds + C::W_LDS + g * C::HALF + wn * 32 + j;
+    float a[H], b[H];
+    lds_vec<H>(a, wrow);
+#pragma unroll
+    for (int c = 0; c < H; ++c) b[c] = xrow[c * 64];
+#pragma unroll
+    for (int c = 0; c < H; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c], b[c], acc, 0, 0, 0);
+}
+
+// The K loop of a pointwise segment: two LDS stages, two register stages,
+// one barrier per chunk (the schedule of run_segment).
+template <class C>
+__device__ __forceinline__ void run_segment_pw(f32x16 &acc, const ConvSeg &sg, int m0, int M, int ox0, float *lds)
+{
+    const int n = sg.nchunk;
+    if (n <= 0) return;
+    PwSlots<C> sl;
+    pw_make_slots<C>(sl, sg, m0, M, ox0);
+    float *l0 = lds, *l1 = lds + C::LDS;
+    const int last = n - 1;
+    PwStage<C> r0, r1;
+    pw_load_chunk<C>(r0, sl, sg, 0);
+    pw_load_chunk<C>(r1, sl, sg, min(1, last));
+    pw_store_chunk<C>(r0, sl, l0);
+    pw_load_chunk<C>(r0, sl, sg, min(2, last));
+    __syncthreads();
+    for (int ck = 0; ck < n; ck += 2) {
+        pw_compute_chunk<C>(acc, l0);
+        pw_store_chunk<C>(r1, sl, l1);
+        pw_load_chunk<C>(r1, sl, sg, min(ck + 3, last));
+        __syncthreads();
+        if (ck + 1 >= n) break;
+        pw_compute_chunk<C>(acc, l1);
+        pw_store_chunk<C>(r0, sl, l0);
+        pw_load_chunk<C>(r0, sl, sg, min(ck + 4, last));
+        __syncthreads();
+    }
+}
+
 // Epilogue operands read from memory (addend, residual) are fetched before
 // the K loop so their latency hides behind it.
 struct EpiPre {
@@ -344,7 +489,10 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    run_segment<C0, NBUF>(acc, P.s0, m0, P.M, oy0, ox0, lds);
+    if constexpr (C0::PW)
+        run_segment_pw<C0>(acc, P.s0, m0, P.M, ox0, lds);
+    else
+        run_segment<C0, NBUF>(acc, P.s0, m0, P.M, oy0, ox0, lds);
     if constexpr (SEG1) {
         using C1 = Cfg<1, 1, 1, false, C0::KC, C0::TR, C0::TC>;
         if (P.s1.nchunk > 0) run_segment<C1, NBUF>(acc, P.s1, m0, P.M, oy0, ox0, lds);
@@ -368,7 +516,6 @@ using CfgHead = Cfg<7, 7, 1, true, 4, 2, 32>;
 using CfgDown = Cfg<3, 3, 2, true, 8, 2, 32>;
 using CfgFfc = Cfg<3, 3, 1, true, 8, 2, 32>;
 using CfgFfc1 = Cfg<1, 1, 1, false, 8, 2, 32>;
-using Cfg1x1 = Cfg<1, 1, 1, false, 32, 1, 64>;
 using CfgT00 = Cfg<1, 1, 1, false, 8, 2, 32>;
 using CfgT01 = Cfg<1, 2, 1, false, 8, 2, 32>;
 using CfgT10 = Cfg<2, 1, 1, false, 8, 2, 32>;
@@ -408,29 +555,29 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
     conv_tile<CfgFfc, true>(probs[pi], b, lds, epl);
 }
 
-// 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit conv).
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1(const ConvProblem *__restrict__ probs, int nprob)
-{
-    side_priority();
-    __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
-    __shared__ float epl[192];
-    int b = blockIdx.x;
-    int pi = find_problem(probs, nprob, b);
-    conv_tile<Cfg1x1, false>(probs[pi], b, lds, epl);
-}
+// 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
+// conv).  lama_conv1x1 needs 16-byte aligned planes with N % 4 == 0;
+// lama_conv1x1_s takes any N.
+#define LAMA_PW_KERNEL(NAME, VEC, PREFETCH)                                                                 \
+    extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, int nprob) \
+    {                                                                                                       \
+        side_priority();                                                                                    \
+        using C = PwCfg<32, VEC>;                                                                           \
+        __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
+        __shared__ float epl[192];                                                                          \
+        int b = blockIdx.x;                                                                                 \
+        int pi = find_problem(probs, nprob, b);                                                             \
+        conv_tile<C, false, 2, PREFETCH>(probs[pi], b, lds, epl);                                           \
+    }
+LAMA_PW_KERNEL(lama_conv1x1, true, false)
+LAMA_PW_KERNEL(lama_conv1x1_s, false, false)
 
 // The same with addend / residual fetched before the K loop (the
 // SpectralTransform conv2, whose epilogue adds the l2g partial and the
 // residual).
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv1x1_res(const ConvProblem *__restrict__ probs, int nprob)
-{
-    side_priority();
-    __shared__ __attribute__((aligned(16))) float lds[2 * Cfg1x1::LDS];
-    __shared__ float epl[192];
-    int b = blockIdx.x;
-    int pi = find_problem(probs, nprob, b);
-    conv_tile<Cfg1x1, false, 2, true>(probs[pi], b, lds, epl);
-}
+LAMA_PW_KERNEL(lama_conv1x1_res, true, true)
+LAMA_PW_KERNEL(lama_conv1x1_res_s, false, true)
+#undef LAMA_PW_KERNEL
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions
 // (problems 0..3 = phases (py,px) = (0,0), (0,1), (1,0), (1,1)), each a valid

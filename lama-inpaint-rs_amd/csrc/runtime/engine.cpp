@@ -50,6 +50,10 @@ const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lam
 
 const char *const kSplitName[4] = {"lama_rfft2_rows", "lama_rfft2_cols", "lama_irfft2_cols", "lama_irfft2_rows"};
 
+// F_CONV1 / F_CONV1R variants with per-element activation loads, for planes
+// whose length is not a multiple of 4 or that are not 16-byte aligned.
+const char *const kPwAnyName[2] = {"lama_conv1x1_s", "lama_conv1x1_res_s"};
+
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 void tile_shape(int family, int &tr, int &tc)
 {
@@ -219,6 +223,8 @@ bool Engine::open(std::string &err)
         if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
     for (int f = 0; f < 4; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_split_[f], module_, kSplitName[f]), kSplitName[f], err)) return false;
+    for (int f = 0; f < 2; ++f)
+        if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err)) return false;
     {
         int lds = 0;
         if (hip_->hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_) == hipSuccess && lds > 0)
@@ -374,6 +380,18 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // twiddle tables) in one block's LDS; it is used while that fits in 64 KB.
 // Larger planes (or LAMA_FFT_SPLIT=1) use the row/column launches, each
 // block holding at most 64 KB of ping-pong buffers.
+// The kernel of a conv launch: the 1x1 families use float4 activation loads
+// only when every plane is 16-byte aligned and a multiple of 4 floats long.
+hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
+{
+    if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
+    for (size_t i = 0; i < n; ++i) {
+        const ConvSeg &s = probs[i].s0;
+        if (((size_t)s.IH * s.IW) % 4 != 0 || (uintptr_t)s.src % 16 != 0) return fn_pw_any_[family == F_CONV1R];
+    }
+    return fn_[family];
+}
+
 bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
 {
     const int Wh = W / 2 + 1, HP = (H + 1) / 2;
@@ -592,7 +610,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
     auto conv_launch = [&](int family, std::vector<ConvProblem> probs, int step, double flops, double bytes,
                            int stream = S_MAIN, int wait_ev = -1, int record_ev = -1) {
         Launch L{};
-        L.fn = fn_[family];
+        L.fn = conv_fn(family, probs.data(), probs.size());
         L.family = family;
         L.stream = stream;
         L.wait_ev = wait_ev;
@@ -1114,7 +1132,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
     if (!check(hip_->hipMemcpy(dq, &q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
     Launch L{};
-    L.fn = fn_[family];
+    L.fn = conv_fn(family, &q, 1);
     L.family = family;
     L.grid = (unsigned)q.nblocks;
     L.arg = dq;

@@ -136,6 +136,8 @@ private:
     hipFunction_t fn_[F_COUNT] = {};
     // split-mode FFT kernels: rfft2 rows, rfft2 cols, irfft2 cols, irfft2 rows
     hipFunction_t fn_split_[4] = {};
+    hipFunction_t fn_pw_any_[2] = {};  // 1x1 kernels for planes that are not float4-aligned
+    hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};

@@ -34,7 +34,11 @@ def _oracle_bn_relu(y, s, t):
     (4, 64, 20, 40, 7, 1),     # model.1 head (cin 4)
     (6, 10, 8, 8, 7, 1),       # 7x7 on a plane barely wider than the kernel
     (384, 192, 8, 8, 1, 1),    # SpectralTransform conv1
-    (40, 70, 5, 33, 1, 1),     # 1x1, ragged everything
+    (40, 70, 5, 33, 1, 1),     # 1x1, ragged everything (plane not a multiple of 4: per-element loads)
+    (384, 384, 64, 33, 1, 1),  # FourierUnit conv at a 512x512 input (float4 loads)
+    (96, 130, 7, 12, 1, 1),    # 1x1 float4 loads: partial last tile, M % 64 != 0
+    (50, 64, 2, 2, 1, 1),      # 1x1 plane of exactly one float4 run
+    (33, 20, 1, 3, 1, 1),      # 1x1 plane shorter than a float4 run
 ])
 def test_conv2d(engine, cin, cout, h, w, k, stride):
     rng = np.random.default_rng(cin * 1000 + cout + k)
