@@ -5,6 +5,11 @@
 #include <stdint.h>
 
 #define LAMA_NT 256      // threads per block (4 waves of 64)
+// input channels per K chunk of the pointwise (1x1) convolutions; their
+// weights are packed in chunks of this many
+#ifndef LAMA_PW_KC
+#define LAMA_PW_KC 32
+#endif
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
 #define LAMA_TAIL_ROWS 8 // output tile of the 7x7 tail kernel (rows x columns)
 #define LAMA_TAIL_COLS 64

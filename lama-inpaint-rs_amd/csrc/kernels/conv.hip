@@ -57,6 +57,14 @@ struct Cfg {
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
+// base + a 32-bit byte offset: a uniform base and a per-lane offset map to
+// the scalar-base global load form (no 64-bit address arithmetic per lane)
+template <class T>
+__device__ __forceinline__ const LAMA_GLOBAL T *at_byte(const LAMA_GLOBAL float *base, unsigned off)
+{
+    return reinterpret_cast<const LAMA_GLOBAL T *>(reinterpret_cast<const LAMA_GLOBAL char *>(base) + off);
+}
+
 // Per-thread staging addresses, fixed for a block: each chunk only adds its
 // channel / K offset.  Staging is branch-free (a divergent branch around a
 // load makes the compiler wait for every outstanding load, which would
@@ -68,9 +76,9 @@ template <class C>
 struct Slots {
     int wg[C::WITER];  // weights: float offset of the float4 within the rows
     int wl[C::WITER];  // weights: LDS float offset
-    int pg[C::PITER];  // patch: spatial offset in the input plane (clamped)
-    int pl[C::PITER];  // patch: LDS float offset
-    int pc[C::PITER];  // patch: channel within the chunk; < 0 marks a zero slot
+    unsigned po[C::PITER];  // patch: byte offset from the chunk's first plane (channel * plane + position)
+    int pl[C::PITER];       // patch: LDS float offset
+    int pc[C::PITER];       // patch: channel within the chunk; < 0 marks a zero slot
 };
 
 template <class C>
@@ -102,7 +110,7 @@ __device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int 
             g = zero ? 0 : iy * sg.IW + ix;
         }
         sl.pl[it] = in ? (r * C::PC + c) * C::KCP + cl : C::PR * C::PC * C::KCP + (idx - C::P_ELEM);
-        sl.pg[it] = g;
+        sl.po[it] = 4u * (unsigned)(min(cl, C::KC - 1) * sg.IH * sg.IW + g);
         sl.pc[it] = (in && !zero) ? cl : -1;
     }
 }
@@ -121,18 +129,21 @@ __device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, con
     const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::WK;
 #pragma unroll
     for (int it = 0; it < C::WITER; ++it) {
-        const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(wt + sl.wg[it]);
+        const float4 v = *at_byte<float4>(wt, 4u * (unsigned)sl.wg[it]);
         st.w[4 * it] = v.x;
         st.w[4 * it + 1] = v.y;
         st.w[4 * it + 2] = v.z;
         st.w[4 * it + 3] = v.w;
     }
-    const long plane = (long)sg.IH * sg.IW;
-    const int c0 = ck * C::KC, clast = sg.C - 1 - c0;  // last valid channel within the chunk
+    // 32-bit byte offsets from the chunk's first plane; slots of channels past C
+    // (zero weights) read the last float of the source instead
+    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const int c0 = ck * C::KC;
+    const unsigned last = 4u * ((unsigned)(sg.C - c0) * plane - 1u);
     const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) {
-        const float v = src[(long)min(max(sl.pc[it], 0), clast) * plane + sl.pg[it]];
+        const float v = *at_byte<float>(src, min(sl.po[it], last));
         st.p[it] = sl.pc[it] >= 0 ? v : 0.f;
     }
 }
@@ -203,9 +214,12 @@ __device__ __forceinline__ void compute_chunk(f32x16 &acc, const float *wl, cons
 // consumed at step k, so each load has two chunks of MFMA time to land.
 // NBUF = 1 (single-chunk segments such as the 4-channel head) stages once.
 template <class C, int NBUF>
-__device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg, int m0, int M, int oy0, int ox0,
+__device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg_mem, int m0, int M, int oy0, int ox0,
                                             float *lds)
 {
+    // a register copy: the barriers of the loop would otherwise make the
+    // compiler re-read the descriptor from memory every chunk
+    const ConvSeg sg = sg_mem;
     const int n = sg.nchunk;
     if (n <= 0) return;
     Slots<C> sl;
@@ -272,6 +286,7 @@ template <class C>
 struct PwSlots {
     int wg[C::WITER], wl[C::WITER];                // weights: global float offset in the row, LDS offset
     int xc[C::XITER], xp[C::XITER], xl[C::XITER];  // activations: channel in chunk, first pixel, LDS offset
+    unsigned xo[C::XITER];                         // VEC: byte offset from the chunk's first plane
 };
 
 template <class C>
@@ -297,6 +312,7 @@ __device__ __forceinline__ void pw_make_slots(PwSlots<C> &sl, const ConvSeg &sg,
         sl.xl[it] = (ci / (C::KC / 2)) * C::HALF + (ci % (C::KC / 2)) * 64 + 4 * q;
         // runs past the plane read the last whole run (VEC) or clamp per element
         sl.xp[it] = C::VEC ? min(ox0 + 4 * q, N - 4) : ox0 + 4 * q;
+        sl.xo[it] = 4u * (unsigned)(ci * N + sl.xp[it]);
     }
 }
 
@@ -306,7 +322,7 @@ __device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &
     const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::KC;
 #pragma unroll
     for (int it = 0; it < C::WITER; ++it) {
-        const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(wt + sl.wg[it]);
+        const float4 v = *at_byte<float4>(wt, 4u * (unsigned)sl.wg[it]);
         st.w[4 * it] = v.x;
         st.w[4 * it + 1] = v.y;
         st.w[4 * it + 2] = v.z;
@@ -315,16 +331,18 @@ __device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &
     const int N = sg.IH * sg.IW;
     const int c0 = ck * C::KC, clast = sg.C - 1 - c0;  // channels past C read a valid plane (zero weights)
     const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * N;
+    // VEC: runs of channels past C (zero weights) read the source's last run
+    const unsigned vlast = 4u * ((unsigned)(sg.C - c0) * (unsigned)N - 4u);
 #pragma unroll
     for (int it = 0; it < C::XITER; ++it) {
-        const LAMA_GLOBAL float *q = src + (long)min(sl.xc[it], clast) * N;
         if constexpr (C::VEC) {
-            const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(q + sl.xp[it]);
+            const float4 v = *at_byte<float4>(src, min(sl.xo[it], vlast));
             st.x[4 * it] = v.x;
             st.x[4 * it + 1] = v.y;
             st.x[4 * it + 2] = v.z;
             st.x[4 * it + 3] = v.w;
         } else {
+            const LAMA_GLOBAL float *q = src + (long)min(sl.xc[it], clast) * N;
 #pragma unroll
             for (int e = 0; e < 4; ++e) st.x[4 * it + e] = q[min(sl.xp[it] + e, N - 1)];
         }
@@ -363,8 +381,9 @@ __device__ __forceinline__ void pw_compute_chunk(f32x16 &acc, const float *lds)
 // The K loop of a pointwise segment: two LDS stages, two register stages,
 // one barrier per chunk (the schedule of run_segment).
 template <class C>
-__device__ __forceinline__ void run_segment_pw(f32x16 &acc, const ConvSeg &sg, int m0, int M, int ox0, float *lds)
+__device__ __forceinline__ void run_segment_pw(f32x16 &acc, const ConvSeg &sg_mem, int m0, int M, int ox0, float *lds)
 {
+    const ConvSeg sg = sg_mem;  // held in registers across the barriers
     const int n = sg.nchunk;
     if (n <= 0) return;
     PwSlots<C> sl;
@@ -562,7 +581,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, int nprob) \
     {                                                                                                       \
         side_priority();                                                                                    \
-        using C = PwCfg<32, VEC>;                                                                           \
+        using C = PwCfg<LAMA_PW_KC, VEC>;                                                                           \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \

@@ -283,9 +283,9 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
                 return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
             });
             F.l2g = pack(A, 384, 128, 9, 8, [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; });
-            F.conv2 = pack(A, 384, 192, 1, 32, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
-            F.conv1 = pack(A, 192, 384, 1, 32, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
-            F.fu = pack(A, 384, 384, 1, 32, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
+            F.conv2 = pack(A, 384, 192, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
+            F.conv1 = pack(A, 192, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
+            F.fu = pack(A, 384, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
             if (!fold_bns(A, S, {{pf + ".convg2g.conv1.1", 192}}, F.bn1, err) ||
                 !fold_bns(A, S, {{pf + ".convg2g.fu.bn", 384}}, F.fu_bn, err) ||
                 !fold_bns(A, S, {{pb + ".bn_l", 128}}, F.bn_l, err) || !fold_bns(A, S, {{pb + ".bn_g", 384}}, F.bn_g, err))
@@ -1089,7 +1089,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     }
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
-    const int KC = family == F_CONV1 ? 32 : family == F_CONV7 ? 4 : 8;
+    const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : 8;
     Arena A;
     const int T = k * k;
     Packed pk = pack(A, cout, cin, T, KC, [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; });
