@@ -32,7 +32,7 @@ namespace {
 template <int KH_, int KW_, int S_, bool REFLECT_, int KC_, int TR_, int TC_>
 struct Cfg {
     static constexpr int KH = KH_, KW = KW_, S = S_, KC = KC_, TR = TR_, TC = TC_;
-    static constexpr bool REFLECT = REFLECT_, PW = false;
+    static constexpr bool REFLECT = REFLECT_;
     static constexpr int T = KH * KW;
     static constexpr int PAD = REFLECT ? (KH - 1) / 2 : 0;
     static constexpr int PR = (TR - 1) * S + KH;
@@ -135,11 +135,12 @@ __device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, con
         st.w[4 * it + 2] = v.z;
         st.w[4 * it + 3] = v.w;
     }
-    // 32-bit byte offsets from the chunk's first plane; slots of channels past C
-    // (zero weights) read the last float of the source instead
+    // 32-bit byte offsets from the chunk's first plane (below 4 * KC * plane,
+    // which the host bounds); slots of channels past C (zero weights) read the
+    // last float of the source instead
     const unsigned plane = (unsigned)(sg.IH * sg.IW);
     const int c0 = ck * C::KC;
-    const unsigned last = 4u * ((unsigned)(sg.C - c0) * plane - 1u);
+    const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
     const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) {
@@ -259,26 +260,29 @@ __device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg_mem, 
     }
 }
 
-// Pointwise (1x1) convolution over flat planes of N pixels: the same 64 x 64
-// tile, 4 waves and two-stage pipeline, but the activations are staged
-// channel-major, [KC][64 px], as they lie in memory.  Every thread moves whole
-// runs of 4 pixels (one 16-byte global load and one 16-byte LDS store, no
-// transpose), and each MFMA's B operand is one 4-byte LDS read per lane: lane
-// half g reads 32 consecutive pixels of channel g*KC/2 + c.  The two halves'
-// rows sit in separate regions whose bases differ by 32 banks.  VEC: planes
-// are 16-byte aligned with N % 4 == 0 (float4 loads); otherwise each run is
-// four clamped scalar loads.
-template <int KC_, bool VEC_>
+// Pointwise (1x1) convolution over flat planes of N pixels: 64 output
+// channels x NPX pixels per block (NPX = 64 or 128), 4 waves, the two-stage
+// pipeline of run_segment.  Wave (wm, wn) owns channels wm*32.. +32 and pixels
+// wn*NPX/2 .. +NPX/2 as NACC = NPX/64 accumulators of 32 pixels.  The
+// activations are staged channel-major, [KC][NPX], as they lie in memory:
+// every thread moves whole runs of 4 pixels (one 16-byte global load and one
+// 16-byte LDS store, no transpose), and each MFMA's B operand is one 4-byte
+// LDS read per lane: lane half g reads 32 consecutive pixels of channel
+// g*KC/2 + c.  The two halves' rows sit in separate regions whose bases
+// differ by 32 banks.  VEC: planes are 16-byte aligned with N % 4 == 0
+// (float4 loads); otherwise each run is four clamped scalar loads.
+template <int KC_, bool VEC_, int NPX_>
 struct PwCfg {
-    static constexpr bool PW = true, VEC = VEC_;
-    static constexpr int KC = KC_, TR = 1, TC = 64;
-    static constexpr int WSTR = KC + 4;             // weight row stride, = 4 (mod 8)
-    static constexpr int HALF = KC / 2 * 64 + 32;   // one lane half's channel rows
+    static constexpr bool VEC = VEC_;
+    static constexpr int KC = KC_, NPX = NPX_, NACC = NPX / 64;
+    static constexpr int WSTR = KC + 4;              // weight row stride, = 4 (mod 8)
+    static constexpr int HALF = KC / 2 * NPX + 32;   // one lane half's channel rows
     static constexpr int W_LDS = 64 * WSTR;
     static constexpr int LDS = W_LDS + 2 * HALF;
-    static constexpr int WITER = 64 * KC / 4 / LAMA_NT;  // weight float4s per thread
-    static constexpr int XITER = KC * 64 / 4 / LAMA_NT;  // activation runs per thread
-    static_assert(WITER * LAMA_NT * 4 == 64 * KC && XITER * LAMA_NT * 4 == KC * 64, "whole float4 slots");
+    static constexpr int WITER = 64 * KC / 4 / LAMA_NT;   // weight float4s per thread
+    static constexpr int XITER = KC * NPX / 4 / LAMA_NT;  // activation runs per thread
+    static_assert(NPX == 64 || NPX == 128, "64 or 128 pixels per tile");
+    static_assert(WITER * LAMA_NT * 4 == 64 * KC && XITER * LAMA_NT * 4 == KC * NPX, "whole float4 slots");
     static_assert(KC % 8 == 0 && WSTR % 8 == 4 && HALF % 64 == 32, "bank placement");
 };
 
@@ -307,9 +311,9 @@ __device__ __forceinline__ void pw_make_slots(PwSlots<C> &sl, const ConvSeg &sg,
     }
 #pragma unroll
     for (int it = 0; it < C::XITER; ++it) {
-        const int idx = tid + it * LAMA_NT, ci = idx / 16, q = idx % 16;
+        const int idx = tid + it * LAMA_NT, ci = idx / (C::NPX / 4), q = idx % (C::NPX / 4);
         sl.xc[it] = ci;
-        sl.xl[it] = (ci / (C::KC / 2)) * C::HALF + (ci % (C::KC / 2)) * 64 + 4 * q;
+        sl.xl[it] = (ci / (C::KC / 2)) * C::HALF + (ci % (C::KC / 2)) * C::NPX + 4 * q;
         // runs past the plane read the last whole run (VEC) or clamp per element
         sl.xp[it] = C::VEC ? min(ox0 + 4 * q, N - 4) : ox0 + 4 * q;
         sl.xo[it] = 4u * (unsigned)(ci * N + sl.xp[it]);
@@ -332,7 +336,7 @@ __device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &
     const int c0 = ck * C::KC, clast = sg.C - 1 - c0;  // channels past C read a valid plane (zero weights)
     const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * N;
     // VEC: runs of channels past C (zero weights) read the source's last run
-    const unsigned vlast = 4u * ((unsigned)(sg.C - c0) * (unsigned)N - 4u);
+    const unsigned vlast = 4u * ((unsigned)min(sg.C - c0, C::KC) * (unsigned)N - 4u);
 #pragma unroll
     for (int it = 0; it < C::XITER; ++it) {
         if constexpr (C::VEC) {
@@ -363,25 +367,30 @@ __device__ __forceinline__ void pw_store_chunk(const PwStage<C> &st, const PwSlo
 }
 
 template <class C>
-__device__ __forceinline__ void pw_compute_chunk(f32x16 &acc, const float *lds)
+__device__ __forceinline__ void pw_compute_chunk(f32x16 (&acc)[C::NACC], const float *lds)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
     constexpr int H = C::KC / 2;
     const float *wrow = lds + (wm * 32 + j) * C::WSTR + g * H;
-    const float *xrow = lds + C::W_LDS + g * C::HALF + wn * 32 + j;
-    float a[H], b[H];
+    const float *xrow = lds + C::W_LDS + g * C::HALF + wn * (C::NPX / 2) + j;
+    float a[H];
     lds_vec<H>(a, wrow);
 #pragma unroll
-    for (int c = 0; c < H; ++c) b[c] = xrow[c * 64];
+    for (int h = 0; h < C::NACC; ++h) {
+        float b[H];
 #pragma unroll
-    for (int c = 0; c < H; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c], b[c], acc, 0, 0, 0);
+        for (int c = 0; c < H; ++c) b[c] = xrow[c * C::NPX + h * 32];
+#pragma unroll
+        for (int c = 0; c < H; ++c) acc[h] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c], b[c], acc[h], 0, 0, 0);
+    }
 }
 
 // The K loop of a pointwise segment: two LDS stages, two register stages,
 // one barrier per chunk (the schedule of run_segment).
 template <class C>
-__device__ __forceinline__ void run_segment_pw(f32x16 &acc, const ConvSeg &sg_mem, int m0, int M, int ox0, float *lds)
+__device__ __forceinline__ void run_segment_pw(f32x16 (&acc)[C::NACC], const ConvSeg &sg_mem, int m0, int M, int ox0,
+                                               float *lds)
 {
     const ConvSeg sg = sg_mem;  // held in registers across the barriers
     const int n = sg.nchunk;
@@ -508,10 +517,7 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    if constexpr (C0::PW)
-        run_segment_pw<C0>(acc, P.s0, m0, P.M, ox0, lds);
-    else
-        run_segment<C0, NBUF>(acc, P.s0, m0, P.M, oy0, ox0, lds);
+    run_segment<C0, NBUF>(acc, P.s0, m0, P.M, oy0, ox0, lds);
     if constexpr (SEG1) {
         using C1 = Cfg<1, 1, 1, false, C0::KC, C0::TR, C0::TC>;
         if (P.s1.nchunk > 0) run_segment<C1, NBUF>(acc, P.s1, m0, P.M, oy0, ox0, lds);
@@ -519,6 +525,39 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
     if (threadIdx.x < 192) epl[threadIdx.x] = ep;
     __syncthreads();
     epilogue<C0::TR, C0::TC, PREFETCH>(acc, pre, P, epl, m0, oy0, ox0);
+}
+
+// One 64 x NPX tile of a pointwise problem (a flat plane: OH == 1).  The
+// epilogue runs once per 32-pixel accumulator; shifting its tile origin by
+// wn*(NPX/2 - 32) + h*32 places accumulator h of wave column wn.
+template <class C, bool PREFETCH>
+__device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds, float *epl)
+{
+    const int mb = b % P.mblocks, t = b / P.mblocks;
+    const int m0 = mb * 64, ox0 = t * C::NPX;
+    const int wn = (threadIdx.x >> 6) & 1;
+    const float ep = epi_param_load(P, m0);
+    EpiPre pre[C::NACC];
+#pragma unroll
+    for (int h = 0; h < C::NACC; ++h) {
+        if constexpr (PREFETCH) {
+            epilogue_prefetch<1, 64>(pre[h], P, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pre[h].add[r] = pre[h].res[r] = 0.f;
+        }
+    }
+    f32x16 acc[C::NACC];
+#pragma unroll
+    for (int h = 0; h < C::NACC; ++h)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[h][r] = 0.f;
+    run_segment_pw<C>(acc, P.s0, m0, P.M, ox0, lds);
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < C::NACC; ++h)
+        epilogue<1, 64, PREFETCH>(acc[h], pre[h], P, epl, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
 }
 
 __device__ __forceinline__ int find_problem(const ConvProblem *probs, int nprob, int &b)
@@ -575,27 +614,26 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 }
 
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
-// conv).  lama_conv1x1 needs 16-byte aligned planes with N % 4 == 0;
-// lama_conv1x1_s takes any N.
-#define LAMA_PW_KERNEL(NAME, VEC, PREFETCH)                                                                 \
+// conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
+// N % 4 == 0; lama_conv1x1_s takes any N.
+#define LAMA_PW_KERNEL(NAME, KC, VEC, NPX, PREFETCH)                                                        \
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, int nprob) \
     {                                                                                                       \
         side_priority();                                                                                    \
-        using C = PwCfg<LAMA_PW_KC, VEC>;                                                                           \
+        using C = PwCfg<KC, VEC, NPX>;                                                                      \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \
         int pi = find_problem(probs, nprob, b);                                                             \
-        conv_tile<C, false, 2, PREFETCH>(probs[pi], b, lds, epl);                                           \
+        pw_tile<C, PREFETCH>(probs[pi], b, lds, epl);                                                       \
     }
-LAMA_PW_KERNEL(lama_conv1x1, true, false)
-LAMA_PW_KERNEL(lama_conv1x1_s, false, false)
+LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, true, 64, false)
+LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, false, 64, false)
 
-// The same with addend / residual fetched before the K loop (the
-// SpectralTransform conv2, whose epilogue adds the l2g partial and the
-// residual).
-LAMA_PW_KERNEL(lama_conv1x1_res, true, true)
-LAMA_PW_KERNEL(lama_conv1x1_res_s, false, true)
+// The SpectralTransform conv2, whose epilogue adds the l2g partial and the
+// residual (fetched before the K loop).
+LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, true, 64, true)
+LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, false, 64, true)
 #undef LAMA_PW_KERNEL
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions

@@ -457,16 +457,29 @@ void Engine::push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int st
     }
 }
 
+// Input shapes the plan supports: multiples of 8, and at most 2^27 pixels --
+// the convolution kernels address one K chunk (at most 8 channels of a
+// full-resolution plane) with 32-bit byte offsets, 32 * h * w < 2^32.
+static bool shape_ok(int h, int w, std::string &err)
+{
+    if (h < 8 || w < 8 || h % 8 || w % 8) {
+        err = "input " + std::to_string(w) + "x" + std::to_string(h) + " is not a multiple of 8 (the caller pads)";
+        return false;
+    }
+    if ((size_t)h * w > ((size_t)1 << 27)) {
+        err = "input " + std::to_string(w) + "x" + std::to_string(h) + " exceeds 2^27 pixels, the largest this engine plans";
+        return false;
+    }
+    return true;
+}
+
 Plan *Engine::plan_for(int h, int w, std::string &err)
 {
     if (!have_weights_) {
         err = "no weights loaded";
         return nullptr;
     }
-    if (h < 8 || w < 8 || h % 8 || w % 8) {
-        err = "input " + std::to_string(w) + "x" + std::to_string(h) + " is not a multiple of 8 (the caller pads)";
-        return nullptr;
-    }
+    if (!shape_ok(h, w, err)) return nullptr;
     auto key = std::make_pair(h, w);
     auto it = plans_.find(key);
     if (it != plans_.end()) return &it->second;
@@ -516,10 +529,7 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
 
 bool Engine::plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::string &err)
 {
-    if (h < 8 || w < 8 || h % 8 || w % 8) {
-        err = "input size must be a multiple of 8 and at least 8";
-        return false;
-    }
+    if (!shape_ok(h, w, err)) return false;
     auto it = plans_.find({h, w});
     weights = warena_bytes_;
     if (it != plans_.end()) {
@@ -1090,6 +1100,10 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
     const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : 8;
+    if ((size_t)4 * KC * h * w >= ((size_t)1 << 32)) {  // 32-bit staging offsets within a K chunk
+        err = "op_conv2d: plane too large";
+        return false;
+    }
     Arena A;
     const int T = k * k;
     Packed pk = pack(A, cout, cin, T, KC, [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; });

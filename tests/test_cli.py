@@ -209,3 +209,13 @@ def test_plan_bytes_is_the_allocated_arena(pkg, engine):
     engine.forward(x)
     actual, _ = engine.plan_bytes(136, 200)
     assert predicted == actual > 0 and weights > 200e6
+
+
+@pytest.mark.gpu
+def test_plan_rejects_unsupported_shapes(pkg, engine):
+    # not padded to 8 (the caller pads, main.rs:241-242), and beyond the 2^27-pixel
+    # bound of the kernels' 32-bit staging offsets
+    for h, w, msg in [(100, 64, "multiple of 8"), (16384, 8200, "2\\^27 pixels")]:
+        with pytest.raises(pkg.hip_engine.HipError, match=msg):
+            engine.plan_bytes(h, w)
+    assert engine.plan_bytes(8192, 16384)[0] > 0  # exactly 2^27 pixels plans
