@@ -11,6 +11,17 @@
 #define LAMA_PW_KC 32
 #endif
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
+
+// Complex values per ping-pong buffer of the single-block FFT kernels: the
+// row-pair layout [(h+1)/2][w] or the half spectrum [h][w/2+1], rounded up to
+// even so the second buffer is 16-byte aligned.  (Padding the rows against
+// bank conflicts would cost LDS: at 512x512 a plane's 34 KB must stay within
+// what two FFC GEMM workgroups leave free on a CU -- 37 KB measured slower.)
+static inline constexpr int lama_fft_nb(int h, int w)
+{
+    const int a = (h + 1) / 2 * w, b = h * (w / 2 + 1);
+    return ((a > b ? a : b) + 1) & ~1;
+}
 #define LAMA_TAIL_ROWS 8 // output tile of the 7x7 tail kernel (rows x columns)
 #define LAMA_TAIL_COLS 64
 

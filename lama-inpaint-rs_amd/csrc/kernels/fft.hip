@@ -163,8 +163,16 @@ __device__ __forceinline__ void pass_fixed(const Pass &P)
         dft<R>(v, P.sign);
         float2 *dst = P.out + (long)b * P.bstride;
         const int base = (j / P.Ns) * P.Ns * R + k;
+        if (R % 2 == 0 && P.Ns == 1 && P.estride == 1 && (P.bstride & 1) == 0) {
+            // first pass of a row transform: the R outputs are adjacent, so
+            // store them as 16-byte pairs (fewer, wider LDS writes)
 #pragma unroll
-        for (int r = 0; r < R; ++r) dst[(base + r * P.Ns) * P.estride] = v[r];
+            for (int r = 0; r < R; r += 2)
+                *reinterpret_cast<float4 *>(dst + base + r) = make_float4(v[r].x, v[r].y, v[r + 1].x, v[r + 1].y);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) dst[(base + r * P.Ns) * P.estride] = v[r];
+        }
     }
 }
 
@@ -249,7 +257,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
-    const int NB = max(HP * W, H * Wh);
+    const int NB = lama_fft_nb(H, W);
     float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
     // Prologue: every global load (the twiddle entry, this block's plane) is
     // issued before the first LDS write; the host keeps this kernel to planes
@@ -327,7 +335,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
-    const int NB = max(HP * W, H * Wh);
+    const int NB = lama_fft_nb(H, W);
     float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
     // Prologue: the twiddle entry, this block's spectrum (at most
     // LAMA_FFT_NT * 8 values per plane, as the host guarantees) and the `f +`

@@ -233,8 +233,14 @@ bool Engine::open(std::string &err)
     if (!check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err) ||
         !check(hip_->hipStreamCreate(&side_), "hipStreamCreate", err))
         return false;
+    // The cross-stream events only order work between this device's two
+    // streams: no system-scope fence (a host-visible cache write-back at each
+    // record costs microseconds on the critical path).
+#ifndef LAMA_EV_FLAGS
+#define LAMA_EV_FLAGS (hipEventDisableTiming | hipEventDisableSystemFence)
+#endif
     for (auto &e : ev_)
-        if (!check(hip_->hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate", err)) return false;
+        if (!check(hip_->hipEventCreateWithFlags(&e, LAMA_EV_FLAGS), "hipEventCreate", err)) return false;
     return true;
 }
 
@@ -397,7 +403,7 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
     const int Wh = W / 2 + 1, HP = (H + 1) / 2;
     const size_t f2 = 8;  // bytes per complex value
     g = FftGeom{};
-    g.lds = (2 * std::max((size_t)HP * W, (size_t)H * Wh) + H + W) * f2;
+    g.lds = (2 * (size_t)lama_fft_nb(H, W) + H + W) * f2;
     const char *env = getenv("LAMA_FFT_SPLIT");
     const bool force = env && atoi(env) == 1;
     // the single-block kernels fetch at most 8 plane values per thread

@@ -73,7 +73,9 @@ def test_conv_transpose(engine, cin, cout, h, w):
     assert rel_err(got, ref) < TOL
 
 
-SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), (64, 33), (16, 12), (38, 19)]
+# (64, 64), (32, 32), (33, 96), (31, 32): padded row-pair stride, odd row counts
+SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), (64, 33), (16, 12), (38, 19),
+         (33, 96), (31, 32)]
 
 
 # planes too large for one block's LDS take the row/column split launches
