@@ -39,20 +39,32 @@ struct Cfg {
     static constexpr int PC = (TC - 1) * S + KW;
     static constexpr int WK = T * KC;
     static constexpr int WSTR = WK + ((12 - WK % 8) % 8);  // = 4 (mod 8)
-    // patch pixel stride: the 16-byte per-lane reads of 16 lanes land on
-    // distinct banks
-    static constexpr int KCP = KC + 4;
+    // patch pixel stride: the 16-byte (KC = 8) or 8-byte (KC = 4) per-lane
+    // operand reads of neighbouring lanes land on distinct banks
+    static constexpr int KCP = (KC / 2) % 4 == 0 ? KC + 4 : KC + 2;
+    // Patch columns: stride-2 convolutions keep even and odd input columns in
+    // two halves of a row (HPC each), so the operand reads of neighbouring
+    // output pixels -- two input columns apart -- are one pixel apart in LDS.
+    static constexpr int HPC = (PC + 1) / 2;
+    static constexpr int PCP = S == 2 ? 2 * HPC : PC;  // LDS pixels per patch row
+    static __device__ __forceinline__ constexpr int col(int c) { return S == 2 ? (c & 1) * HPC + (c >> 1) : c; }
     static constexpr int W4 = 64 * WK / 4;
     static constexpr int WITER = (W4 + LAMA_NT - 1) / LAMA_NT;
-    static constexpr int P_ELEM = KC * PR * PC;
-    static constexpr int PITER = (P_ELEM + LAMA_NT - 1) / LAMA_NT;
+    // Patch staging: each 64-lane group takes 16 consecutive pixels x 4
+    // consecutive channels (pixel fastest), so a wave's loads are 64-byte runs
+    // and its 4-byte LDS stores, at pixel stride KCP, cover every bank once.
+    static constexpr int NPIX = PR * PC;
+    static constexpr int NPB = (NPIX + 15) / 16;            // 16-pixel blocks
+    static constexpr int P_SLOTS = NPB * 16 * KC;
+    static constexpr int PITER = (P_SLOTS + LAMA_NT - 1) / LAMA_NT;
     // staging is branch-free: slots past the data land in a dummy tail
     static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT - W4) * 4;
-    static constexpr int P_LDS = PR * PC * KCP + (PITER * LAMA_NT - P_ELEM);
+    static constexpr int P_LDS = PR * PCP * KCP + 64;
     static constexpr int LDS = W_LDS + P_LDS;
     static_assert(TR * TC == 64, "pixel tile must hold 64 pixels");
     static_assert(KC % 4 == 0, "KC must be a multiple of 4");
     static_assert((KC / 2) % 4 != 0 || KCP % 4 == 0, "b128 operand reads need 16-byte pixel stride");
+    static_assert(S == 1 || S == 2, "stride 1 or 2");
 };
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -96,11 +108,12 @@ __device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int 
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) {
         const int idx = tid + it * LAMA_NT;
-        const int cl = idx / (C::PR * C::PC);
-        const int rem = idx - cl * (C::PR * C::PC);
-        const int r = rem / C::PC, c = rem - r * C::PC;
+        const int q = idx >> 6, l = idx & 63;  // 64-slot group: 16 pixels x 4 channels
+        const int cl = (q % (C::KC / 4)) * 4 + (l >> 4);
+        const int pix = (q / (C::KC / 4)) * 16 + (l & 15);
+        const int r = min(pix, C::NPIX - 1) / C::PC, c = min(pix, C::NPIX - 1) - r * C::PC;
         const int iy = oy0 * C::S - C::PAD + r, ix = ox0 * C::S - C::PAD + c;
-        const bool in = idx < C::P_ELEM;
+        const bool in = idx < C::P_SLOTS && pix < C::NPIX;
         bool zero = false;
         int g;
         if (C::REFLECT) {
@@ -109,7 +122,7 @@ __device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int 
             zero = !(iy >= 0 && ix >= 0 && iy < sg.IH && ix < sg.IW);
             g = zero ? 0 : iy * sg.IW + ix;
         }
-        sl.pl[it] = in ? (r * C::PC + c) * C::KCP + cl : C::PR * C::PC * C::KCP + (idx - C::P_ELEM);
+        sl.pl[it] = in ? (r * C::PCP + C::col(c)) * C::KCP + cl : C::PR * C::PCP * C::KCP + l;
         sl.po[it] = 4u * (unsigned)(min(cl, C::KC - 1) * sg.IH * sg.IW + g);
         sl.pc[it] = (in && !zero) ? cl : -1;
     }
@@ -191,7 +204,7 @@ __device__ __forceinline__ void compute_chunk(f32x16 &acc, const float *wl, cons
     const int p = wn * 32 + j;
     const int pr = p / C::TC, pc = p % C::TC;
     const float *wrow = wl + (wm * 32 + j) * C::WSTR + g * (C::KC / 2);
-    const float *prow = pl + ((pr * C::S) * C::PC + pc * C::S) * C::KCP + g * (C::KC / 2);
+    const float *prow = pl + ((pr * C::S) * C::PCP + C::col(pc * C::S)) * C::KCP + g * (C::KC / 2);
     constexpr int H = C::KC / 2;
     float a[2][H], b[2][H];
     lds_vec<H>(a[0], wrow);
@@ -202,7 +215,7 @@ __device__ __forceinline__ void compute_chunk(f32x16 &acc, const float *wl, cons
         if (t + 1 < C::T) {
             const int ky = (t + 1) / C::KW, kx = (t + 1) % C::KW;
             lds_vec<H>(a[cur ^ 1], wrow + (t + 1) * C::KC);
-            lds_vec<H>(b[cur ^ 1], prow + (ky * C::PC + kx) * C::KCP);
+            lds_vec<H>(b[cur ^ 1], prow + (ky * C::PCP + C::col(kx)) * C::KCP);
         }
 #pragma unroll
         for (int c = 0; c < H; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][c], b[cur][c], acc, 0, 0, 0);
