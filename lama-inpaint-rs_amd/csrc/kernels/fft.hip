@@ -573,3 +573,222 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const
         d[idx] = ((y & 1) ? v.y : v.x) * A.scale + f[idx];
     }
 }
+
+// ---- compile-time shapes: square power-of-two planes -------------------------
+//
+// The bottleneck planes of 256x256 and 512x512 inputs (32x32, 64x64) use the
+// single-block algorithm above with every length, count and stride a
+// compile-time constant, so no index arithmetic is left in the kernels but
+// shifts, masks and a multiply-high by the constant W/2+1.  This matters
+// beside the FFC GEMM: its FP32 MFMAs hold the SIMDs' math pipes, and every
+// VALU instruction of these kernels then waits its turn, so the runtime
+// integer divisions of the generic path (about half of its instructions)
+// cost more than the butterflies themselves.  The radix plan is 8 first,
+// then one 4 or 2 (64 = 8*8, 32 = 8*4); power-of-two lengths use the sign
+// -1 forward, +1 inverse.
+
+namespace {
+
+template <int N, int R, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
+__device__ __forceinline__ void ct_pass(const float2 *in, float2 *out, const float2 *tw)
+{
+    constexpr int M = N / R, TWSTEP = N / (NS * R), TOTAL = COUNT * M;
+#pragma unroll
+    for (int it = 0; it < (TOTAL + LAMA_FFT_NT - 1) / LAMA_FFT_NT; ++it) {
+        const int idx = threadIdx.x + it * LAMA_FFT_NT;
+        if (TOTAL % LAMA_FFT_NT != 0 && idx >= TOTAL) break;
+        // rows: a transform's butterflies on neighbouring lanes; columns:
+        // neighbouring transforms on neighbouring lanes
+        const int b = ESTRIDE == 1 ? idx / M : idx % COUNT;
+        const int j = ESTRIDE == 1 ? idx % M : idx / COUNT;
+        const int k = j % NS;
+        const float2 *src = in + b * BSTRIDE;
+        float2 v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float2 x = src[(j + r * M) * ESTRIDE];
+            if (NS > 1 && r > 0) x = cmul(x, twd(tw, k * r * TWSTEP, SIGN));
+            v[r] = x;
+        }
+        dft<R>(v, SIGN);
+        float2 *dst = out + b * BSTRIDE;
+        const int base = (j / NS) * NS * R + k;
+        if (NS == 1 && ESTRIDE == 1) {
+#pragma unroll
+            for (int r = 0; r < R; r += 2)
+                *reinterpret_cast<float4 *>(dst + base + r) = make_float4(v[r].x, v[r].y, v[r + 1].x, v[r + 1].y);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) dst[(base + r * NS) * ESTRIDE] = v[r];
+        }
+    }
+}
+
+// All passes of a length-N transform; returns the buffer holding the result.
+template <int N, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
+__device__ __forceinline__ float2 *ct_stockham(float2 *a, float2 *b, const float2 *tw)
+{
+    if constexpr (NS >= N) {
+        return a;
+    } else {
+        constexpr int REM = N / NS, R = REM % 8 == 0 ? 8 : REM % 4 == 0 ? 4 : 2;
+        ct_pass<N, R, NS, COUNT, BSTRIDE, ESTRIDE, SIGN>(a, b, tw);
+        __syncthreads();
+        return ct_stockham<N, NS * R, COUNT, BSTRIDE, ESTRIDE, SIGN>(b, a, tw);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void ct_twiddles(const FftArgs &A, float2 *twr, float2 *twc, float2 &v)
+{
+    // both tables (row then column, N entries each): one entry per thread
+    const int t = threadIdx.x;
+    if (t < 2 * N) (t < N ? twr[t] : twc[t - N]) = v;
+}
+
+template <int N>
+__device__ __forceinline__ float2 ct_twiddle_fetch(const FftArgs &A)
+{
+    const int t = min((int)threadIdx.x, 2 * N - 1);
+    const LAMA_GLOBAL float2 *p = t < N ? gp(reinterpret_cast<const float2 *>(A.row.tw)) + t
+                                        : gp(reinterpret_cast<const float2 *>(A.col.tw)) + (t - N);
+    return *p;
+}
+
+template <int N>
+__device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
+{
+    constexpr int H = N, W = N, Wh = N / 2 + 1, HP = N / 2, NB = lama_fft_nb(N, N), NT = LAMA_FFT_NT;
+    static_assert(2 * N <= NT && HP * W / 4 <= 2 * NT, "one twiddle and at most two quads per thread");
+    float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
+    const int c = blockIdx.x;
+    // prologue: every global load before the first LDS write
+    float2 tv = ct_twiddle_fetch<N>(A);
+    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
+    constexpr int W4 = W / 4, NQ = HP * W4, RQ = (NQ + NT - 1) / NT;
+    float4 qa[RQ], qb[RQ];
+#pragma unroll
+    for (int k = 0; k < RQ; ++k) {
+        const int q = min((int)threadIdx.x + k * NT, NQ - 1), p = q / W4, x = (q % W4) * 4;
+        qa[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
+        qb[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
+    }
+    ct_twiddles<N>(A, twr, twc, tv);
+#pragma unroll
+    for (int k = 0; k < RQ; ++k) {
+        const int q = threadIdx.x + k * NT;
+        if (NQ % NT != 0 && q >= NQ) break;
+        const int p = q / W4, x = (q % W4) * 4;
+        float2 *d = b0 + p * W + x;
+        d[0] = make_float2(qa[k].x, qb[k].x);
+        d[1] = make_float2(qa[k].y, qb[k].y);
+        d[2] = make_float2(qa[k].z, qb[k].z);
+        d[3] = make_float2(qa[k].w, qb[k].w);
+    }
+    __syncthreads();
+    float2 *r = ct_stockham<W, 1, HP, W, 1, -1>(b0, b1, twr);
+    float2 *o = r == b0 ? b1 : b0;
+    // split each row pair into the two half spectra
+    for (int idx = threadIdx.x; idx < H * Wh; idx += NT) {
+        const int y = idx / Wh, k = idx % Wh, p = y >> 1;
+        const float2 z = r[p * W + k], zm = r[p * W + ((W - k) & (W - 1))];
+        o[idx] = (y & 1) ? make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x))
+                         : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+    }
+    __syncthreads();
+    float2 *q = ct_stockham<H, 1, Wh, 1, Wh, -1>(o, r, twc);
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh, *dim = dre + H * Wh;
+    for (int idx = threadIdx.x; idx < H * Wh; idx += NT) {
+        const float2 v = q[idx];
+        dre[idx] = v.x * A.scale;
+        dim[idx] = v.y * A.scale;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
+{
+    constexpr int H = N, W = N, Wh = N / 2 + 1, HP = N / 2, NB = lama_fft_nb(N, N), NT = LAMA_FFT_NT;
+    constexpr int N4 = H * W / 4, FP = (N4 + NT - 1) / NT, NS = H * Wh, RS = (NS + NT - 1) / NT;
+    static_assert(2 * N <= NT && FP <= 2 && RS <= 8, "prologue register budget");
+    float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
+    const int c = blockIdx.x;
+    // prologue: twiddles, this block's spectrum and the `f +` addend
+    float2 tv = ct_twiddle_fetch<N>(A);
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + H * Wh;
+    const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.feat) + (long)c * H * W);
+    float4 fpre[FP];
+#pragma unroll
+    for (int k = 0; k < FP; ++k) fpre[k] = f4[min((int)threadIdx.x + k * NT, N4 - 1)];
+    float re[RS], im[RS];
+#pragma unroll
+    for (int k = 0; k < RS; ++k) {
+        const int idx = min((int)threadIdx.x + k * NT, NS - 1);
+        re[k] = sre[idx];
+        im[k] = sim[idx];
+    }
+    ct_twiddles<N>(A, twr, twc, tv);
+#pragma unroll
+    for (int k = 0; k < RS; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        if (idx >= NS) break;
+        b0[idx] = make_float2(re[k], im[k]);
+    }
+    __syncthreads();
+    float2 *r = ct_stockham<H, 1, Wh, 1, Wh, 1>(b0, b1, twc);
+    float2 *o = r == b0 ? b1 : b0;
+    // Hermitian rows, two per complex transform: z = Ga + i Gb
+    for (int idx = threadIdx.x; idx < HP * W; idx += NT) {
+        const int p = idx / W, x = idx % W;
+        float2 g[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int y = 2 * p + h;
+            float2 v;
+            if (x < Wh) {
+                v = r[y * Wh + x];
+                if (x == 0 || 2 * x == W) v.y = 0.f;
+            } else {
+                v = r[y * Wh + (W - x)];
+                v.y = -v.y;
+            }
+            g[h] = v;
+        }
+        o[idx] = make_float2(g[0].x - g[1].y, g[0].y + g[1].x);
+    }
+    __syncthreads();
+    float2 *q = ct_stockham<W, 1, HP, W, 1, 1>(o, r, twr);
+    LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + (long)c * H * W);
+#pragma unroll
+    for (int k = 0; k < FP; ++k) {
+        const int i4 = threadIdx.x + k * NT;
+        if (N4 % NT != 0 && i4 >= N4) break;
+        const int idx = i4 * 4, y = idx / W, x = idx % W;
+        const float2 *v = q + (y >> 1) * W + x;
+        float4 o4 = (y & 1) ? make_float4(v[0].y, v[1].y, v[2].y, v[3].y) : make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
+        o4.x = o4.x * A.scale + fpre[k].x;
+        o4.y = o4.y * A.scale + fpre[k].y;
+        o4.z = o4.z * A.scale + fpre[k].z;
+        o4.w = o4.w * A.scale + fpre[k].w;
+        d4[i4] = o4;
+    }
+}
+
+}  // namespace
+
+#define LAMA_FFT_CT(N)                                                                                          \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_##N(const FftArgs *__restrict__ args)  \
+    {                                                                                                           \
+        side_priority();                                                                                        \
+        extern __shared__ float2 sm[];                                                                          \
+        rfft2_ct<N>(*args, sm);                                                                                 \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_##N(const FftArgs *__restrict__ args) \
+    {                                                                                                           \
+        side_priority();                                                                                        \
+        extern __shared__ float2 sm[];                                                                          \
+        irfft2_ct<N>(*args, sm);                                                                                \
+    }
+LAMA_FFT_CT(64)
+LAMA_FFT_CT(32)
+#undef LAMA_FFT_CT

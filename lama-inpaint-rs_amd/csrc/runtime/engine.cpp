@@ -54,6 +54,9 @@ const char *const kSplitName[4] = {"lama_rfft2_rows", "lama_rfft2_cols", "lama_i
 // whose length is not a multiple of 4 or that are not 16-byte aligned.
 const char *const kPwAnyName[2] = {"lama_conv1x1_s", "lama_conv1x1_res_s"};
 
+// Single-block FFT kernels with the plane shape fixed at compile time.
+const char *const kFftCtName[2][2] = {{"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}};
+
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 void tile_shape(int family, int &tr, int &tc)
 {
@@ -225,6 +228,10 @@ bool Engine::open(std::string &err)
         if (!check(hip_->hipModuleGetFunction(&fn_split_[f], module_, kSplitName[f]), kSplitName[f], err)) return false;
     for (int f = 0; f < 2; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err)) return false;
+    for (int s = 0; s < 2; ++s)
+        for (int f = 0; f < 2; ++f)
+            if (!check(hip_->hipModuleGetFunction(&fn_fft_ct_[s][f], module_, kFftCtName[s][f]), kFftCtName[s][f], err))
+                return false;
     {
         int lds = 0;
         if (hip_->hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_) == hipSuccess && lds > 0)
@@ -410,6 +417,10 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
     const bool fits = std::max((size_t)HP * W, (size_t)H * Wh) <= 8 * (size_t)LAMA_FFT_NT;
     if (!force && fits && g.lds <= std::min<size_t>(max_lds_, 64 * 1024)) {
         g.grid_rows = g.grid_cols = (unsigned)C;  // one block per plane
+        // square 64 or 32 planes have kernels with the shape compiled in
+        // (LAMA_FFT_GENERIC=1 keeps the runtime-shaped ones, for tests)
+        const char *gen = getenv("LAMA_FFT_GENERIC");
+        if (H == W && (H == 64 || H == 32) && !(gen && atoi(gen) == 1)) g.ct = H;
         return true;
     }
     // complex values the two ping-pong buffers may hold next to the twiddles
@@ -446,7 +457,7 @@ void Engine::push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int st
     L.nparams = 1;
     L.step_end = -1;
     if (!g.split) {
-        L.fn = fn_[L.family];
+        L.fn = g.ct ? fn_fft_ct_[g.ct == 64 ? 0 : 1][inverse ? 1 : 0] : fn_[L.family];
         L.grid = g.grid_rows;
         L.shmem = (unsigned)g.lds;
         L.bytes = bytes_a + bytes_b;

@@ -59,6 +59,7 @@ struct FftGeom {
     size_t lds_rows = 0, lds_cols = 0;
     unsigned grid_rows = 0, grid_cols = 0;
     size_t tmp_bytes = 0;           // interleaved complex [C][H][W/2+1]
+    int ct = 0;                     // single-block square plane with compile-time kernels (32 or 64), else 0
 };
 
 struct ArenaLayout {
@@ -137,6 +138,7 @@ private:
     // split-mode FFT kernels: rfft2 rows, rfft2 cols, irfft2 cols, irfft2 rows
     hipFunction_t fn_split_[4] = {};
     hipFunction_t fn_pw_any_[2] = {};  // 1x1 kernels for planes that are not float4-aligned
+    hipFunction_t fn_fft_ct_[2][2] = {};  // [64x64, 32x32][rfft2, irfft2]
     hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr;

@@ -113,6 +113,23 @@ def test_forward_split_forced_matches_single(pkg, engine, monkeypatch):
     assert rel_err(b, a) < 1e-5
 
 
+@pytest.mark.parametrize("size", [256, 512])
+def test_compiled_shape_fft_equals_generic(pkg, engine, monkeypatch, size):
+    """The 32x32 / 64x64 bottleneck planes (256 and 512 inputs) use FFT kernels
+    with the shape compiled in; they run the same radix plan as the
+    runtime-shaped kernels (LAMA_FFT_GENERIC=1), so the whole forward agrees to
+    float rounding (the compiler contracts a few multiply-adds differently)."""
+    img, mask = _case(pkg, size, size, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    a = engine.forward(x)
+    monkeypatch.setenv("LAMA_FFT_GENERIC", "1")
+    eng2 = pkg.hip_engine.Engine()
+    eng2.load_weights(engine._store)
+    b = eng2.forward(x)
+    eng2.close()
+    assert rel_err(b, a) < 1e-5
+
+
 def test_forward_2048_whole_image(pkg, engine):
     """configs[4] at its full size (bottleneck 512 x 256 x 256): checked by
     size-independent properties -- finite, bitwise repeatable, sigmoid range,

@@ -82,19 +82,23 @@ SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), 
 LARGE = [(256, 256), (200, 130), (150, 90)]
 
 
-@pytest.fixture(params=["single", "split"])
+@pytest.fixture(params=["single", "split", "generic"])
 def fft_mode(request, monkeypatch):
-    """'split' forces the row/column launches (LAMA_FFT_SPLIT=1) at every size."""
+    """'split' forces the row/column launches (LAMA_FFT_SPLIT=1) at every size;
+    'generic' keeps the runtime-shaped single-block kernels where a kernel with
+    the plane shape compiled in exists (32x32, 64x64; LAMA_FFT_GENERIC=1)."""
+    monkeypatch.delenv("LAMA_FFT_SPLIT", raising=False)
+    monkeypatch.delenv("LAMA_FFT_GENERIC", raising=False)
     if request.param == "split":
         monkeypatch.setenv("LAMA_FFT_SPLIT", "1")
-    else:
-        monkeypatch.delenv("LAMA_FFT_SPLIT", raising=False)
+    elif request.param == "generic":
+        monkeypatch.setenv("LAMA_FFT_GENERIC", "1")
     return request.param
 
 
 @pytest.mark.parametrize("h,w", SIZES + LARGE)
 def test_rfft2(engine, fft_mode, h, w):
-    if fft_mode == "single" and (h, w) in LARGE:
+    if fft_mode != "split" and (h, w) in LARGE:
         pytest.skip("large planes always split")
     rng = np.random.default_rng(h * 100 + w)
     c = 3
@@ -107,7 +111,7 @@ def test_rfft2(engine, fft_mode, h, w):
 
 @pytest.mark.parametrize("h,w", SIZES + LARGE)
 def test_irfft2(engine, fft_mode, h, w):
-    if fft_mode == "single" and (h, w) in LARGE:
+    if fft_mode != "split" and (h, w) in LARGE:
         pytest.skip("large planes always split")
     rng = np.random.default_rng(h * 100 + w + 1)
     c = 3
