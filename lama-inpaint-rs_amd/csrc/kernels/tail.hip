@@ -4,9 +4,10 @@
 // With only three output channels an MFMA tile would be >90% padding, so this
 // is VALU work: a block covers 8 rows x 64 columns, each thread two adjacent
 // pixels x 3 channels (6 accumulators).  All 3 x Cin x 49 weights are staged
-// in LDS once (wave-uniform broadcast reads); per input channel the block
-// stages the reflect-padded 14 x 70 patch, its global loads issued one
-// channel ahead so they overlap the current channel's FMAs.
+// in LDS once, as [ci][ky][co][8] (kx padded to 8), so the 21 weights of one
+// kernel row are six wave-uniform 16-byte broadcast reads; per input channel
+// the block stages the reflect-padded 14 x 70 patch, its global loads issued
+// one channel ahead so they overlap the current channel's FMAs.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -22,7 +23,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
 {
     constexpr int PE = PR * PC, PK = (PE + LAMA_NT - 1) / LAMA_NT;  // patch elements per thread
     __shared__ float patch[2][PE];
-    __shared__ __attribute__((aligned(16))) float wl[3 * 64 * 49];
+    constexpr int WROW = 3 * 8;  // one (ci, ky): 3 output channels x 8 (7 taps + pad)
+    __shared__ __attribute__((aligned(16))) float wl[64 * 7 * WROW];
     const TailArgs &A = *args;
     const int H = A.H, W = A.W;
     const int tiles_x = (W + TCOLS - 1) / TCOLS;
@@ -55,20 +57,23 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
             if ((int)threadIdx.x + k * LAMA_NT < PE) dst[threadIdx.x + k * LAMA_NT] = nxt[k];
     };
 
-    // weights (3 x Cin x 49 <= 9408 floats), four float4 loads in flight per round
+    // weights [3][Cin][7][7] -> LDS [Cin][7][3][8], eight loads in flight per round
     {
-        const int nw = 3 * A.Cin * 49, n4 = nw >> 2;
-        const LAMA_GLOBAL float4 *w4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.wt));
+        const int nw = A.Cin * 7 * WROW, wstride = A.Cin * 49;
+        const LAMA_GLOBAL float *w = gp(A.wt);
         fetch(0);
-        for (int b = threadIdx.x; b < n4; b += 4 * LAMA_NT) {
-            float4 wv[4];
+        for (int b = threadIdx.x; b < nw; b += 8 * LAMA_NT) {
+            float wv[8];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) wv[k] = w4[min(b + k * LAMA_NT, n4 - 1)];
-            // lanes past the end rewrite the last float4 with the same value
+            for (int k = 0; k < 8; ++k) {
+                const int i = min(b + k * LAMA_NT, nw - 1), row = i / WROW, r = i - row * WROW;
+                const int co = r >> 3, kx = r & 7;  // row = ci * 7 + ky
+                wv[k] = w[co * wstride + row * 7 + min(kx, 6)];
+            }
+            // lanes past the end rewrite the last entry; kx == 7 is padding (never read)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) reinterpret_cast<float4 *>(wl)[min(b + k * LAMA_NT, n4 - 1)] = wv[k];
+            for (int k = 0; k < 8; ++k) wl[min(b + k * LAMA_NT, nw - 1)] = wv[k];
         }
-        for (int i = 4 * n4 + threadIdx.x; i < nw; i += LAMA_NT) wl[i] = gp(A.wt)[i];
     }
     put(patch[0]);
     // one barrier per channel: channel ci+1's loads are in flight during
@@ -77,18 +82,26 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
         if (ci + 1 < A.Cin) fetch(ci + 1);
         __syncthreads();
         const float *pp = patch[ci & 1] + tr * PC + tc;
-        const float *w0 = wl + ci * 49;
-        const int wstride = A.Cin * 49;
 #pragma unroll
         for (int ky = 0; ky < 7; ++ky) {
             float row[PX + 6];
 #pragma unroll
             for (int q = 0; q < PX + 6; ++q) row[q] = pp[ky * PC + q];
+            float wk[WROW];
+            const float4 *w4 = reinterpret_cast<const float4 *>(wl + (ci * 7 + ky) * WROW);
+#pragma unroll
+            for (int q = 0; q < WROW / 4; ++q) {
+                const float4 v = w4[q];
+                wk[4 * q] = v.x;
+                wk[4 * q + 1] = v.y;
+                wk[4 * q + 2] = v.z;
+                wk[4 * q + 3] = v.w;
+            }
 #pragma unroll
             for (int kx = 0; kx < 7; ++kx) {
 #pragma unroll
                 for (int co = 0; co < 3; ++co) {
-                    const float wv = w0[co * wstride + ky * 7 + kx];
+                    const float wv = wk[co * 8 + kx];
 #pragma unroll
                     for (int p = 0; p < PX; ++p) acc[co][p] += wv * row[p + kx];
                 }
