@@ -38,6 +38,9 @@ def main():
     ap.add_argument("--cpu-size", type=int, default=0, help="CPU sample size (default: the workload size)")
     ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "traffic_conv3x3_512.json"),
                     help="JSON with the measured HBM bytes per launch of the dominant kernel")
+    ap.add_argument("--sample-every", type=int, default=16,
+                    help="time the dominant kernel's launches (HIP events in the dispatch packets) on every "
+                         "N-th timed pass")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="MiB of one untimed device-to-device copy made before the warmup: the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -81,14 +84,14 @@ def main():
     eng.synchronize()
 
     # The dominant kernel is timed with HIP events on its own stream during the
-    # timed region, on every fourth pass (the events ride in the dispatch
-    # packets; sampling keeps their cost out of `value`).
+    # timed region, on every --sample-every-th pass (the events ride in the
+    # dispatch packets; sampling keeps their cost out of `value`).
     dom = "conv3x3"
     eng.profile_reset()
     eng.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        eng.profile([dom] if i % 4 == 0 else ())
+        eng.profile([dom] if i % args.sample_every == 0 else ())
         eng.forward_device(d_in, S, S, d_out)
     eng.synchronize()
     elapsed = time.perf_counter() - t0
