@@ -76,6 +76,16 @@ struct ConvSeg {
     int pad_;
 };
 
+// Second argument of the grouped conv kernels, by value: the first workgroup
+// of problems 1..3 (INT32_MAX where absent), so a workgroup finds its problem
+// without reading the descriptors' block counts first (that chain of
+// dependent scalar loads sat at the head of every workgroup's prologue).
+#define LAMA_MAX_PROBS 4
+struct alignas(16) ProbStarts {
+    int n;                       // number of problems (1..LAMA_MAX_PROBS)
+    int s[LAMA_MAX_PROBS - 1];   // first workgroup of problems 1, 2, ...
+};
+
 // One output problem: out[co][oy'][ox'] for co < M, (oy, ox) on the OH x OW
 // GEMM grid, stored at oy' = oy*oy_mul + oy_off, ox' = ox*ox_mul + ox_off
 // (the conv-transpose phases interleave four grids into one plane).
@@ -127,7 +137,10 @@ struct FftArgs {
 };
 
 // Sum of K-partials + BN + ReLU (+ residual) over [C][plane].
-#define LAMA_FIN_PARTS 5  // K partials of the FFC local GEMM: l2l, then g2l in four K ranges
+#ifndef LAMA_G2L_RANGES
+#define LAMA_G2L_RANGES 4  // K ranges of the FFC g2l GEMM (384 input channels)
+#endif
+#define LAMA_FIN_PARTS (1 + LAMA_G2L_RANGES)  // K partials of the FFC local GEMM: l2l, then g2l's K ranges
 struct FinalizeArgs {
     const float *part[LAMA_FIN_PARTS];
     int nparts, C;

@@ -573,13 +573,12 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
         epilogue<1, 64, PREFETCH>(acc[h], pre[h], P, epl, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
 }
 
-__device__ __forceinline__ int find_problem(const ConvProblem *probs, int nprob, int &b)
+__device__ __forceinline__ int find_problem(const ProbStarts &ps, int &b)
 {
     int pi = 0;
-    while (pi + 1 < nprob && b >= probs[pi].nblocks) {
-        b -= probs[pi].nblocks;
-        ++pi;
-    }
+#pragma unroll
+    for (int i = 0; i < LAMA_MAX_PROBS - 1; ++i) pi += b >= ps.s[i];
+    b -= pi == 0 ? 0 : ps.s[pi - 1];
     return pi;
 }
 
@@ -596,33 +595,33 @@ using CfgT11 = Cfg<2, 2, 1, false, 8, 2, 32>;
 
 // model.1: 7x7, reflect pad 3 (the ReflectionPad2d(3) + valid 7x7 of the
 // reference), 4 -> 64, BN + ReLU.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvProblem *__restrict__ probs, int nprob)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvProblem *__restrict__ probs, ProbStarts ps)
 {
     __shared__ __attribute__((aligned(16))) float lds[CfgHead::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
-    int pi = find_problem(probs, nprob, b);
+    int pi = find_problem(ps, b);
     conv_tile<CfgHead, false, 1>(probs[pi], b, lds, epl);
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvProblem *__restrict__ probs, int nprob)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvProblem *__restrict__ probs, ProbStarts ps)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
-    int pi = find_problem(probs, nprob, b);
+    int pi = find_problem(ps, b);
     conv_tile<CfgDown, false>(probs[pi], b, lds, epl);
 }
 
 // FFC spatial convolutions: 3x3 stride 1 reflect pad 1, with an optional 1x1
 // second K segment (the SpectralTransform's conv2, summed before BN_g).
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvProblem *__restrict__ probs, int nprob)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvProblem *__restrict__ probs, ProbStarts ps)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(CfgFfc::LDS, CfgFfc1::LDS)];
     __shared__ float epl[192];
     int b = blockIdx.x;
-    int pi = find_problem(probs, nprob, b);
+    int pi = find_problem(ps, b);
     conv_tile<CfgFfc, true>(probs[pi], b, lds, epl);
 }
 
@@ -630,14 +629,14 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 // conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
 // N % 4 == 0; lama_conv1x1_s takes any N.
 #define LAMA_PW_KERNEL(NAME, KC, VEC, NPX, PREFETCH)                                                        \
-    extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, int nprob) \
+    extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, ProbStarts ps) \
     {                                                                                                       \
         side_priority();                                                                                    \
         using C = PwCfg<KC, VEC, NPX>;                                                                      \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \
-        int pi = find_problem(probs, nprob, b);                                                             \
+        int pi = find_problem(ps, b);                                                             \
         pw_tile<C, PREFETCH>(probs[pi], b, lds, epl);                                                       \
     }
 LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, true, 64, false)
@@ -652,12 +651,12 @@ LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, false, 64, true)
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions
 // (problems 0..3 = phases (py,px) = (0,0), (0,1), (1,0), (1,1)), each a valid
 // (1+py) x (1+px) convolution with zero fill at the bottom/right edge.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(const ConvProblem *__restrict__ probs, int nprob)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(const ConvProblem *__restrict__ probs, ProbStarts ps)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
     __shared__ float epl[192];
     int b = blockIdx.x;
-    int pi = find_problem(probs, nprob, b);
+    int pi = find_problem(ps, b);
     switch (pi) {
     case 0: conv_tile<CfgT00, false>(probs[0], b, lds, epl); break;
     case 1: conv_tile<CfgT01, false>(probs[1], b, lds, epl); break;

@@ -57,6 +57,15 @@ const char *const kPwAnyName[2] = {"lama_conv1x1_s", "lama_conv1x1_res_s"};
 // Single-block FFT kernels with the plane shape fixed at compile time.
 const char *const kFftCtName[2][2] = {{"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}};
 
+// The first workgroup of each problem after the first, for a grouped launch.
+ProbStarts prob_starts(const ConvProblem *q, size_t n)
+{
+    ProbStarts ps{(int)n, {}};
+    int cum = 0;
+    for (int i = 0; i < LAMA_MAX_PROBS - 1; ++i) ps.s[i] = (size_t)i + 1 < n ? cum += q[i].nblocks : INT32_MAX;
+    return ps;
+}
+
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 void tile_shape(int family, int &tr, int &tc)
 {
@@ -651,7 +660,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
         L.grid = nb;
         L.shmem = 0;
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
-        L.nprob = (int)probs.size();
+        L.ps = prob_starts(probs.data(), probs.size());
+        if (probs.size() > LAMA_MAX_PROBS) bad_problem = true;
         L.nparams = 2;
         L.step_end = step;
         L.flops = flops;
@@ -716,7 +726,9 @@ bool Engine::build_plan(Plan &p, std::string &err)
     // equal workgroups -- one per slot of two per CU.
     auto part = [&](int k, int q) {
         const FfcW &Fw = ffc_[k];
-        const int c0 = q == 0 ? 0 : 128 + 96 * (q - 1), nch = q == 0 ? 128 : 96;
+        constexpr int RC = 384 / LAMA_G2L_RANGES;  // channels per g2l K range
+        static_assert(RC % 8 == 0, "whole K chunks per range");
+        const int c0 = q == 0 ? 0 : 128 + RC * (q - 1), nch = q == 0 ? 128 : RC;
         ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8, Fw.local, nch, H8, W8);
         sq.wt = wp(Fw.local.off) + (size_t)(c0 / 8) * 72;  // chunk c0/8 of the packed rows
         sq.nchunk = nch / 8;
@@ -732,8 +744,10 @@ bool Engine::build_plan(Plan &p, std::string &err)
                     k % 2 ? EV_A1 : EV_A0);
     };
     auto launch_b = [&](int k) {
-        std::vector<ConvProblem> probs{part(k, 1), part(k, 2), part(k, 3), part(k, 4)};
-        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9), f4 * (384 * P8 + 4 * 128 * P8 + 128 * 384 * 9),
+        std::vector<ConvProblem> probs;
+        for (int q = 1; q <= LAMA_G2L_RANGES; ++q) probs.push_back(part(k, q));
+        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
+                    f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9),
                     S_MAIN, k == 0 ? -1 : ((k - 1) % 2 ? EV_S1 : EV_S0));
     };
     auto launch_finalize = [&](int k) {
@@ -867,8 +881,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
 bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record)
 {
     void *arg = L.arg;
-    int nprob = L.nprob;
-    void *params[2] = {&arg, &nprob};
+    ProbStarts ps = L.ps;
+    void *params[2] = {&arg, &ps};
     const bool prof = (prof_mask_ >> L.family) & 1u;
     Pending pe{};
     if (prof) {
@@ -1168,7 +1182,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     L.family = family;
     L.grid = (unsigned)q.nblocks;
     L.arg = dq;
-    L.nprob = 1;
+    L.ps = prob_starts(&q, 1);
     L.nparams = 2;
     if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
     return check(hip_->hipMemcpy(out, dout, (size_t)cout * oh * ow * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);
@@ -1235,7 +1249,7 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
     L.family = F_CONVT;
     L.grid = nb;
     L.arg = dq;
-    L.nprob = 4;
+    L.ps = prob_starts(q, 4);
     L.nparams = 2;
     if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
     return check(hip_->hipMemcpy(out, dout, (size_t)cout * 4 * h * w * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);

@@ -45,7 +45,7 @@ struct Launch {
     unsigned block;  // threads per block (0 = LAMA_NT)
     unsigned shmem;
     void *arg;   // device pointer to this launch's descriptor(s)
-    int nprob;   // conv kernels: number of problems (second parameter)
+    ProbStarts ps;  // conv kernels: problem count and first workgroups (second parameter)
     int nparams;
     int step_end;  // plan step completed by this launch, or -1
     double flops, bytes;
