@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #define LAMA_NT 256      // threads per block (4 waves of 64)
+#define LAMA_CUS 256     // compute units of an MI355X (grid sizing of tile-walking kernels)
 // input channels per K chunk of the pointwise (1x1) convolutions; their
 // weights are packed in chunks of this many
 #ifndef LAMA_PW_KC

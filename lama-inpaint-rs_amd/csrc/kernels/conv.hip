@@ -94,7 +94,7 @@ struct Slots {
 };
 
 template <class C>
-__device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int m0, int M, int oy0, int ox0)
+__device__ __forceinline__ void make_wslots(Slots<C> &sl, const ConvSeg &sg, int m0, int M)
 {
     const int tid = threadIdx.x;
 #pragma unroll
@@ -105,6 +105,14 @@ __device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int 
         sl.wl[it] = in ? row * C::WSTR + c4 * 4 : 64 * C::WSTR + (idx - C::W4) * 4;
         sl.wg[it] = in ? min(m0 + row, M - 1) * sg.wrow + c4 * 4 : 0;
     }
+}
+
+// Patch slots of the tile at (oy0, ox0); the LDS side (pl) does not depend on
+// the tile.
+template <class C>
+__device__ __forceinline__ void make_pslots(Slots<C> &sl, const ConvSeg &sg, int oy0, int ox0)
+{
+    const int tid = threadIdx.x;
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) {
         const int idx = tid + it * LAMA_NT;
@@ -128,6 +136,13 @@ __device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int 
     }
 }
 
+template <class C>
+__device__ __forceinline__ void make_slots(Slots<C> &sl, const ConvSeg &sg, int m0, int M, int oy0, int ox0)
+{
+    make_wslots<C>(sl, sg, m0, M);
+    make_pslots<C>(sl, sg, oy0, ox0);
+}
+
 // Registers holding one chunk on its way from global memory to LDS.
 template <class C>
 struct Stage {
@@ -135,9 +150,9 @@ struct Stage {
     float p[C::PITER];
 };
 
-// Issue the global loads of chunk `ck`.
+// Issue the global loads of chunk `ck`: weights, then the input patch.
 template <class C>
-__device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, const ConvSeg &sg, int ck)
+__device__ __forceinline__ void load_w(Stage<C> &st, const Slots<C> &sl, const ConvSeg &sg, int ck)
 {
     const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::WK;
 #pragma unroll
@@ -148,6 +163,11 @@ __device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, con
         st.w[4 * it + 2] = v.z;
         st.w[4 * it + 3] = v.w;
     }
+}
+
+template <class C>
+__device__ __forceinline__ void load_p(Stage<C> &st, const Slots<C> &sl, const ConvSeg &sg, int ck)
+{
     // 32-bit byte offsets from the chunk's first plane (below 4 * KC * plane,
     // which the host bounds); slots of channels past C (zero weights) read the
     // last float of the source instead
@@ -163,14 +183,33 @@ __device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, con
 }
 
 template <class C>
-__device__ __forceinline__ void store_chunk(const Stage<C> &st, const Slots<C> &sl, float *wl, float *pl)
+__device__ __forceinline__ void load_chunk(Stage<C> &st, const Slots<C> &sl, const ConvSeg &sg, int ck)
+{
+    load_w<C>(st, sl, sg, ck);
+    load_p<C>(st, sl, sg, ck);
+}
+
+template <class C>
+__device__ __forceinline__ void store_w(const Stage<C> &st, const Slots<C> &sl, float *wl)
 {
 #pragma unroll
     for (int it = 0; it < C::WITER; ++it)
         *reinterpret_cast<float4 *>(wl + sl.wl[it]) =
             make_float4(st.w[4 * it], st.w[4 * it + 1], st.w[4 * it + 2], st.w[4 * it + 3]);
+}
+
+template <class C>
+__device__ __forceinline__ void store_p(const Stage<C> &st, const Slots<C> &sl, float *pl)
+{
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) pl[sl.pl[it]] = st.p[it];
+}
+
+template <class C>
+__device__ __forceinline__ void store_chunk(const Stage<C> &st, const Slots<C> &sl, float *wl, float *pl)
+{
+    store_w<C>(st, sl, wl);
+    store_p<C>(st, sl, pl);
 }
 
 template <int N>
@@ -594,14 +633,70 @@ using CfgT11 = Cfg<2, 2, 1, false, 8, 2, 32>;
 }  // namespace
 
 // model.1: 7x7, reflect pad 3 (the ReflectionPad2d(3) + valid 7x7 of the
-// reference), 4 -> 64, BN + ReLU.
+// reference), 4 -> 64, BN + ReLU.  K = 4 x 49 is one chunk, so the 64 x 196
+// weights (53 KB) would be re-fetched by every tile; instead each workgroup
+// keeps them in LDS and walks tiles blockIdx.x, + gridDim.x, ..., with the
+// next tile's 4-channel patch loaded into registers during this tile's MFMAs
+// and parked in the other of two patch buffers.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvProblem *__restrict__ probs, ProbStarts ps)
 {
-    __shared__ __attribute__((aligned(16))) float lds[CfgHead::LDS];
+    using C = CfgHead;
+    __shared__ __attribute__((aligned(16))) float lds[C::W_LDS + 2 * C::P_LDS];
     __shared__ float epl[192];
-    int b = blockIdx.x;
-    int pi = find_problem(ps, b);
-    conv_tile<CfgHead, false, 1>(probs[pi], b, lds, epl);
+    float *const wl = lds, *const pl0 = lds + C::W_LDS, *const pl1 = pl0 + C::P_LDS;
+    const ConvProblem &P = probs[0];
+    const ConvSeg sg = P.s0;
+    const int ntiles = P.nblocks;
+    int t = blockIdx.x;
+    if (t >= ntiles) return;  // whole workgroup
+    if (sg.nchunk != 1 || P.mblocks != 1) {
+        // more than 4 input channels or 64 output channels (single-op tests):
+        // one tile at a time through the generic path
+        for (; t < ntiles; t += gridDim.x) conv_tile<C, false, 1>(P, t, lds, epl);
+        return;
+    }
+    auto origin = [&](int tile, int &oy0, int &ox0) {
+        oy0 = (tile / P.tiles_x) * C::TR;
+        ox0 = (tile % P.tiles_x) * C::TC;
+    };
+    Slots<C> sl;
+    Stage<C> cur, nxt;
+    int oy0, ox0, ny0, nx0;
+    origin(t, oy0, ox0);
+    make_wslots<C>(sl, sg, 0, P.M);
+    make_pslots<C>(sl, sg, oy0, ox0);
+    load_w<C>(cur, sl, sg, 0);
+    load_p<C>(cur, sl, sg, 0);
+    const float ep = epi_param_load(P, 0);
+    // the next tile (clamped: the last tile is re-read instead of branching)
+    int tn = min(t + (int)gridDim.x, ntiles - 1);
+    origin(tn, ny0, nx0);
+    make_pslots<C>(sl, sg, ny0, nx0);
+    load_p<C>(nxt, sl, sg, 0);
+    store_w<C>(cur, sl, wl);
+    store_p<C>(cur, sl, pl0);
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    __syncthreads();
+    EpiPre pre;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pre.add[r] = pre.res[r] = 0.f;
+    for (int i = 0;; ++i) {
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+        compute_chunk<C>(acc, wl, (i & 1) ? pl1 : pl0);
+        epilogue<C::TR, C::TC, false>(acc, pre, P, epl, 0, oy0, ox0);
+        t += gridDim.x;
+        if (t >= ntiles) break;
+        oy0 = ny0;
+        ox0 = nx0;
+        store_p<C>(nxt, sl, (i & 1) ? pl0 : pl1);
+        tn = min(t + (int)gridDim.x, ntiles - 1);
+        origin(tn, ny0, nx0);
+        make_pslots<C>(sl, sg, ny0, nx0);
+        load_p<C>(nxt, sl, sg, 0);
+        __syncthreads();
+    }
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.

@@ -657,7 +657,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
             if (q.nblocks != q.tiles_x * q.tiles_y * q.mblocks)
                 bad_problem = true;
         }
-        L.grid = nb;
+        // the head kernel walks its tiles: two resident workgroups per CU
+        L.grid = family == F_CONV7 ? std::min(nb, 2u * LAMA_CUS) : nb;
         L.shmem = 0;
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
         L.ps = prob_starts(probs.data(), probs.size());
