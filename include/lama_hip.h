@@ -52,10 +52,7 @@ int lama_hip_forward(lama_hip_ctx *ctx, const float *input, int h, int w, float 
                      char *err, size_t errlen);
 
 /* The same pass on device-resident buffers, enqueued on `stream` (a
- * hipStream_t; NULL = the engine's own stream).  Asynchronous.  Inside the
- * pass one cross-stream edge is a bounded device-side wait; should it ever
- * expire (a pass starved for over a second), the next lama_hip_synchronize
- * or lama_hip_forward fails with a message saying the output is invalid. */
+ * hipStream_t; NULL = the engine's own stream).  Asynchronous. */
 int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int w,
                             float *d_output, void *stream, char *err, size_t errlen);
 
@@ -101,8 +98,6 @@ int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size
 int lama_hip_free(lama_hip_ctx *ctx, void *ptr);
 int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, size_t bytes, int kind,
                     char *err, size_t errlen); /* kind: 1 HtoD, 2 DtoH, 3 DtoD */
-/* Waits for all work on the device, then reports an expired device-side
- * wait of an earlier lama_hip_forward_device (see above). */
 int lama_hip_synchronize(lama_hip_ctx *ctx, char *err, size_t errlen);
 
 /* Single kernel families on host buffers, for parity tests against the

@@ -81,27 +81,11 @@ struct ConvSeg {
 // of problems 1..3 (INT32_MAX where absent), so a workgroup finds its problem
 // without reading the descriptors' block counts first (that chain of
 // dependent scalar loads sat at the head of every workgroup's prologue).
-//
-// The same argument carries one device-side ordering edge.  `sync` points at
-// two words: sync[0] is a counter, sync[1] a fault word.  The counter only
-// grows (modulo 2^32: the host hands out values from a per-shape sequence),
-// so any copy of it a cache still holds is a lower bound of its value.
-// role LAMA_EDGE_SIGNAL: workgroup 0 stores `val` when the launch starts (its
-// stream's previous kernel has then completed and its writes are visible);
-// role LAMA_EDGE_WAIT: every workgroup waits until the counter reaches `val`
-// before it reads anything.  The wait is bounded (LAMA_WAIT_TICKS); on expiry
-// it sets the fault word, which the host reports, and proceeds.
 #define LAMA_MAX_PROBS 4
-#define LAMA_EDGE_SIGNAL 1
-#define LAMA_EDGE_WAIT 2
 struct alignas(16) ProbStarts {
     int n;                       // number of problems (1..LAMA_MAX_PROBS)
     int s[LAMA_MAX_PROBS - 1];   // first workgroup of problems 1, 2, ...
-    unsigned *sync;              // nullptr: no edge
-    unsigned val;                // counter value signalled / awaited
-    int role;                    // LAMA_EDGE_SIGNAL or LAMA_EDGE_WAIT
 };
-#define LAMA_WAIT_TICKS 100000000LL  // 1 s of the 100 MHz constant clock
 
 // One output problem: out[co][oy'][ox'] for co < M, (oy, ox) on the OH x OW
 // GEMM grid, stored at oy' = oy*oy_mul + oy_off, ox' = ox*ox_mul + ox_off

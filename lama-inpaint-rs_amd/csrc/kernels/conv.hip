@@ -612,45 +612,6 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
         epilogue<1, 64, PREFETCH>(acc[h], pre[h], P, epl, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
 }
 
-// The ordering edge of a launch (ProbStarts::sync).  Signal: workgroup 0
-// publishes `val` with a coherent store; the kernel boundary before this
-// launch has already made the previous kernel's writes visible at agent
-// scope.  Wait: thread 0 first reads the counter through the caches -- a copy
-// there is a lower bound, so reaching `val` proves the signal -- and only
-// otherwise polls it coherently, then invalidates its caches (agent acquire)
-// before the barrier releases the workgroup's loads.  When the cached read
-// suffices no line of the awaited data can be stale in this XCD's L2: those
-// lines were invalidated when this launch began, and until the counter is
-// seen no workgroup of the launch reads them.
-__device__ __forceinline__ bool edge_reached(unsigned v, unsigned val) { return (int)(v - val) >= 0; }
-
-__device__ __forceinline__ void edge_sync(const ProbStarts &ps)
-{
-    if (!ps.sync) return;
-    if (ps.role == LAMA_EDGE_SIGNAL) {
-        if (blockIdx.x == 0 && threadIdx.x == 0)
-            __hip_atomic_store(ps.sync, ps.val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    if (threadIdx.x == 0) {
-        unsigned v = __hip_atomic_load(ps.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (!edge_reached(v, ps.val)) {
-            const long t0 = wall_clock64();
-            v = __hip_atomic_load(ps.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            while (!edge_reached(v, ps.val)) {
-                if (wall_clock64() - t0 > LAMA_WAIT_TICKS) {
-                    __hip_atomic_store(ps.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
-                v = __hip_atomic_load(ps.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        }
-    }
-    __syncthreads();
-}
-
 __device__ __forceinline__ int find_problem(const ProbStarts &ps, int &b)
 {
     int pi = 0;
@@ -679,7 +640,6 @@ using CfgT11 = Cfg<2, 2, 1, false, 8, 2, 32>;
 // and parked in the other of two patch buffers.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvProblem *__restrict__ probs, ProbStarts ps)
 {
-    edge_sync(ps);
     using C = CfgHead;
     __shared__ __attribute__((aligned(16))) float lds[C::W_LDS + 2 * C::P_LDS];
     __shared__ float epl[192];
@@ -744,7 +704,6 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvP
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
     __shared__ float epl[192];
-    edge_sync(ps);
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     conv_tile<CfgDown, false>(probs[pi], b, lds, epl);
@@ -756,7 +715,6 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(CfgFfc::LDS, CfgFfc1::LDS)];
     __shared__ float epl[192];
-    edge_sync(ps);
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     conv_tile<CfgFfc, true>(probs[pi], b, lds, epl);
@@ -772,7 +730,6 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
         using C = PwCfg<KC, VEC, NPX>;                                                                      \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
-        edge_sync(ps);                                                                                      \
         int b = blockIdx.x;                                                                                 \
         int pi = find_problem(ps, b);                                                             \
         pw_tile<C, PREFETCH>(probs[pi], b, lds, epl);                                                       \
@@ -793,7 +750,6 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(const ConvProbl
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
     __shared__ float epl[192];
-    edge_sync(ps);
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     switch (pi) {

@@ -169,8 +169,7 @@ extern "C" int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, si
 
 extern "C" int lama_hip_synchronize(lama_hip_ctx *ctx, char *err, size_t errlen)
 {
-    GUARD(ctx->eng.check(ctx->eng.hip()->hipDeviceSynchronize(), "hipDeviceSynchronize", e_) &&
-          ctx->eng.check_faults(e_));
+    GUARD(ctx->eng.check(ctx->eng.hip()->hipStreamSynchronize(ctx->eng.stream()), "hipStreamSynchronize", e_));
 }
 
 extern "C" int lama_hip_op_conv2d(lama_hip_ctx *ctx, const float *x, int cin, int h, int w, const float *wt,

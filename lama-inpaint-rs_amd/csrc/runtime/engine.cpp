@@ -60,7 +60,7 @@ const char *const kFftCtName[2][2] = {{"lama_rfft2_64", "lama_irfft2_64"}, {"lam
 // The first workgroup of each problem after the first, for a grouped launch.
 ProbStarts prob_starts(const ConvProblem *q, size_t n)
 {
-    ProbStarts ps{(int)n, {}, nullptr, 0u, 0};
+    ProbStarts ps{(int)n, {}};
     int cum = 0;
     for (int i = 0; i < LAMA_MAX_PROBS - 1; ++i) ps.s[i] = (size_t)i + 1 < n ? cum += q[i].nblocks : INT32_MAX;
     return ps;
@@ -548,7 +548,7 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.twr = take(ntwr * 4);
     L.twc = take(ntwc * 4);
     const size_t n_conv = 4 + 36 * 9 + 4 * 3;      // problems
-    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 2 + 1;  // descriptor uploads (and the sync words), 256-byte aligned
+    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
     L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
     return off;
 }
@@ -608,10 +608,6 @@ bool Engine::build_plan(Plan &p, std::string &err)
         std::memcpy(desc.data() + o, src, bytes);
         return (void *)(base + o_desc + o);
     };
-    // the x_g edge's device words (ProbStarts::sync), zero at upload
-    static const unsigned kSyncZero[64] = {};
-    p.sync = (unsigned *)put(kSyncZero, sizeof kSyncZero);
-    dev_edges_ = !(getenv("LAMA_EDGE_EVENTS") && atoi(getenv("LAMA_EDGE_EVENTS")) == 1);
     auto seg = [&](const float *src, const Packed &pk, int C, int IH, int IW) {
         ConvSeg s{};
         s.src = src;
@@ -748,25 +744,12 @@ bool Engine::build_plan(Plan &p, std::string &err)
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
                     k % 2 ? EV_A1 : EV_A0);
     };
-    // B(k) reads x_g(k), written by conv2(k-1) on the side stream.  That edge
-    // is a device-side counter: conv1(k), the side stream's next kernel,
-    // publishes k when it starts (conv2(k-1) has then completed), and B(k)'s
-    // workgroups wait for it.  conv1(k) starts long before A(k) ends, so the
-    // wait is normally already met, and the main stream carries no barrier
-    // packet, whose processing cost ~6 us per FFC even when satisfied.
-    // Deadlock-free: conv1(k) depends only on work enqueued before B(k), and
-    // fits on a CU beside two B workgroups (36 KB of LDS, 132 VGPRs).
     auto launch_b = [&](int k) {
         std::vector<ConvProblem> probs;
         for (int q = 1; q <= LAMA_G2L_RANGES; ++q) probs.push_back(part(k, q));
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
-                    f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9), S_MAIN);
-        if (k > 0) {
-            Launch &L = p.launches.back();
-            L.edge_role = LAMA_EDGE_WAIT;
-            L.edge_k = k;
-            L.edge_ev = (k - 1) % 2 ? EV_S1 : EV_S0;
-        }
+                    f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9),
+                    S_MAIN, k == 0 ? -1 : ((k - 1) % 2 ? EV_S1 : EV_S0));
     };
     auto launch_finalize = [&](int k) {
         const FfcW &Fw = ffc_[k];
@@ -798,8 +781,6 @@ bool Engine::build_plan(Plan &p, std::string &err)
                     {problem(F_CONV1, seg(ffc_src(k) + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1,
                              192, Fb, P8, (int)P8, nullptr)},
                     -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384), S_SIDE, k == 0 ? EV_FORK : -1);
-        p.launches.back().edge_role = LAMA_EDGE_SIGNAL;
-        p.launches.back().edge_k = k;
         push_fft(p, false, fg, d_rfft, S_SIDE, f4 * 192 * P8, 8.0 * 192 * PS);
         // FourierUnit conv over the stacked spectrum + BN + ReLU
         conv_launch(F_CONV1,
@@ -902,11 +883,6 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t
 {
     void *arg = L.arg;
     ProbStarts ps = L.ps;
-    if (L.edge_role && run_sync_) {  // else the edge is an event wait (run)
-        ps.sync = run_sync_;
-        ps.val = run_base_ + (unsigned)L.edge_k;
-        ps.role = L.edge_role;
-    }
     void *params[2] = {&arg, &ps};
     const bool prof = (prof_mask_ >> L.family) & 1u;
     Pending pe{};
@@ -962,19 +938,9 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
     // LAMA_STREAMS=1 puts the side-stream work on the main stream (profiling)
     static const bool single = getenv("LAMA_STREAMS") && atoi(getenv("LAMA_STREAMS")) == 1;
     hipStream_t st[2] = {s, single ? s : side_};
-    // device edges: this pass's counter values (a captured graph keeps event
-    // edges: it may place its nodes on queues of its own)
-    const bool dev = dev_edges_ && !capturing_;
-    run_sync_ = dev ? p.sync : nullptr;
-    run_base_ = ++p.seq * 64u;
     for (const Launch &L : p.launches) {
         hipStream_t ls = st[L.stream];
         if (L.wait_ev >= 0 && !check(hip_->hipStreamWaitEvent(ls, ev_[L.wait_ev], 0), "hipStreamWaitEvent", err))
-            return false;
-        // a captured graph may order its nodes on its own queues, so it keeps
-        // the x_g edge as a graph edge
-        if (L.edge_ev >= 0 && !dev &&
-            !check(hip_->hipStreamWaitEvent(ls, ev_[L.edge_ev], 0), "hipStreamWaitEvent", err))
             return false;
         // cross-stream events ride in the dispatch packet, unless the launch is
         // being profiled (its packet then carries the timing events) or the
@@ -1006,7 +972,6 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
             if (stp == 26 && steps[27]) host_reflect_pad(dst, 64, p.H, p.W, 3, steps[27]);
         }
     }
-    run_sync_ = nullptr;
     return true;
 }
 
@@ -1070,7 +1035,7 @@ bool Engine::forward_host(const float *in, int h, int w, float *out, float *cons
     if (!(steps || !use_graph() ? run(*p, stream_, steps, err) : replay(*p, stream_, err))) return false;
     if (!check(hip_->hipMemcpyAsync(out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(output)", err))
         return false;
-    return check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err) && check_faults(err);
+    return check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err);
 }
 
 bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err)
@@ -1082,25 +1047,6 @@ bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipSt
         return false;
     if (!(use_graph() ? replay(*p, s, err) : run(*p, s, nullptr, err))) return false;
     return check(hip_->hipMemcpyAsync(d_out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err);
-}
-
-bool Engine::check_faults(std::string &err)
-{
-    for (auto &kv : plans_) {
-        unsigned *sync = kv.second.sync;
-        if (!sync) continue;
-        unsigned fault = 0;
-        if (!check(hip_->hipMemcpy(&fault, sync + 1, sizeof fault, hipMemcpyDeviceToHost), "hipMemcpy(fault word)", err))
-            return false;
-        if (fault) {
-            fault = 0;
-            hip_->hipMemcpy(sync + 1, &fault, sizeof fault, hipMemcpyHostToDevice);
-            err = "device-side x_g edge wait timed out at " + std::to_string(kv.first.first) + "x" +
-                  std::to_string(kv.first.second) + ": an earlier forward's output is invalid";
-            return false;
-        }
-    }
-    return true;
 }
 
 int Engine::launch_count(int h, int w)

@@ -46,11 +46,6 @@ struct Launch {
     unsigned shmem;
     void *arg;   // device pointer to this launch's descriptor(s)
     ProbStarts ps;  // conv kernels: problem count and first workgroups (second parameter)
-    // device-side ordering edge (ProbStarts::role): LAMA_EDGE_SIGNAL or
-    // LAMA_EDGE_WAIT with counter value pass base + edge_k, or 0; edge_ev is
-    // the event waited on instead when device edges are off, or -1
-    int edge_role = 0, edge_k = 0;
-    int edge_ev = -1;
     int nparams;
     int step_end;  // plan step completed by this launch, or -1
     double flops, bytes;
@@ -78,8 +73,6 @@ struct Plan {
     float *in = nullptr, *out = nullptr;
     std::vector<std::pair<const float *, size_t>> step_src;  // per step (nullptr: host-derived)
     std::vector<Launch> launches;
-    unsigned *sync = nullptr;        // device words of the x_g edge: counter, fault
-    unsigned seq = 0;                // passes run (the edge counter's values advance by 64 per pass)
     hipGraphExec_t graph = nullptr;  // the launch list captured once, replayed per forward
     bool graph_failed = false;
 };
@@ -113,9 +106,6 @@ public:
     const HipApi *hip() const { return hip_; }
     hipStream_t stream() const { return stream_; }
     bool check(hipError_t e, const char *what, std::string &err);
-    // After a synchronisation: fails (and clears the word) when a device-side
-    // wait of an earlier forward timed out, i.e. that forward's output is invalid.
-    bool check_faults(std::string &err);
 
 private:
     struct FfcW {
@@ -154,9 +144,6 @@ private:
     hipStream_t stream_ = nullptr, side_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};
     bool capturing_ = false;  // run() is recording a graph
-    bool dev_edges_ = true;   // x_g edge as a device-side counter (LAMA_EDGE_EVENTS=1: an event wait)
-    unsigned *run_sync_ = nullptr;  // the running plan's edge words and counter base (run())
-    unsigned run_base_ = 0;
 
     // weights
     bool have_weights_ = false;

@@ -183,48 +183,6 @@ def test_graph_replays_match_eager(pkg, engine, monkeypatch):
     eng1.close()
 
 
-@pytest.mark.parametrize("h,w", [(512, 512), (256, 384)])
-def test_device_edge_matches_event_edge(pkg, engine, monkeypatch, h, w):
-    """The x_g edge of every FFC (conv2(k-1) on the side stream -> the g2l
-    launch B(k) on the main stream) as a device-side counter, against the same
-    edge as a HIP event wait (LAMA_EDGE_EVENTS=1): three passes with different
-    inputs queued back to back, each into its own output, all bit-identical
-    to the event-ordered forward.  A B(k) that read x_g before conv2(k-1)
-    finished would see the buffer's previous contents (x_g(k-2), or another
-    image's) and differ."""
-    H = pkg.host_api
-    xs = []
-    for seed in range(3):
-        img = H.synth_image(h, w, seed + 1)
-        mask, _ = H.synth_mask_strokes(h, w, 0.25, seed + 2)
-        xs.append(H.build_input(img, mask))
-    monkeypatch.setenv("LAMA_EDGE_EVENTS", "1")
-    eng0 = pkg.hip_engine.Engine()
-    eng0.load_weights(engine._store)
-    ref = [eng0.forward(x) for x in xs]
-    eng0.close()
-    monkeypatch.delenv("LAMA_EDGE_EVENTS")
-    eng1 = pkg.hip_engine.Engine()
-    eng1.load_weights(engine._store)
-    d_in = [eng1.malloc(x.nbytes) for x in xs]
-    d_out = [eng1.malloc(3 * h * w * 4) for _ in xs]
-    for d, x in zip(d_in, xs):
-        eng1.upload(d, x)
-    print(f"case {h}x{w} device edge, 2 x 3 queued passes", flush=True)
-    for rep in range(2):
-        for d, o in zip(d_in, d_out):
-            eng1.forward_device(d, h, w, o)
-        eng1.synchronize()
-        for i, o in enumerate(d_out):
-            out = np.empty((3, h, w), np.float32)
-            eng1.download(out, o)
-            assert np.array_equal(out, ref[i]), f"rep {rep} pass {i}"
-    assert np.array_equal(eng1.forward(xs[1]), ref[1])
-    for d in d_in + d_out:
-        eng1.free(d)
-    eng1.close()
-
-
 def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal):
     """configs[4]'s --tile window: 600 x 600 (75 x 75 bottleneck, FFT lengths
     75 and 38 through the reference's opposite-sign rule) against the oracle,
