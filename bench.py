@@ -47,7 +47,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs one forward on one GPU; multi-GPU runs are not part of this build "
-              "(a batch-1 pass does not shard; see DESIGN.md for how it would)", file=sys.stderr)
+              "(a batch-1 pass does not shard across GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import __graft_entry__

@@ -31,8 +31,11 @@ int fail(char *err, size_t len, const std::string &m)
 }
 }  // namespace
 
+// Every entry point with a context: a null context is an error, and no C++
+// exception crosses the C boundary.
 #define GUARD(expr)                          \
     do {                                     \
+        if (!ctx) return fail(err, errlen, "lama_hip: null context"); \
         std::string e_;                      \
         try {                                \
             if (!(expr)) return fail(err, errlen, e_); \
@@ -44,14 +47,19 @@ int fail(char *err, size_t len, const std::string &m)
 
 extern "C" int lama_hip_open(lama_hip_ctx **out, char *err, size_t errlen)
 {
+    if (!out) return fail(err, errlen, "lama_hip_open: null output pointer");
     *out = nullptr;
-    auto *c = new lama_hip_ctx;
-    std::string e;
-    if (!c->eng.open(e)) {
-        delete c;
-        return fail(err, errlen, e);
+    try {
+        auto *c = new lama_hip_ctx;
+        std::string e;
+        if (!c->eng.open(e)) {
+            delete c;
+            return fail(err, errlen, e);
+        }
+        *out = c;
+    } catch (const std::exception &x) {
+        return fail(err, errlen, x.what());
     }
-    *out = c;
     return 0;
 }
 
@@ -105,11 +113,15 @@ extern "C" int lama_hip_vram(uint64_t *free_bytes, uint64_t *total_bytes, char *
 
 extern "C" int lama_hip_profile(lama_hip_ctx *ctx, uint32_t mask)
 {
+    if (!ctx) return 1;
     ctx->eng.set_profile(mask);
     return 0;
 }
 
-extern "C" void lama_hip_profile_reset(lama_hip_ctx *ctx) { ctx->eng.profile_reset(); }
+extern "C" void lama_hip_profile_reset(lama_hip_ctx *ctx)
+{
+    if (ctx) ctx->eng.profile_reset();
+}
 
 extern "C" int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, uint64_t *launches,
                                      double *ms, double *flops, double *bytes)
@@ -117,7 +129,7 @@ extern "C" int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_
     std::string n;
     uint64_t l = 0;
     double m = 0, f = 0, b = 0;
-    if (!ctx->eng.profile_read(i, n, l, m, f, b)) return 0;
+    if (!ctx || !ctx->eng.profile_read(i, n, l, m, f, b)) return 0;
     if (name && namelen) snprintf(name, namelen, "%s", n.c_str());
     if (launches) *launches = l;
     if (ms) *ms = m;
@@ -128,7 +140,7 @@ extern "C" int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_
 
 extern "C" void lama_hip_print_stats(lama_hip_ctx *ctx)
 {
-    for (int i = 0;; ++i) {
+    for (int i = 0; ctx; ++i) {
         std::string n;
         uint64_t l;
         double m, f, b;
@@ -151,14 +163,17 @@ extern "C" int lama_hip_plan_bytes(lama_hip_ctx *ctx, int h, int w, uint64_t *ar
     })());
 }
 
-extern "C" int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w) { return ctx->eng.launch_count(h, w); }
+extern "C" int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w) { return ctx ? ctx->eng.launch_count(h, w) : -1; }
 
 extern "C" int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size_t errlen)
 {
     GUARD(ctx->eng.check(ctx->eng.hip()->hipMalloc(ptr, bytes), "hipMalloc", e_));
 }
 
-extern "C" int lama_hip_free(lama_hip_ctx *ctx, void *ptr) { return ctx->eng.hip()->hipFree(ptr) == hipSuccess ? 0 : 1; }
+extern "C" int lama_hip_free(lama_hip_ctx *ctx, void *ptr)
+{
+    return ctx && ctx->eng.hip()->hipFree(ptr) == hipSuccess ? 0 : 1;
+}
 
 extern "C" int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, size_t bytes, int kind, char *err,
                                size_t errlen)

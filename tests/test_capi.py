@@ -91,3 +91,24 @@ def test_missing_library_raises(tmp_path):
             "try:\n    E.Engine()\nexcept RuntimeError as e:\n    print('RAISED', e)\n")
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert "RAISED" in r.stdout and "not built" in r.stdout
+
+
+def test_null_context_is_an_error_not_a_crash():
+    """Every entry point that takes a context rejects a null one with a
+    message (no GPU call is made)."""
+    L = ctypes.CDLL(os.path.join(LIB, "liblama_hip.so"))
+    err = ctypes.create_string_buffer(256)
+    buf = (ctypes.c_float * 16)()
+    L.lama_hip_forward.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_char_p, ctypes.c_size_t]
+    assert L.lama_hip_forward(None, buf, 8, 8, buf, err, 256) == 1
+    assert b"null context" in err.value
+    L.lama_hip_synchronize.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    err.value = b""
+    assert L.lama_hip_synchronize(None, err, 256) == 1 and b"null context" in err.value
+    L.lama_hip_launch_count.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    assert L.lama_hip_launch_count(None, 8, 8) == -1
+    L.lama_hip_open.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    assert L.lama_hip_open(None, err, 256) == 1 and b"null output" in err.value
+    L.lama_hip_close.argtypes = [ctypes.c_void_p]
+    L.lama_hip_close(None)
