@@ -438,9 +438,15 @@ __device__ __forceinline__ void pw_compute_chunk(f32x16 (&acc)[C::NACC], const f
     }
 }
 
-// The K loop of a pointwise segment: two LDS stages, two register stages,
-// one barrier per chunk (the schedule of run_segment).
-template <class C>
+// The K loop of a pointwise segment: two LDS stages and D register stages,
+// one barrier per chunk.  Chunk c's global loads are issued D steps before it
+// is written to LDS (at step c - 1) and consumed at step c, so each load has
+// D chunks of MFMA time to land; these small-K GEMMs run one wave per SIMD
+// and are bound by that latency.
+#ifndef LAMA_PW_DEPTH
+#define LAMA_PW_DEPTH 3
+#endif
+template <class C, int D>
 __device__ __forceinline__ void run_segment_pw(f32x16 (&acc)[C::NACC], const ConvSeg &sg_mem, int m0, int M, int ox0,
                                                float *lds)
 {
@@ -451,22 +457,23 @@ __device__ __forceinline__ void run_segment_pw(f32x16 (&acc)[C::NACC], const Con
     pw_make_slots<C>(sl, sg, m0, M, ox0);
     float *l0 = lds, *l1 = lds + C::LDS;
     const int last = n - 1;
-    PwStage<C> r0, r1;
-    pw_load_chunk<C>(r0, sl, sg, 0);
-    pw_load_chunk<C>(r1, sl, sg, min(1, last));
-    pw_store_chunk<C>(r0, sl, l0);
-    pw_load_chunk<C>(r0, sl, sg, min(2, last));
+    // prefetches past the last chunk re-read it (uniform control flow)
+    PwStage<C> r[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) pw_load_chunk<C>(r[d], sl, sg, min(d, last));
+    pw_store_chunk<C>(r[0], sl, l0);
+    pw_load_chunk<C>(r[0], sl, sg, min(D, last));
     __syncthreads();
-    for (int ck = 0; ck < n; ck += 2) {
-        pw_compute_chunk<C>(acc, l0);
-        pw_store_chunk<C>(r1, sl, l1);
-        pw_load_chunk<C>(r1, sl, sg, min(ck + 3, last));
-        __syncthreads();
-        if (ck + 1 >= n) break;
-        pw_compute_chunk<C>(acc, l1);
-        pw_store_chunk<C>(r0, sl, l0);
-        pw_load_chunk<C>(r0, sl, sg, min(ck + 4, last));
-        __syncthreads();
+    for (int ck = 0; ck < n; ck += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const int k = ck + j;
+            if (j > 0 && k >= n) break;
+            pw_compute_chunk<C>(acc, (k & 1) ? l1 : l0);
+            pw_store_chunk<C>(r[(j + 1) % D], sl, (k & 1) ? l0 : l1);
+            pw_load_chunk<C>(r[(j + 1) % D], sl, sg, min(k + 1 + D, last));
+            __syncthreads();
+        }
     }
 }
 
@@ -582,7 +589,7 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
 // One 64 x NPX tile of a pointwise problem (a flat plane: OH == 1).  The
 // epilogue runs once per 32-pixel accumulator; shifting its tile origin by
 // wn*(NPX/2 - 32) + h*32 places accumulator h of wave column wn.
-template <class C, bool PREFETCH>
+template <class C, bool PREFETCH, int D>
 __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds, float *epl)
 {
     const int mb = b % P.mblocks, t = b / P.mblocks;
@@ -604,7 +611,7 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
     for (int h = 0; h < C::NACC; ++h)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[h][r] = 0.f;
-    run_segment_pw<C>(acc, P.s0, m0, P.M, ox0, lds);
+    run_segment_pw<C, D>(acc, P.s0, m0, P.M, ox0, lds);
     if (threadIdx.x < 192) epl[threadIdx.x] = ep;
     __syncthreads();
 #pragma unroll
@@ -723,7 +730,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
 // conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
 // N % 4 == 0; lama_conv1x1_s takes any N.
-#define LAMA_PW_KERNEL(NAME, KC, VEC, NPX, PREFETCH)                                                        \
+#define LAMA_PW_KERNEL(NAME, KC, VEC, NPX, PREFETCH, D)                                                      \
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, ProbStarts ps) \
     {                                                                                                       \
         side_priority();                                                                                    \
@@ -732,15 +739,18 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \
         int pi = find_problem(ps, b);                                                             \
-        pw_tile<C, PREFETCH>(probs[pi], b, lds, epl);                                                       \
+        pw_tile<C, PREFETCH, D>(probs[pi], b, lds, epl);                                                     \
     }
-LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, true, 64, false)
-LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, false, 64, false)
+#ifndef LAMA_PW_DEPTH_RES
+#define LAMA_PW_DEPTH_RES LAMA_PW_DEPTH
+#endif
+LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, true, 64, false, LAMA_PW_DEPTH)
+LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, false, 64, false, LAMA_PW_DEPTH)
 
 // The SpectralTransform conv2, whose epilogue adds the l2g partial and the
 // residual (fetched before the K loop).
-LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, true, 64, true)
-LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, false, 64, true)
+LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, true, 64, true, LAMA_PW_DEPTH_RES)
+LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, false, 64, true, LAMA_PW_DEPTH_RES)
 #undef LAMA_PW_KERNEL
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions
