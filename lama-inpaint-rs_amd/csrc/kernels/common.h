@@ -23,6 +23,23 @@ static inline constexpr int lama_fft_nb(int h, int w)
     const int a = (h + 1) / 2 * w, b = h * (w / 2 + 1);
     return ((a > b ? a : b) + 1) & ~1;
 }
+// Input channels per K chunk of the four transposed-convolution phases
+// (py, px) = (0,0), (0,1), (1,0), (1,1), which have 1, 2, 2 and 4 taps.  The
+// one-tap phase takes 16 channels per chunk (8 MFMAs per wave between
+// barriers), the others 8.  Measured at 512x512 (ms per pass): 8/8/8/8 4.809,
+// 16/8/8/8 4.796, 16/16/16/8 4.825, 32/16/16/8 4.831 (the larger chunks
+// cost a workgroup of occupancy).  Their weights are packed in chunks of
+// these sizes.
+#ifndef LAMA_CONVT_KC0
+#define LAMA_CONVT_KC0 16
+#define LAMA_CONVT_KC1 8
+#define LAMA_CONVT_KC2 8
+#define LAMA_CONVT_KC3 8
+#endif
+static inline constexpr int lama_convt_kc(int phase)
+{
+    return phase == 0 ? LAMA_CONVT_KC0 : phase == 3 ? LAMA_CONVT_KC3 : phase == 1 ? LAMA_CONVT_KC1 : LAMA_CONVT_KC2;
+}
 #define LAMA_TAIL_ROWS 8 // output tile of the 7x7 tail kernel (rows x columns)
 #define LAMA_TAIL_COLS 64
 

@@ -632,10 +632,10 @@ using CfgHead = Cfg<7, 7, 1, true, 4, 2, 32>;
 using CfgDown = Cfg<3, 3, 2, true, 8, 2, 32>;
 using CfgFfc = Cfg<3, 3, 1, true, 8, 2, 32>;
 using CfgFfc1 = Cfg<1, 1, 1, false, 8, 2, 32>;
-using CfgT00 = Cfg<1, 1, 1, false, 8, 2, 32>;
-using CfgT01 = Cfg<1, 2, 1, false, 8, 2, 32>;
-using CfgT10 = Cfg<2, 1, 1, false, 8, 2, 32>;
-using CfgT11 = Cfg<2, 2, 1, false, 8, 2, 32>;
+using CfgT00 = Cfg<1, 1, 1, false, LAMA_CONVT_KC0, 2, 32>;
+using CfgT01 = Cfg<1, 2, 1, false, LAMA_CONVT_KC1, 2, 32>;
+using CfgT10 = Cfg<2, 1, 1, false, LAMA_CONVT_KC2, 2, 32>;
+using CfgT11 = Cfg<2, 2, 1, false, LAMA_CONVT_KC3, 2, 32>;
 
 }  // namespace
 

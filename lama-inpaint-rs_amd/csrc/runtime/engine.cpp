@@ -329,7 +329,7 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
         for (int ph = 0; ph < 4; ++ph) {
             const int py = ph >> 1, px = ph & 1, nx = 1 + px;
             const int cout = U.cout;
-            U.ph[ph] = pack(A, cout, U.cin, (1 + py) * nx, 8, [&](int co, int ci, int t) {
+            U.ph[ph] = pack(A, cout, U.cin, (1 + py) * nx, lama_convt_kc(ph), [&](int co, int ci, int t) {
                 const int a = t / nx, b = t % nx;
                 const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
                 return w[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
@@ -1196,7 +1196,7 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
     Packed ph[4];
     for (int k = 0; k < 4; ++k) {
         const int py = k >> 1, px = k & 1, nx = 1 + px;
-        ph[k] = pack(A, cout, cin, (1 + py) * nx, 8, [&](int co, int ci, int t) {
+        ph[k] = pack(A, cout, cin, (1 + py) * nx, lama_convt_kc(k), [&](int co, int ci, int t) {
             const int a = t / nx, b = t % nx;
             const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
             return wt[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
