@@ -94,10 +94,11 @@ struct ConvSeg {
     int pad_;
 };
 
-// Second argument of the grouped conv kernels, by value: the first workgroup
-// of problems 1..3 (INT32_MAX where absent), so a workgroup finds its problem
-// without reading the descriptors' block counts first (that chain of
-// dependent scalar loads sat at the head of every workgroup's prologue).
+// The first workgroup of problems 1..3 of a grouped conv launch (INT32_MAX
+// where absent), passed to the kernels as three scalar arguments that the
+// dispatch preloads into SGPRs, so a workgroup finds its problem without
+// reading the descriptors' block counts first (that chain of dependent scalar
+// loads sat at the head of every workgroup's prologue).
 #define LAMA_MAX_PROBS 4
 struct alignas(16) ProbStarts {
     int n;                       // number of problems (1..LAMA_MAX_PROBS)

@@ -619,14 +619,28 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
         epilogue<1, 64, PREFETCH>(acc[h], pre[h], P, epl, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
 }
 
+// Problem index of workgroup b, and b made relative to that problem's first
+// workgroup.  Selects over the (already loaded) starts, not an indexed read,
+// which would be one more dependent scalar load at the head of the prologue.
 __device__ __forceinline__ int find_problem(const ProbStarts &ps, int &b)
 {
-    int pi = 0;
+    int pi = 0, start = 0;
 #pragma unroll
-    for (int i = 0; i < LAMA_MAX_PROBS - 1; ++i) pi += b >= ps.s[i];
-    b -= pi == 0 ? 0 : ps.s[pi - 1];
+    for (int i = 0; i < LAMA_MAX_PROBS - 1; ++i) {
+        const bool in = b >= ps.s[i];
+        pi += in;
+        start = in ? ps.s[i] : start;
+    }
+    b -= start;
     return pi;
 }
+
+// Parameters of every conv kernel: the problem table and the first workgroup
+// of problems 1..3 as separate scalars, so all of them are preloaded into
+// SGPRs with the dispatch (-amdgpu-kernarg-preload-count) instead of being
+// fetched from the kernarg segment at the head of the prologue.
+#define LAMA_CONV_PARAMS const ConvProblem *__restrict__ probs, int ps1, int ps2, int ps3
+#define LAMA_CONV_STARTS const ProbStarts ps{0, {ps1, ps2, ps3}}
 
 using CfgHead = Cfg<7, 7, 1, true, 4, 2, 32>;
 using CfgDown = Cfg<3, 3, 2, true, 8, 2, 32>;
@@ -645,7 +659,7 @@ using CfgT11 = Cfg<2, 2, 1, false, LAMA_CONVT_KC3, 2, 32>;
 // keeps them in LDS and walks tiles blockIdx.x, + gridDim.x, ..., with the
 // next tile's 4-channel patch loaded into registers during this tile's MFMAs
 // and parked in the other of two patch buffers.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvProblem *__restrict__ probs, ProbStarts ps)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(LAMA_CONV_PARAMS)
 {
     using C = CfgHead;
     __shared__ __attribute__((aligned(16))) float lds[C::W_LDS + 2 * C::P_LDS];
@@ -707,8 +721,9 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(const ConvPro
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvProblem *__restrict__ probs, ProbStarts ps)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_PARAMS)
 {
+    LAMA_CONV_STARTS;
     __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
@@ -718,8 +733,9 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(const ConvP
 
 // FFC spatial convolutions: 3x3 stride 1 reflect pad 1, with an optional 1x1
 // second K segment (the SpectralTransform's conv2, summed before BN_g).
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvProblem *__restrict__ probs, ProbStarts ps)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PARAMS)
 {
+    LAMA_CONV_STARTS;
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(CfgFfc::LDS, CfgFfc1::LDS)];
     __shared__ float epl[192];
     int b = blockIdx.x;
@@ -731,9 +747,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(const ConvPro
 // conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
 // N % 4 == 0; lama_conv1x1_s takes any N.
 #define LAMA_PW_KERNEL(NAME, KC, VEC, NPX, PREFETCH, D)                                                      \
-    extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const ConvProblem *__restrict__ probs, ProbStarts ps) \
+    extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(LAMA_CONV_PARAMS) \
     {                                                                                                       \
         side_priority();                                                                                    \
+        LAMA_CONV_STARTS;                                                                                   \
         using C = PwCfg<KC, VEC, NPX>;                                                                      \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
@@ -756,8 +773,9 @@ LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, false, 64, true, LAMA_PW_DEPTH_RE
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions
 // (problems 0..3 = phases (py,px) = (0,0), (0,1), (1,0), (1,1)), each a valid
 // (1+py) x (1+px) convolution with zero fill at the bottom/right edge.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(const ConvProblem *__restrict__ probs, ProbStarts ps)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(LAMA_CONV_PARAMS)
 {
+    LAMA_CONV_STARTS;
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
     __shared__ float epl[192];
     int b = blockIdx.x;

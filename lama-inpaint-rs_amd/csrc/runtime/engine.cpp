@@ -883,7 +883,8 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t
 {
     void *arg = L.arg;
     ProbStarts ps = L.ps;
-    void *params[2] = {&arg, &ps};
+    // conv kernels: the table, then the three problem starts as scalars
+    void *params[4] = {&arg, &ps.s[0], &ps.s[1], &ps.s[2]};
     const bool prof = (prof_mask_ >> L.family) & 1u;
     Pending pe{};
     if (prof) {
