@@ -87,6 +87,12 @@ def main():
     # timed region, on every --sample-every-th pass (the events ride in the
     # dispatch packets; sampling keeps their cost out of `value`).
     dom = "conv3x3"
+    # the FFC 3x3 convolutions run as Winograd F(2,3) along x unless
+    # LAMA_FFC_WINO=0 selects the direct implicit GEMM; FLOPs are the
+    # convolution's algorithmic count either way (Winograd issues 2/3 of them
+    # as MFMA work)
+    wino = os.environ.get("LAMA_FFC_WINO", "1") != "0"
+    dom_kernel = "lama_conv3x3w" if wino else "lama_conv3x3"
     eng.profile_reset()
     eng.synchronize()
     t0 = time.perf_counter()
@@ -128,8 +134,9 @@ def main():
     if args.traffic and os.path.exists(args.traffic):
         with open(args.traffic) as fh:
             t = json.load(fh)
-        # only a measurement of the same launch shapes (same FLOPs per launch) applies
-        if t.get("size") == S and abs(t.get("flops_per_launch", 0) - flops_launch) <= 1e-6 * flops_launch:
+        # only a measurement of the same kernel and launch shapes applies
+        if (t.get("kernel") == dom_kernel and t.get("size") == S
+                and abs(t.get("flops_per_launch", 0) - flops_launch) <= 1e-6 * flops_launch):
             traffic = t["bytes_per_launch"]
 
     conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt", "conv1x1res"]
@@ -179,10 +186,17 @@ def main():
                                + {512: " (BASELINE configs[3])", 2048: " (BASELINE configs[4])",
                                   256: " (BASELINE configs[0] shape)"}.get(S, ""),
                    "h": S, "w": S, "mask_coverage": round(coverage, 4), "launches_per_pass": eng.launch_count(S, S)},
-        "roofline": {"bound": "mfma", "kernel": "lama_conv3x3 (FFC 3x3 implicit GEMMs, two 512-workgroup launches per FFC: l2l+l2g, then g2l in four 96-channel K ranges; per-launch figures average the two)",
+        "roofline": {"bound": "mfma",
+                     "kernel": (dom_kernel + (" (FFC 3x3 convolutions as Winograd F(2,3) along x, 256 workgroups of "
+                                              "64 channels x 2 rows x 64 px" if wino else
+                                              " (FFC 3x3 implicit GEMMs, 512 workgroups of 64 channels x 64 px")
+                                + "; two launches per FFC: l2l+l2g, then g2l in four 96-channel K ranges; "
+                                  "per-launch figures average the two; achieved counts the convolution's "
+                                  "algorithmic FLOPs)"),
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
-                     "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5)},
+                     "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5),
+                     "mfma_issued_frac": round(achieved * (2.0 / 3.0 if wino else 1.0) / PEAK_FP32_MFMA, 4)},
         "conv_tflops": round(conv_flops / (conv_ms * 1e9), 2),
         "conv_frac_of_peak": round(conv_flops / (conv_ms * 1e9) / PEAK_FP32_MFMA, 4),
         "fft_gbps": round(fft_bytes / (fft_ms * 1e6), 1) if fft_ms > 0 else None,

@@ -40,6 +40,11 @@ static inline constexpr int lama_convt_kc(int phase)
 {
     return phase == 0 ? LAMA_CONVT_KC0 : phase == 3 ? LAMA_CONVT_KC3 : phase == 1 ? LAMA_CONVT_KC1 : LAMA_CONVT_KC2;
 }
+// Input channels per K chunk of the Winograd FFC kernel (lama_conv3x3w);
+// its weights are packed in chunks of this many
+#ifndef LAMA_WINO_KC
+#define LAMA_WINO_KC 4
+#endif
 #define LAMA_TAIL_ROWS 8 // output tile of the 7x7 tail kernel (rows x columns)
 #define LAMA_TAIL_COLS 64
 

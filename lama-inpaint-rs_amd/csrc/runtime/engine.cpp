@@ -67,9 +67,12 @@ ProbStarts prob_starts(const ConvProblem *q, size_t n)
 }
 
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
-void tile_shape(int family, int &tr, int &tc)
+void tile_shape(int family, int &tr, int &tc, bool wino = false)
 {
-    if (family == F_CONV1 || family == F_CONV1R) {
+    if (family == F_CONV3 && wino) {  // lama_conv3x3w: 2 rows x 32 Winograd tiles
+        tr = 2;
+        tc = 64;
+    } else if (family == F_CONV1 || family == F_CONV1R) {
         tr = 1;
         tc = 64;
     } else {
@@ -140,6 +143,37 @@ Packed pack(Arena &A, int M, int C, int T, int KC, const std::function<float(int
                     const int ci = ck * KC + kc;
                     d[(((size_t)co * p.nchunk + ck) * T + t) * KC + kc] = ci < C ? get(co, ci, t) : 0.f;
                 }
+    return p;
+}
+
+// 3x3 weights for lama_conv3x3w: per output channel and chunk of
+// LAMA_WINO_KC input channels, [u][ky][ci] with U_u = sum over kx of G[u][kx] * w[ky][kx],
+// G = (1, 0, 0; 1/2, 1/2, 1/2; 1/2, -1/2, 1/2; 0, 0, 1) -- the Winograd F(2,3)
+// weight transform along x, evaluated in f64 and rounded once to f32.
+Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int)> &get)
+{
+    static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    constexpr int KC = LAMA_WINO_KC;
+    Packed p;
+    p.M = M;
+    p.C = C;
+    p.T = 12;  // (u, ky)
+    p.KC = KC;
+    p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
+    p.wrow = p.nchunk * 12 * KC;
+    p.off = A.add((size_t)M * p.wrow);
+    float *d = A.h.data() + p.off;
+    for (int co = 0; co < M; ++co)
+        for (int ck = 0; ck < p.nchunk; ++ck)
+            for (int u = 0; u < 4; ++u)
+                for (int ky = 0; ky < 3; ++ky)
+                    for (int kc = 0; kc < KC; ++kc) {
+                        const int ci = ck * KC + kc;
+                        double v = 0;
+                        if (ci < C)
+                            for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
+                        d[((size_t)co * p.nchunk + ck) * 12 * KC + (u * 3 + ky) * KC + kc] = (float)v;
+                    }
     return p;
 }
 
@@ -237,6 +271,8 @@ bool Engine::open(std::string &err)
         if (!check(hip_->hipModuleGetFunction(&fn_split_[f], module_, kSplitName[f]), kSplitName[f], err)) return false;
     for (int f = 0; f < 2; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err)) return false;
+    if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err)) return false;
+    wino_ = !(getenv("LAMA_FFC_WINO") && atoi(getenv("LAMA_FFC_WINO")) == 0);
     for (int s = 0; s < 2; ++s)
         for (int f = 0; f < 2; ++f)
             if (!check(hip_->hipModuleGetFunction(&fn_fft_ct_[s][f], module_, kFftCtName[s][f]), kFftCtName[s][f], err))
@@ -301,10 +337,12 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
                 !S.get(pf + ".convg2g.fu.conv_layer.weight", {384, 384, 1, 1}, fu, err) ||
                 !S.get(pf + ".convg2g.conv2.weight", {384, 192, 1, 1}, c2, err))
                 return false;
-            F.local = pack(A, 128, 512, 9, 8, [&](int co, int ci, int t) {
+            auto local = [&](int co, int ci, int t) {
                 return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
-            });
-            F.l2g = pack(A, 384, 128, 9, 8, [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; });
+            };
+            auto l2gw = [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; };
+            F.local = wino_ ? pack_wino(A, 128, 512, local) : pack(A, 128, 512, 9, 8, local);
+            F.l2g = wino_ ? pack_wino(A, 384, 128, l2gw) : pack(A, 384, 128, 9, 8, l2gw);
             F.conv2 = pack(A, 384, 192, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
             F.conv1 = pack(A, 192, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
             F.fu = pack(A, 384, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
@@ -406,6 +444,7 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
 hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
 {
+    if (family == F_CONV3 && wino_) return fn_wino_;
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
     for (size_t i = 0; i < n; ++i) {
         const ConvSeg &s = probs[i].s0;
@@ -627,7 +666,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc);
+        tile_shape(family, tr, tc, wino_);
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
         q.mblocks = (M + 63) / 64;
@@ -728,11 +767,12 @@ bool Engine::build_plan(Plan &p, std::string &err)
     auto part = [&](int k, int q) {
         const FfcW &Fw = ffc_[k];
         constexpr int RC = 384 / LAMA_G2L_RANGES;  // channels per g2l K range
-        static_assert(RC % 8 == 0, "whole K chunks per range");
+        static_assert(RC % 8 == 0 && RC % (2 * LAMA_WINO_KC) == 0, "whole K chunks (Winograd: chunk pairs) per range");
         const int c0 = q == 0 ? 0 : 128 + RC * (q - 1), nch = q == 0 ? 128 : RC;
-        ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8, Fw.local, nch, H8, W8);
-        sq.wt = wp(Fw.local.off) + (size_t)(c0 / 8) * 72;  // chunk c0/8 of the packed rows
-        sq.nchunk = nch / 8;
+        const Packed &pk = Fw.local;
+        ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8, pk, nch, H8, W8);
+        sq.wt = wp(pk.off) + (size_t)(c0 / pk.KC) * pk.T * pk.KC;  // chunk c0/KC of the packed rows
+        sq.nchunk = nch / pk.KC;
         return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, LQ + (size_t)q * 128 * P8, P8, W8, nullptr));
     };
     auto launch_a = [&](int k) {
@@ -1133,14 +1173,16 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     }
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
-    const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : 8;
+    const bool wino = family == F_CONV3 && wino_;
+    const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : 8;
     if ((size_t)4 * KC * h * w >= ((size_t)1 << 32)) {  // 32-bit staging offsets within a K chunk
         err = "op_conv2d: plane too large";
         return false;
     }
     Arena A;
     const int T = k * k;
-    Packed pk = pack(A, cout, cin, T, KC, [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; });
+    auto getw = [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; };
+    Packed pk = wino ? pack_wino(A, cout, cin, getw) : pack(A, cout, cin, T, KC, getw);
     size_t bn = A.add(2 * (size_t)cout);
     for (int i = 0; i < cout; ++i) {
         A.h[bn + i] = scale ? scale[i] : 1.f;
@@ -1164,7 +1206,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.OH = family == F_CONV1 ? 1 : oh;
     q.OW = family == F_CONV1 ? oh * ow : ow;
     int tr, tc;
-    tile_shape(family, tr, tc);
+    tile_shape(family, tr, tc, wino);
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
     q.mblocks = (cout + 63) / 64;

@@ -139,6 +139,11 @@ private:
     hipFunction_t fn_split_[4] = {};
     hipFunction_t fn_pw_any_[2] = {};  // 1x1 kernels for planes that are not float4-aligned
     hipFunction_t fn_fft_ct_[2][2] = {};  // [64x64, 32x32][rfft2, irfft2]
+    // FFC 3x3 convolutions as Winograd F(2,3) along x (lama_conv3x3w), or
+    // with LAMA_FFC_WINO=0 as the direct implicit GEMM (lama_conv3x3); chosen
+    // at open, since the weights are packed for one or the other
+    bool wino_ = true;
+    hipFunction_t fn_wino_ = nullptr;
     hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr;

@@ -47,6 +47,43 @@ def test_forward_steps_calibrated(pkg, engine, oracle_cal, h, w, kind):
     assert np.array_equal(u8g[keep], img[keep])
 
 
+@pytest.fixture(scope="module")
+def direct_engine(pkg, weights_dir):
+    # the engine reads LAMA_FFC_WINO when it opens
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_FFC_WINO", "0")
+        eng = pkg.hip_engine.Engine()
+    eng.load_weights(pkg.host_api.Store(weights_dir["cal"]))
+    yield eng
+    eng.close()
+
+
+@pytest.mark.parametrize("h,w,kind", [(64, 64, "rect"), (128, 96, "strokes"), (512, 512, "strokes")])
+def test_forward_direct_3x3_matches_winograd(pkg, direct_engine, engine, oracle_cal, h, w, kind):
+    """The forward with the FFC 3x3 convolutions as direct implicit GEMMs
+    (LAMA_FFC_WINO=0): every plan step within the per-layer bound of the
+    oracle (where it runs in seconds), and the output within float rounding
+    of the default Winograd forward, its composite within 1/255."""
+    img, mask = _case(pkg, h, w, kind)
+    x = pkg.host_api.build_input(img, mask)
+    print(f"case direct {h}x{w} {kind}", flush=True)
+    got, got_steps = direct_engine.forward_steps(x, list(range(29)))
+    if h * w <= 128 * 128:
+        ref, ref_steps = oracle_cal.forward(x, steps=True)
+        for s in range(29):
+            e = rel_err(got_steps[s], ref_steps[s])
+            assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+        assert rel_err(got, ref) < STEP_TOL
+    wino = engine.forward(x)
+    assert rel_err(got, wino) < 1e-4
+    u8g = pkg.host_api.composite(img, mask, got, 0, 0)
+    u8w = pkg.host_api.composite(img, mask, wino, 0, 0)
+    d = np.abs(u8g.astype(int) - u8w.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
+    keep = mask == 0
+    assert np.array_equal(u8g[keep], img[keep])
+
+
 def test_forward_plain_weights(pkg, weights_dir):
     """The BASELINE fixture as specified (uncalibrated BN statistics, so the
     activations grow by ~1e10 through the resblocks): per-step relative error

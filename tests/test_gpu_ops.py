@@ -133,3 +133,51 @@ def test_tail(engine, h, w):
     z = O.conv2d(O.reflect_pad(x, 3), wt, b, pad=0, stride=1, reflect=False)
     ref = (1.0 / (1.0 + np.exp(-z.astype(np.float64)))).astype(np.float32)
     assert rel_err(got, ref) < TOL
+
+
+@pytest.fixture(scope="module")
+def direct_engine(pkg):
+    # the engine reads LAMA_FFC_WINO when it opens
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_FFC_WINO", "0")
+        eng = pkg.hip_engine.Engine()
+    yield eng
+    eng.close()
+
+
+WINO_CASES = [
+    (40, 72, 13, 37),     # ragged channel chunk, odd width (last Winograd tile half outside), M % 64 != 0
+    (128, 128, 16, 16),   # resblock l2l shape at a 128x128 input
+    (384, 128, 64, 64),   # g2l at a 512x512 input
+    (12, 9, 3, 1),        # a one-pixel-wide plane (both taps reflect onto column 0); odd chunk count
+    (5, 64, 2, 130),      # more than one 64-pixel tile column, partial last one
+]
+
+
+@pytest.mark.parametrize("cin,cout,h,w", WINO_CASES)
+def test_conv3x3_winograd(engine, cin, cout, h, w):
+    """The FFC 3x3 convolution as Winograd F(2,3) along x (lama_conv3x3w, the
+    default) against the oracle's direct sum.  The transforms round
+    differently from the direct sum, within the same 1e-5 relative bound."""
+    rng = np.random.default_rng(cin * 100 + cout + w)
+    x = rng.standard_normal((cin, h, w), np.float32)
+    wt = (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
+    s, t = _bn(rng, cout)
+    print(f"case wino {cin}x{h}x{w} -> {cout}", flush=True)
+    got = engine.op_conv2d(x, wt, None, 1, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv2d(x, wt, None, pad=1, stride=1, reflect=True), s, t)
+    assert got.shape == ref.shape
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("cin,cout,h,w", WINO_CASES)
+def test_conv3x3_direct(direct_engine, cin, cout, h, w):
+    """The same cases on the direct implicit GEMM (LAMA_FFC_WINO=0)."""
+    rng = np.random.default_rng(cin * 100 + cout + w)
+    x = rng.standard_normal((cin, h, w), np.float32)
+    wt = (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
+    s, t = _bn(rng, cout)
+    print(f"case direct {cin}x{h}x{w} -> {cout}", flush=True)
+    got = direct_engine.op_conv2d(x, wt, None, 1, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv2d(x, wt, None, pad=1, stride=1, reflect=True), s, t)
+    assert rel_err(got, ref) < TOL
