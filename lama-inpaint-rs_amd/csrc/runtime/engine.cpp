@@ -224,6 +224,7 @@ Engine::~Engine()
     for (auto e : event_pool_) hip_->hipEventDestroy(e);
     for (auto e : ev_)
         if (e) hip_->hipEventDestroy(e);
+    if (g2l_) hip_->hipStreamDestroy(g2l_);
     if (side_) hip_->hipStreamDestroy(side_);
     if (stream_) hip_->hipStreamDestroy(stream_);
     if (module_) hip_->hipModuleUnload(module_);
@@ -283,9 +284,10 @@ bool Engine::open(std::string &err)
             max_lds_ = (size_t)lds;
     }
     if (!check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err) ||
-        !check(hip_->hipStreamCreate(&side_), "hipStreamCreate", err))
+        !check(hip_->hipStreamCreate(&side_), "hipStreamCreate", err) ||
+        !check(hip_->hipStreamCreate(&g2l_), "hipStreamCreate", err))
         return false;
-    // The cross-stream events only order work between this device's two
+    // The cross-stream events only order work between this device's
     // streams: no system-scope fence (a host-visible cache write-back at each
     // record costs microseconds on the critical path).
 #ifndef LAMA_EV_FLAGS
@@ -582,7 +584,9 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.s2 = take(384 * PS * 4);
     L.out = take(3 * P * 4);
     L.gc = take(2 * 384 * P8 * 4);  // the l2g partial, double-buffered by FFC parity
-    L.lq = take(LAMA_FIN_PARTS * 128 * P8 * 4);  // the FFC local GEMM's K-range partials
+    // the FFC local GEMM's K-range partials: l2l, then the g2l ranges twice (by
+    // FFC parity: B(k+1) may run while finalize(k) still reads B(k)'s)
+    L.lq = take((1 + 2 * LAMA_G2L_RANGES) * 128 * P8 * 4);
     L.tmp = take(fg.split ? fg.tmp_bytes : 0);
     L.twr = take(ntwr * 4);
     L.twc = take(ntwc * 4);
@@ -760,6 +764,10 @@ bool Engine::build_plan(Plan &p, std::string &err)
         q.relu = 0;
         return q;
     };
+    // LQ plane of local part q of FFC k: l2l at 0, g2l range q at q + (k%2)*ranges
+    auto lq_plane = [&](int k, int q) {
+        return LQ + (size_t)(q == 0 ? 0 : q + (k % 2) * LAMA_G2L_RANGES) * 128 * P8;
+    };
     // Local GEMM part q of FFC k, a raw partial into LQ plane q: part 0 is l2l
     // (input channels 0..127, 16 chunks of 8), parts 1-4 are g2l over input
     // channels 128 + 96 (q-1) .. +95 (12 chunks each), so the g2l launch is 512
@@ -773,7 +781,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8, pk, nch, H8, W8);
         sq.wt = wp(pk.off) + (size_t)(c0 / pk.KC) * pk.T * pk.KC;  // chunk c0/KC of the packed rows
         sq.nchunk = nch / pk.KC;
-        return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, LQ + (size_t)q * 128 * P8, P8, W8, nullptr));
+        return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, lq_plane(k, q), P8, W8, nullptr));
     };
     auto launch_a = [&](int k) {
         const FfcW &Fw = ffc_[k];
@@ -784,17 +792,23 @@ bool Engine::build_plan(Plan &p, std::string &err)
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
                     k % 2 ? EV_A1 : EV_A0);
     };
+    // B(k) on its own stream overlaps A(k+1); LAMA_B_STREAM=0 keeps it in the
+    // main stream's order (the two are bit-identical)
+    const bool b_stream = !(getenv("LAMA_B_STREAM") && atoi(getenv("LAMA_B_STREAM")) == 0);
     auto launch_b = [&](int k) {
         std::vector<ConvProblem> probs;
         for (int q = 1; q <= LAMA_G2L_RANGES; ++q) probs.push_back(part(k, q));
+        // own stream: waits for x_g(k) (conv2(k-1), or model.4 for k = 0) and
+        // records EV_B for finalize(k); else in the main stream's order
+        const int xg = k == 0 ? EV_FORK : ((k - 1) % 2 ? EV_S1 : EV_S0);
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
                     f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9),
-                    S_MAIN, k == 0 ? -1 : ((k - 1) % 2 ? EV_S1 : EV_S0));
+                    b_stream ? S_G2L : S_MAIN, b_stream || k > 0 ? xg : -1, b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1);
     };
     auto launch_finalize = [&](int k) {
         const FfcW &Fw = ffc_[k];
         FinalizeArgs fa2{};
-        for (int q = 0; q < LAMA_FIN_PARTS; ++q) fa2.part[q] = LQ + (size_t)q * 128 * P8;
+        for (int q = 0; q < LAMA_FIN_PARTS; ++q) fa2.part[q] = lq_plane(k, q);
         fa2.nparts = LAMA_FIN_PARTS;
         fa2.C = 128;
         fa2.plane = (long)P8;
@@ -806,7 +820,8 @@ bool Engine::build_plan(Plan &p, std::string &err)
         L.fn = fn_[F_FINAL];
         L.family = F_FINAL;
         L.stream = S_MAIN;
-        L.wait_ev = L.record_ev = -1;
+        L.wait_ev = b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1;
+        L.record_ev = -1;
         L.grid = (unsigned)(((128 * P8 + 3) / 4 + LAMA_NT - 1) / LAMA_NT);
         L.arg = put(&fa2, sizeof fa2);
         L.nparams = 1;
@@ -978,7 +993,7 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
 {
     // LAMA_STREAMS=1 puts the side-stream work on the main stream (profiling)
     static const bool single = getenv("LAMA_STREAMS") && atoi(getenv("LAMA_STREAMS")) == 1;
-    hipStream_t st[2] = {s, single ? s : side_};
+    hipStream_t st[S_COUNT] = {s, single ? s : side_, single ? s : g2l_};
     for (const Launch &L : p.launches) {
         hipStream_t ls = st[L.stream];
         if (L.wait_ev >= 0 && !check(hip_->hipStreamWaitEvent(ls, ev_[L.wait_ev], 0), "hipStreamWaitEvent", err))

@@ -29,11 +29,15 @@ struct Packed {
 // Streams of a forward: the main one (the caller's) and a side stream that
 // carries the SpectralTransform chain of every FFC concurrently with the
 // FFC's spatial GEMM.  Cross-stream order is kept with the engine's events.
-enum { S_MAIN = 0, S_SIDE = 1 };
+// S_G2L carries the FFC's g2l launch B(k), so that B(k+1) overlaps A(k+1): they read
+// different inputs (x_g from the side stream, x_l from the main stream's finalize).
+// LAMA_B_STREAM=0 runs B on the main stream instead.
+enum { S_MAIN = 0, S_SIDE = 1, S_G2L = 2, S_COUNT = 3 };
 // EV_FORK: model.4 done (the side stream's first input); EV_A0/1: FFC k's
 // l2l + l2g launch done (its GC partial), by parity of k; EV_S0/1: FFC k's
 // conv2 done (its global output half), by parity of k.
-enum { EV_FORK = 0, EV_A0 = 1, EV_A1 = 2, EV_S0 = 3, EV_S1 = 4, EV_COUNT = 5 };
+// EV_B0/1: FFC k's g2l launch done (on S_G2L), by parity of k.
+enum { EV_FORK = 0, EV_A0 = 1, EV_A1 = 2, EV_S0 = 3, EV_S1 = 4, EV_B0 = 5, EV_B1 = 6, EV_COUNT = 7 };
 
 struct Launch {
     hipFunction_t fn;
@@ -146,7 +150,7 @@ private:
     hipFunction_t fn_wino_ = nullptr;
     hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
-    hipStream_t stream_ = nullptr, side_ = nullptr;
+    hipStream_t stream_ = nullptr, side_ = nullptr, g2l_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};
     bool capturing_ = false;  // run() is recording a graph
 

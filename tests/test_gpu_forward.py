@@ -84,6 +84,46 @@ def test_forward_direct_3x3_matches_winograd(pkg, direct_engine, engine, oracle_
     assert np.array_equal(u8g[keep], img[keep])
 
 
+@pytest.mark.parametrize("h,w", [(512, 512), (256, 384)])
+def test_g2l_stream_matches_single_order(pkg, engine, monkeypatch, h, w):
+    """The FFC's g2l launch B(k) on a stream of its own (LAMA_B_STREAM=1),
+    overlapping A(k+1), ordered by events (B waits for x_g, finalize waits
+    for B) and with the g2l partials double-buffered by FFC parity: three
+    passes with different inputs queued back to back, each into its own
+    output, all bit-identical to the default schedule's forward."""
+    H = pkg.host_api
+    xs = []
+    for seed in range(3):
+        img = H.synth_image(h, w, seed + 1)
+        mask, _ = H.synth_mask_strokes(h, w, 0.25, seed + 2)
+        xs.append(H.build_input(img, mask))
+    monkeypatch.setenv("LAMA_B_STREAM", "0")
+    eng0 = pkg.hip_engine.Engine()
+    eng0.load_weights(engine._cal_store)
+    ref = [eng0.forward(x) for x in xs]
+    eng0.close()
+    monkeypatch.setenv("LAMA_B_STREAM", "1")
+    eng1 = pkg.hip_engine.Engine()
+    eng1.load_weights(engine._cal_store)
+    d_in = [eng1.malloc(x.nbytes) for x in xs]
+    d_out = [eng1.malloc(3 * h * w * 4) for _ in xs]
+    for d, x in zip(d_in, xs):
+        eng1.upload(d, x)
+    print(f"case {h}x{w} g2l stream, 2 x 3 queued passes", flush=True)
+    for rep in range(2):
+        for d, o in zip(d_in, d_out):
+            eng1.forward_device(d, h, w, o)
+        eng1.synchronize()
+        for i, o in enumerate(d_out):
+            out = np.empty((3, h, w), np.float32)
+            eng1.download(out, o)
+            assert np.array_equal(out, ref[i]), f"rep {rep} pass {i}"
+    assert np.array_equal(eng1.forward(xs[1]), ref[1])
+    for d in d_in + d_out:
+        eng1.free(d)
+    eng1.close()
+
+
 def test_forward_plain_weights(pkg, weights_dir):
     """The BASELINE fixture as specified (uncalibrated BN statistics, so the
     activations grow by ~1e10 through the resblocks): per-step relative error
