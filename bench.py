@@ -190,9 +190,10 @@ def main():
                      "kernel": (dom_kernel + (" (FFC 3x3 convolutions as Winograd F(2,3) along x, 256 workgroups of "
                                               "64 channels x 2 rows x 64 px" if wino else
                                               " (FFC 3x3 implicit GEMMs, 512 workgroups of 64 channels x 64 px")
-                                + "; two launches per FFC: l2l+l2g, then g2l in four 96-channel K ranges; "
-                                  "per-launch figures average the two; achieved counts the convolution's "
-                                  "algorithmic FLOPs)"),
+                                + "; two launches per FFC, l2l+l2g and g2l in four 96-channel K ranges, which "
+                                  "overlap on two streams, so a launch's duration includes the time it shares the "
+                                  "CUs with the other; per-launch figures average the two; achieved counts the "
+                                  "convolution's algorithmic FLOPs)"),
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
                      "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5),
