@@ -198,8 +198,12 @@ def main():
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
                      "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5),
                      "mfma_issued_frac": round(achieved * (2.0 / 3.0 if wino else 1.0) / PEAK_FP32_MFMA, 4)},
+        # conv FLOPs over the conv kernels' summed launch times (launches that overlap
+        # on different streams are counted once each), and over the pass's wall time
         "conv_tflops": round(conv_flops / (conv_ms * 1e9), 2),
         "conv_frac_of_peak": round(conv_flops / (conv_ms * 1e9) / PEAK_FP32_MFMA, 4),
+        "pass_conv_tflops": round(conv_flops / (ms * 1e9), 2),
+        "pass_conv_frac_of_peak": round(conv_flops / (ms * 1e9) / PEAK_FP32_MFMA, 4),
         "fft_gbps": round(fft_bytes / (fft_ms * 1e6), 1) if fft_ms > 0 else None,
         "fft_frac_of_hbm": round(fft_bytes / (fft_ms * 1e6) / PEAK_HBM, 4) if fft_ms > 0 else None,
         "host_io_passes_per_s": round(host_io, 3),
