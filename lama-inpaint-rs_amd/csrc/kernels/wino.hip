@@ -16,10 +16,12 @@
 // Winograd tiles per row).  Wave (wm, wn) owns channels wm*32 .. +32 of
 // output row wn, as four 32 x 32 accumulators (u = 0..3) of
 // v_mfma_f32_32x32x2f32: GEMM rows are output channels, GEMM columns the 32
-// tiles of the row, K = (ci, ky).  K is walked in chunks of 4 input channels;
-// per chunk the block stages in LDS the transformed weights [64 co][u][ky][4]
-// and the transformed input [4 rows][u][32 tiles][4 (+2 pad)], with the same
-// two-stage pipeline as the direct kernels.
+// tiles of the row, K = (ci, ky).  K is walked in chunks of LAMA_WINO_KC = 4
+// input channels; per chunk the block stages in LDS the transformed weights
+// [64 co][u][ky][4] and the transformed input [4 rows][u][32 tiles][4 (+2
+// pad)], with the same two-stage pipeline as the direct kernels.  The chunk
+// count is even (the host pads the packed weights with a zero chunk), so the
+// K loop runs in chunk pairs with a single exit.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -29,7 +31,7 @@ namespace {
 struct WCfg {
     static constexpr int KC = LAMA_WINO_KC;         // input channels per chunk
     static constexpr int NU = 4, KY = 3;            // Winograd positions, kernel rows
-    static constexpr int WK = NU * KY * KC;         // 48 weights per output channel and chunk
+    static constexpr int WK = NU * KY * KC;         // weights per output channel and chunk
     static constexpr int WSTR = WK + 4;             // LDS row stride (= 4 mod 8)
     static constexpr int NT = 32;                   // tiles per output row
     static constexpr int TR = 2, TC = 2 * NT;       // output rows x pixels per block
@@ -122,9 +124,11 @@ __device__ __forceinline__ void wino_store(const WStage &st, const WSlots &sl, f
     }
 }
 
-// MFMAs of one chunk: for each (ky, u) one 8-byte weight read and one 8-byte
-// input read per lane (the two K slots are channels g*2, g*2+1 of lane half
-// g); the reads of the next (ky, u) are issued before the current MFMAs.
+// MFMAs of one chunk: for each (ky, u), lane half g reads its H = KC/2
+// channels H*g .. H*g + H - 1 of the weights and of the input (one 8-byte
+// read each at KC = 4) and feeds one of them to each of H MFMAs as the
+// MFMA's K slot g; the reads of the next (ky, u) are issued before the
+// current MFMAs.
 __device__ __forceinline__ void wino_compute(f32x16 (&acc)[WCfg::NU], const float *lds)
 {
     using C = WCfg;
