@@ -9,7 +9,7 @@
 // input channels per K chunk of the pointwise (1x1) convolutions; their
 // weights are packed in chunks of this many
 #ifndef LAMA_PW_KC
-#define LAMA_PW_KC 32
+#define LAMA_PW_KC 16
 #endif
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
 

@@ -442,9 +442,10 @@ __device__ __forceinline__ void pw_compute_chunk(f32x16 (&acc)[C::NACC], const f
 // one barrier per chunk.  Chunk c's global loads are issued D steps before it
 // is written to LDS (at step c - 1) and consumed at step c, so each load has
 // D chunks of MFMA time to land; these small-K GEMMs run one wave per SIMD
-// and are bound by that latency.
+// and are bound by that latency.  A depth that divides the chunk counts (12
+// and 24 at 16 channels) keeps the unrolled group free of early exits.
 #ifndef LAMA_PW_DEPTH
-#define LAMA_PW_DEPTH 3
+#define LAMA_PW_DEPTH 4
 #endif
 template <class C, int D>
 __device__ __forceinline__ void run_segment_pw(f32x16 (&acc)[C::NACC], const ConvSeg &sg_mem, int m0, int M, int ox0,

@@ -22,8 +22,8 @@
 
 namespace lama {
 
-const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt",
-                                          "rfft2",   "irfft2",    "tail",    "finalize", "conv1x1res"};
+const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3",  "conv1x1",    "convt",     "rfft2",
+                                          "irfft2",  "tail",      "finalize", "conv1x1res", "conv3x3g2l"};
 
 size_t step_numel(int step, int h, int w)
 {
@@ -46,7 +46,7 @@ namespace {
 
 const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lama_conv3x3", "lama_conv1x1",
                                           "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail",
-                                          "lama_finalize", "lama_conv1x1_res"};
+                                          "lama_finalize", "lama_conv1x1_res", "lama_conv3x3"};
 
 const char *const kSplitName[4] = {"lama_rfft2_rows", "lama_rfft2_cols", "lama_irfft2_cols", "lama_irfft2_rows"};
 
@@ -446,7 +446,7 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
 hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
 {
-    if (family == F_CONV3 && wino_) return fn_wino_;
+    if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
     for (size_t i = 0; i < n; ++i) {
         const ConvSeg &s = probs[i].s0;
@@ -801,7 +801,7 @@ bool Engine::build_plan(Plan &p, std::string &err)
         // own stream: waits for x_g(k) (conv2(k-1), or model.4 for k = 0) and
         // records EV_B for finalize(k); else in the main stream's order
         const int xg = k == 0 ? EV_FORK : ((k - 1) % 2 ? EV_S1 : EV_S0);
-        conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
+        conv_launch(F_CONV3G, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
                     f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9),
                     b_stream ? S_G2L : S_MAIN, b_stream || k > 0 ? xg : -1, b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1);
     };
@@ -959,7 +959,11 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t
     const unsigned block = L.block ? L.block : LAMA_NT;
     if (prof) {
         // the events ride in the dispatch packet itself (no marker packets on
-        // the stream), so timing a kernel does not stall the queue around it
+        // the stream), so timing a kernel does not stall the queue around it.
+        // A launch issued after a cross-stream wait is timed from the wait's
+        // barrier packet (it then reads long by the time spent waiting,
+        // whether the events ride in the packet or are separate markers), so
+        // kernel time is read from launches that wait on nothing.
         if (!check(hip_->hipExtModuleLaunchKernel(L.fn, L.grid * block, 1, 1, block, 1, 1, L.shmem, s, params, nullptr,
                                                   pe.a, pe.b, 0),
                    kFamilyName[L.family], err))
@@ -1019,10 +1023,10 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
                 tmp.resize(src.second);
                 dst = tmp.data();
             }
-            // a step is complete when both streams have drained
-            if (!check(hip_->hipStreamSynchronize(st[0]), "hipStreamSynchronize", err) ||
-                !check(hip_->hipStreamSynchronize(st[1]), "hipStreamSynchronize", err) ||
-                !check(hip_->hipMemcpyAsync(dst, src.first, src.second * 4, hipMemcpyDeviceToHost, s), "hipMemcpy(dump)", err) ||
+            // a step is complete when every stream has drained
+            for (hipStream_t q : st)
+                if (!check(hip_->hipStreamSynchronize(q), "hipStreamSynchronize", err)) return false;
+            if (!check(hip_->hipMemcpyAsync(dst, src.first, src.second * 4, hipMemcpyDeviceToHost, s), "hipMemcpy(dump)", err) ||
                 !check(hip_->hipStreamSynchronize(s), "hipStreamSynchronize", err))
                 return false;
             if (stp == 26 && steps[27]) host_reflect_pad(dst, 64, p.H, p.W, 3, steps[27]);

@@ -12,7 +12,9 @@
 
 namespace lama {
 
-enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_CONV1R, F_COUNT };
+// F_CONV3G: the FFC's g2l launches, the same kernel as F_CONV3 (l2l + l2g);
+// a family of its own so that profiling keeps the two launches apart.
+enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_CONV1R, F_CONV3G, F_COUNT };
 extern const char *const kFamilyName[F_COUNT];
 
 // Number of plan steps of the reference (model.rs:135-207) and the size in

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 HIP_SO = os.path.join(HERE, "lib", "liblama_hip.so")
 
 FAMILIES = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt", "rfft2", "irfft2", "tail", "finalize",
-            "conv1x1res"]
+            "conv1x1res", "conv3x3g2l"]
 N_STEPS = 29
 
 _lib = None
