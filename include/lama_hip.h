@@ -71,9 +71,11 @@ int lama_hip_vram(uint64_t *free_bytes, uint64_t *total_bytes, char *name, size_
 /* Per-kernel timing, the analogue of LAMA_PROFILE_OPS / print_op_stats
  * (cuda.rs:1703-1782): while enabled, every launch of a kernel family whose
  * bit is set in `mask` is bracketed by events on the stream it runs on.
- * Families: 0 conv7x7, 1 conv3x3s2, 2 conv3x3 (FFC), 3 conv1x1, 4 convt,
- * 5 rfft2, 6 irfft2, 7 tail, 8 finalize (FFC local branch epilogue),
- * 9 conv1x1res (SpectralTransform conv2 with the l2g addend). */
+ * Families: 0 conv7x7, 1 conv3x3s2, 2 conv3x3 (FFC l2l + l2g), 3 conv1x1,
+ * 4 convt, 5 rfft2, 6 irfft2, 7 tail, 8 finalize (FFC local branch
+ * epilogue), 9 conv1x1res (SpectralTransform conv2 with the l2g addend),
+ * 10 conv3x3g2l (FFC g2l).  A launch issued after a wait on another stream
+ * is timed from that wait, so its time includes the wait. */
 int lama_hip_profile(lama_hip_ctx *ctx, uint32_t mask);
 void lama_hip_profile_reset(lama_hip_ctx *ctx);
 /* Family i's accumulated launches, device milliseconds (waits for the
