@@ -45,8 +45,17 @@ static inline constexpr int lama_convt_kc(int phase)
 #ifndef LAMA_WINO_KC
 #define LAMA_WINO_KC 4
 #endif
-#define LAMA_TAIL_ROWS 8 // output tile of the 7x7 tail kernel (rows x columns)
+// output tile of the 7x7 tail kernel (rows x columns) and the adjacent
+// pixels each of its threads computes
+#ifndef LAMA_TAIL_ROWS
+#define LAMA_TAIL_ROWS 8
+#endif
+#ifndef LAMA_TAIL_COLS
 #define LAMA_TAIL_COLS 64
+#endif
+#ifndef LAMA_TAIL_PX
+#define LAMA_TAIL_PX 2
+#endif
 
 #ifdef __HIP_DEVICE_COMPILE__
 // Wave priority of the SpectralTransform chain (conv1, rfft2, FU conv,

@@ -13,7 +13,7 @@
 #include "common.h"
 
 namespace {
-constexpr int TROWS = LAMA_TAIL_ROWS, TCOLS = LAMA_TAIL_COLS, PX = 2;
+constexpr int TROWS = LAMA_TAIL_ROWS, TCOLS = LAMA_TAIL_COLS, PX = LAMA_TAIL_PX;
 static_assert(TROWS * TCOLS / PX == LAMA_NT, "one thread per PX pixels of the tile");
 constexpr int PR = TROWS + 6, PC = TCOLS + 6;
 
