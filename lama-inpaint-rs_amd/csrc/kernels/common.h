@@ -12,6 +12,13 @@
 #define LAMA_PW_KC 16
 #endif
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
+// LDS bytes of the two ping-pong buffers of a split-mode FFT block (row pairs
+// or columns per block = this / (2 * 8 * plane side)).  32 KB rather than 64:
+// a block then fits on a CU beside the FFC GEMM's two workgroups (51 KB each),
+// so the side stream's transforms are not held back by that GEMM's launches.
+#ifndef LAMA_FFT_SPLIT_LDS
+#define LAMA_FFT_SPLIT_LDS (32 * 1024)
+#endif
 
 // Complex values per ping-pong buffer of the single-block FFT kernels: the
 // row-pair layout [(h+1)/2][w] or the half spectrum [h][w/2+1], rounded up to

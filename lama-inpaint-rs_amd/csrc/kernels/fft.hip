@@ -792,3 +792,223 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
 LAMA_FFT_CT(64)
 LAMA_FFT_CT(32)
 #undef LAMA_FFT_CT
+
+// ---- split mode with compile-time shapes: square power-of-two planes -------
+//
+// The 128x128 and 256x256 bottleneck planes (1024^2 and 2048^2 inputs) take
+// the row/column split launches above, with the plane shape, the row pairs per
+// row block and the columns per column block compiled in.  Both counts are
+// LAMA_FFT_SPLIT_LDS / (16 N): the two ping-pong buffers fill that many
+// bytes, as in the host's split geometry for these planes.  Each row block's 2*PB real rows are contiguous in memory and
+// are read as float4s.  The W/2+1 kept columns are CB-wide column blocks
+// plus one block holding the Nyquist column alone.  Butterflies, twiddles and
+// pass order are those of the kernels above (sign -1 forward, +1 inverse).
+
+namespace {
+
+template <int N>
+struct SplitCt {
+    static constexpr int W = N, H = N, Wh = N / 2 + 1, HP = N / 2, NT = LAMA_FFT_NT;
+    static constexpr int PB = LAMA_FFT_SPLIT_LDS / 8 / (2 * N), CB = PB;  // row pairs / columns per block
+    static constexpr int RCH = HP / PB;                             // row blocks per channel
+    static constexpr int CCH = (Wh + CB - 1) / CB;                  // column blocks per channel
+    static_assert(HP % PB == 0 && Wh == (CCH - 1) * CB + 1, "whole row blocks; the last column block is Nyquist");
+    static_assert(W <= NT && (PB * W / 4) % NT == 0 && (PB * W) % NT == 0, "whole per-thread shares");
+};
+
+// real [C][H][W] -> tmp: x transforms of PB row pairs of one channel
+template <int N>
+__device__ __forceinline__ void rfft2_rows_ct(const FftArgs &A, float2 *sm)
+{
+    using S = SplitCt<N>;
+    constexpr int W = S::W, Wh = S::Wh, PB = S::PB, NT = S::NT, W4 = W / 4, RQ = PB * W4 / NT;
+    float2 *b0 = sm, *b1 = sm + PB * W, *twr = sm + 2 * PB * W;
+    const int c = blockIdx.x / S::RCH, p0 = (blockIdx.x % S::RCH) * PB;
+    const float2 tv = gp(reinterpret_cast<const float2 *>(A.row.tw))[min((int)threadIdx.x, W - 1)];
+    const LAMA_GLOBAL float4 *src =
+        reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.in) + ((long)c * N + 2 * p0) * W);
+    float4 qa[RQ], qb[RQ];
+#pragma unroll
+    for (int k = 0; k < RQ; ++k) {
+        const int q = threadIdx.x + k * NT, p = q / W4, x4 = q % W4;
+        qa[k] = src[(2 * p) * W4 + x4];
+        qb[k] = src[(2 * p + 1) * W4 + x4];
+    }
+    if (threadIdx.x < W) twr[threadIdx.x] = tv;
+#pragma unroll
+    for (int k = 0; k < RQ; ++k) {
+        const int q = threadIdx.x + k * NT, p = q / W4, x = (q % W4) * 4;
+        float2 *d = b0 + p * W + x;
+        d[0] = make_float2(qa[k].x, qb[k].x);
+        d[1] = make_float2(qa[k].y, qb[k].y);
+        d[2] = make_float2(qa[k].z, qb[k].z);
+        d[3] = make_float2(qa[k].w, qb[k].w);
+    }
+    __syncthreads();
+    const float2 *r = ct_stockham<W, 1, PB, W, 1, -1>(b0, b1, twr);
+    LAMA_GLOBAL float2 *t = gp(reinterpret_cast<float2 *>(A.tmp)) + ((long)c * N + 2 * p0) * Wh;
+    for (int idx = threadIdx.x; idx < 2 * PB * Wh; idx += NT) {
+        const int y = idx / Wh, k = idx % Wh, p = y >> 1;
+        const float2 z = r[p * W + k], zm = r[p * W + ((W - k) & (W - 1))];
+        t[idx] = (y & 1) ? make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x))
+                         : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+    }
+}
+
+// tmp -> stacked [2C][H][Wh]: y transforms of NC columns x0.. of channel c
+template <int N, int NC>
+__device__ __forceinline__ void rfft2_cols_ct(const FftArgs &A, float2 *sm, int c, int x0)
+{
+    using S = SplitCt<N>;
+    constexpr int H = S::H, Wh = S::Wh, CB = S::CB, NT = S::NT, L = (H * NC + NT - 1) / NT;
+    float2 *b0 = sm, *b1 = sm + H * CB, *twc = sm + 2 * H * CB;
+    const float2 tv = gp(reinterpret_cast<const float2 *>(A.col.tw))[min((int)threadIdx.x, H - 1)];
+    const LAMA_GLOBAL float2 *t = gp(reinterpret_cast<const float2 *>(A.tmp)) + (long)c * H * Wh + x0;
+    float2 v[L];
+#pragma unroll
+    for (int k = 0; k < L; ++k) {
+        const int idx = min((int)threadIdx.x + k * NT, H * NC - 1), y = idx / NC, j = idx % NC;
+        v[k] = t[y * Wh + j];
+    }
+    if (threadIdx.x < H) twc[threadIdx.x] = tv;
+#pragma unroll
+    for (int k = 0; k < L; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        if ((H * NC) % NT != 0 && idx >= H * NC) break;
+        b0[idx] = v[k];
+    }
+    __syncthreads();
+    const float2 *q = ct_stockham<H, 1, NC, 1, NC, -1>(b0, b1, twc);
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh + x0, *dim = dre + H * Wh;
+    for (int idx = threadIdx.x; idx < H * NC; idx += NT) {
+        const int y = idx / NC, j = idx % NC;
+        const float2 u = q[idx];
+        dre[y * Wh + j] = u.x * A.scale;
+        dim[y * Wh + j] = u.y * A.scale;
+    }
+}
+
+// stacked [2C][H][Wh] -> tmp: inverse y transforms of NC columns x0.. of channel c
+template <int N, int NC>
+__device__ __forceinline__ void irfft2_cols_ct(const FftArgs &A, float2 *sm, int c, int x0)
+{
+    using S = SplitCt<N>;
+    constexpr int H = S::H, Wh = S::Wh, CB = S::CB, NT = S::NT, L = (H * NC + NT - 1) / NT;
+    float2 *b0 = sm, *b1 = sm + H * CB, *twc = sm + 2 * H * CB;
+    const float2 tv = gp(reinterpret_cast<const float2 *>(A.col.tw))[min((int)threadIdx.x, H - 1)];
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh + x0, *sim = sre + H * Wh;
+    float2 v[L];
+#pragma unroll
+    for (int k = 0; k < L; ++k) {
+        const int idx = min((int)threadIdx.x + k * NT, H * NC - 1), y = idx / NC, j = idx % NC;
+        v[k] = make_float2(sre[y * Wh + j], sim[y * Wh + j]);
+    }
+    if (threadIdx.x < H) twc[threadIdx.x] = tv;
+#pragma unroll
+    for (int k = 0; k < L; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        if ((H * NC) % NT != 0 && idx >= H * NC) break;
+        b0[idx] = v[k];
+    }
+    __syncthreads();
+    const float2 *q = ct_stockham<H, 1, NC, 1, NC, 1>(b0, b1, twc);
+    LAMA_GLOBAL float2 *t = gp(reinterpret_cast<float2 *>(A.tmp)) + (long)c * H * Wh + x0;
+    for (int idx = threadIdx.x; idx < H * NC; idx += NT) {
+        const int y = idx / NC, j = idx % NC;
+        t[y * Wh + j] = q[idx];
+    }
+}
+
+// tmp -> real [C][H][W]: complex-to-real x transforms of PB row pairs of one
+// channel, ortho scale, plus feat
+template <int N>
+__device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
+{
+    using S = SplitCt<N>;
+    constexpr int W = S::W, Wh = S::Wh, PB = S::PB, NT = S::NT;
+    constexpr int NF = 2 * PB * W / 4 / NT, NZ = PB * W / NT;  // feat float4s, row-pair values per thread
+    float2 *b0 = sm, *b1 = sm + PB * W, *twr = sm + 2 * PB * W;
+    const int c = blockIdx.x / S::RCH, p0 = (blockIdx.x % S::RCH) * PB;
+    const float2 tv = gp(reinterpret_cast<const float2 *>(A.row.tw))[min((int)threadIdx.x, W - 1)];
+    const long base = ((long)c * N + 2 * p0) * W;
+    const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.feat) + base);
+    float4 fpre[NF];
+#pragma unroll
+    for (int k = 0; k < NF; ++k) fpre[k] = f4[threadIdx.x + k * NT];
+    // the Hermitian rows 2p and 2p+1, completed from the stored half spectra
+    const LAMA_GLOBAL float2 *t = gp(reinterpret_cast<const float2 *>(A.tmp)) + ((long)c * N + 2 * p0) * Wh;
+    float2 g[NZ][2];
+#pragma unroll
+    for (int k = 0; k < NZ; ++k) {
+        const int idx = threadIdx.x + k * NT, p = idx / W, x = idx % W;
+        const int col = x < Wh ? x : W - x;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) g[k][h] = t[(2 * p + h) * Wh + col];
+    }
+    if (threadIdx.x < W) twr[threadIdx.x] = tv;
+#pragma unroll
+    for (int k = 0; k < NZ; ++k) {
+        const int idx = threadIdx.x + k * NT, x = idx % W;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (x >= Wh) g[k][h].y = -g[k][h].y;
+            else if (x == 0 || 2 * x == W) g[k][h].y = 0.f;
+        }
+        b0[idx] = make_float2(g[k][0].x - g[k][1].y, g[k][0].y + g[k][1].x);
+    }
+    __syncthreads();
+    const float2 *q = ct_stockham<W, 1, PB, W, 1, 1>(b0, b1, twr);
+    LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + base);
+#pragma unroll
+    for (int k = 0; k < NF; ++k) {
+        const int i4 = threadIdx.x + k * NT, idx = i4 * 4, y = idx / W, x = idx % W;
+        const float2 *v = q + (y >> 1) * W + x;
+        float4 o4 = (y & 1) ? make_float4(v[0].y, v[1].y, v[2].y, v[3].y) : make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
+        o4.x = o4.x * A.scale + fpre[k].x;
+        o4.y = o4.y * A.scale + fpre[k].y;
+        o4.z = o4.z * A.scale + fpre[k].z;
+        o4.w = o4.w * A.scale + fpre[k].w;
+        d4[i4] = o4;
+    }
+}
+
+}  // namespace
+
+#define LAMA_FFT_SPLIT_CT(N)                                                                                         \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows_##N(const FftArgs *__restrict__ args)  \
+    {                                                                                                                \
+        side_priority();                                                                                             \
+        extern __shared__ float2 sm[];                                                                               \
+        rfft2_rows_ct<N>(*args, sm);                                                                                 \
+    }                                                                                                                \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols_##N(const FftArgs *__restrict__ args)  \
+    {                                                                                                                \
+        side_priority();                                                                                             \
+        extern __shared__ float2 sm[];                                                                               \
+        using S = SplitCt<N>;                                                                                        \
+        const int c = blockIdx.x / S::CCH, ch = blockIdx.x % S::CCH;                                                 \
+        if (ch < S::CCH - 1)                                                                                         \
+            rfft2_cols_ct<N, S::CB>(*args, sm, c, ch * S::CB);                                                       \
+        else                                                                                                         \
+            rfft2_cols_ct<N, 1>(*args, sm, c, ch * S::CB);                                                           \
+    }                                                                                                                \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols_##N(const FftArgs *__restrict__ args) \
+    {                                                                                                                \
+        side_priority();                                                                                             \
+        extern __shared__ float2 sm[];                                                                               \
+        using S = SplitCt<N>;                                                                                        \
+        const int c = blockIdx.x / S::CCH, ch = blockIdx.x % S::CCH;                                                 \
+        if (ch < S::CCH - 1)                                                                                         \
+            irfft2_cols_ct<N, S::CB>(*args, sm, c, ch * S::CB);                                                      \
+        else                                                                                                         \
+            irfft2_cols_ct<N, 1>(*args, sm, c, ch * S::CB);                                                          \
+    }                                                                                                                \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows_##N(const FftArgs *__restrict__ args) \
+    {                                                                                                                \
+        side_priority();                                                                                             \
+        extern __shared__ float2 sm[];                                                                               \
+        irfft2_rows_ct<N>(*args, sm);                                                                                \
+    }
+LAMA_FFT_SPLIT_CT(256)
+LAMA_FFT_SPLIT_CT(128)
+#undef LAMA_FFT_SPLIT_CT

@@ -49,6 +49,9 @@ const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lam
                                           "lama_finalize", "lama_conv1x1_res", "lama_conv3x3"};
 
 const char *const kSplitName[4] = {"lama_rfft2_rows", "lama_rfft2_cols", "lama_irfft2_cols", "lama_irfft2_rows"};
+const char *const kSplitCtName[2][4] = {
+    {"lama_rfft2_rows_256", "lama_rfft2_cols_256", "lama_irfft2_cols_256", "lama_irfft2_rows_256"},
+    {"lama_rfft2_rows_128", "lama_rfft2_cols_128", "lama_irfft2_cols_128", "lama_irfft2_rows_128"}};
 
 // F_CONV1 / F_CONV1R variants with per-element activation loads, for planes
 // whose length is not a multiple of 4 or that are not 16-byte aligned.
@@ -270,6 +273,11 @@ bool Engine::open(std::string &err)
         if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
     for (int f = 0; f < 4; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_split_[f], module_, kSplitName[f]), kSplitName[f], err)) return false;
+    for (int s = 0; s < 2; ++s)
+        for (int f = 0; f < 4; ++f)
+            if (!check(hip_->hipModuleGetFunction(&fn_split_ct_[s][f], module_, kSplitCtName[s][f]), kSplitCtName[s][f],
+                       err))
+                return false;
     for (int f = 0; f < 2; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err)) return false;
     if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err)) return false;
@@ -441,7 +449,7 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // Single-block mode keeps a whole plane (two ping-pong buffers + both
 // twiddle tables) in one block's LDS; it is used while that fits in 64 KB.
 // Larger planes (or LAMA_FFT_SPLIT=1) use the row/column launches, each
-// block holding at most 64 KB of ping-pong buffers.
+// block holding at most LAMA_FFT_SPLIT_LDS bytes of ping-pong buffers.
 // The kernel of a conv launch: the 1x1 families use float4 activation loads
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
 hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
@@ -474,7 +482,7 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
         return true;
     }
     // complex values the two ping-pong buffers may hold next to the twiddles
-    const size_t cap = max_lds_ / f2, buf = 64 * 1024 / f2;
+    const size_t cap = max_lds_ / f2, buf = LAMA_FFT_SPLIT_LDS / f2;
     const size_t avail_r = cap > (size_t)W ? std::min(buf, cap - W) : 0;
     const size_t avail_c = cap > (size_t)H ? std::min(buf, cap - H) : 0;
     g.split = true;
@@ -489,6 +497,14 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
     g.grid_rows = (unsigned)(C * ((HP + g.rows_per_block - 1) / g.rows_per_block));
     g.grid_cols = (unsigned)(C * ((Wh + g.cols_per_block - 1) / g.cols_per_block));
     g.tmp_bytes = (size_t)C * H * Wh * f2;
+    // square 256 or 128 planes have split kernels with the shape compiled in,
+    // whose blocks hold LAMA_FFT_SPLIT_LDS / (16 N) row pairs or columns
+    // (LAMA_FFT_GENERIC=1 keeps the runtime-shaped ones, for tests)
+    const char *gen = getenv("LAMA_FFT_GENERIC");
+    const int per_block = (int)(buf / (2 * (size_t)H));
+    if (H == W && (H == 256 || H == 128) && !(gen && atoi(gen) == 1) && g.rows_per_block == per_block &&
+        g.cols_per_block == per_block)
+        g.ct_split = H;
     return true;
 }
 
@@ -516,7 +532,7 @@ void Engine::push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int st
     }
     for (int k = 0; k < 2; ++k) {
         const bool rows = inverse ? k == 1 : k == 0;
-        L.fn = fn_split_[inverse ? 2 + k : k];
+        L.fn = g.ct_split ? fn_split_ct_[g.ct_split == 256 ? 0 : 1][inverse ? 2 + k : k] : fn_split_[inverse ? 2 + k : k];
         L.grid = rows ? g.grid_rows : g.grid_cols;
         L.shmem = (unsigned)(rows ? g.lds_rows : g.lds_cols);
         L.bytes = k == 0 ? bytes_a : bytes_b;

@@ -66,6 +66,7 @@ struct FftGeom {
     unsigned grid_rows = 0, grid_cols = 0;
     size_t tmp_bytes = 0;           // interleaved complex [C][H][W/2+1]
     int ct = 0;                     // single-block square plane with compile-time kernels (32 or 64), else 0
+    int ct_split = 0;               // split square plane with compile-time kernels (128 or 256), else 0
 };
 
 struct ArenaLayout {
@@ -145,6 +146,7 @@ private:
     hipFunction_t fn_split_[4] = {};
     hipFunction_t fn_pw_any_[2] = {};  // 1x1 kernels for planes that are not float4-aligned
     hipFunction_t fn_fft_ct_[2][2] = {};  // [64x64, 32x32][rfft2, irfft2]
+    hipFunction_t fn_split_ct_[2][4] = {};  // [256x256, 128x128][as fn_split_]
     // FFC 3x3 convolutions as Winograd F(2,3) along x (lama_conv3x3w), or
     // with LAMA_FFC_WINO=0 as the direct implicit GEMM (lama_conv3x3); chosen
     // at open, since the weights are packed for one or the other

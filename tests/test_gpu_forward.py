@@ -190,12 +190,15 @@ def test_forward_split_forced_matches_single(pkg, engine, monkeypatch):
     assert rel_err(b, a) < 1e-5
 
 
-@pytest.mark.parametrize("size", [256, 512])
+@pytest.mark.parametrize("size", [256, 512, 1024, 2048])
 def test_compiled_shape_fft_equals_generic(pkg, engine, monkeypatch, size):
-    """The 32x32 / 64x64 bottleneck planes (256 and 512 inputs) use FFT kernels
-    with the shape compiled in; they run the same radix plan as the
-    runtime-shaped kernels (LAMA_FFT_GENERIC=1), so the whole forward agrees to
-    float rounding (the compiler contracts a few multiply-adds differently)."""
+    """The 32x32 / 64x64 bottleneck planes (256 and 512 inputs) use single-block
+    FFT kernels with the shape compiled in, the 128x128 / 256x256 planes (1024
+    and 2048 inputs) split row/column kernels with the shape compiled in; they
+    run the same radix plan as the runtime-shaped kernels (LAMA_FFT_GENERIC=1),
+    so the whole forward agrees to float rounding (the compiler contracts a few
+    multiply-adds differently)."""
+    print(f"case {size}x{size} strokes (compiled-shape vs generic FFT)", flush=True)
     img, mask = _case(pkg, size, size, "strokes")
     x = pkg.host_api.build_input(img, mask)
     a = engine.forward(x)

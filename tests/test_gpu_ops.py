@@ -78,15 +78,17 @@ SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), 
          (33, 96), (31, 32)]
 
 
-# planes too large for one block's LDS take the row/column split launches
-LARGE = [(256, 256), (200, 130), (150, 90)]
+# planes too large for one block's LDS take the row/column split launches;
+# the square 256 and 128 planes have split kernels with the shape compiled in
+LARGE = [(256, 256), (128, 128), (200, 130), (150, 90)]
 
 
 @pytest.fixture(params=["single", "split", "generic"])
 def fft_mode(request, monkeypatch):
     """'split' forces the row/column launches (LAMA_FFT_SPLIT=1) at every size;
-    'generic' keeps the runtime-shaped single-block kernels where a kernel with
-    the plane shape compiled in exists (32x32, 64x64; LAMA_FFT_GENERIC=1)."""
+    'generic' keeps the runtime-shaped kernels where a kernel with the plane
+    shape compiled in exists (single-block 32x32 and 64x64, split 128x128 and
+    256x256; LAMA_FFT_GENERIC=1)."""
     monkeypatch.delenv("LAMA_FFT_SPLIT", raising=False)
     monkeypatch.delenv("LAMA_FFT_GENERIC", raising=False)
     if request.param == "split":
@@ -98,8 +100,8 @@ def fft_mode(request, monkeypatch):
 
 @pytest.mark.parametrize("h,w", SIZES + LARGE)
 def test_rfft2(engine, fft_mode, h, w):
-    if fft_mode != "split" and (h, w) in LARGE:
-        pytest.skip("large planes always split")
+    if fft_mode == "single" and (h, w) in LARGE:
+        pytest.skip("large planes always split (the 'split' case)")
     rng = np.random.default_rng(h * 100 + w)
     c = 3
     x = rng.standard_normal((c, h, w), np.float32)
@@ -111,8 +113,8 @@ def test_rfft2(engine, fft_mode, h, w):
 
 @pytest.mark.parametrize("h,w", SIZES + LARGE)
 def test_irfft2(engine, fft_mode, h, w):
-    if fft_mode != "split" and (h, w) in LARGE:
-        pytest.skip("large planes always split")
+    if fft_mode == "single" and (h, w) in LARGE:
+        pytest.skip("large planes always split (the 'split' case)")
     rng = np.random.default_rng(h * 100 + w + 1)
     c = 3
     wh = w // 2 + 1
