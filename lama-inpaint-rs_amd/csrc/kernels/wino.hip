@@ -95,9 +95,10 @@ __device__ __forceinline__ void wino_load(WStage &st, const WSlots &sl, const Co
         st.w[4 * it + 2] = v.z;
         st.w[4 * it + 3] = v.w;
     }
-    // channels past C (zero weights) read the last float of the source
+    // channels past C (zero weights) read the last float of the source; the
+    // zero chunk that pads the count to even reads within channel C - 1
     const unsigned plane = (unsigned)(sg.IH * sg.IW);
-    const int c0 = ck * C::KC;
+    const int c0 = min(ck * C::KC, sg.C - 1);
     const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
     const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
 #pragma unroll
