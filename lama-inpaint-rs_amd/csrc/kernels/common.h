@@ -66,7 +66,7 @@ static inline constexpr int lama_convt_kc(int phase)
 
 #ifdef __HIP_DEVICE_COMPILE__
 // Wave priority of the SpectralTransform chain (conv1, rfft2, FU conv,
-// irfft2, conv2).  It runs on a second stream beside the FFC 3x3 GEMM and is
+// irfft2, conv2).  It runs on its own stream beside the FFC 3x3 GEMMs and is
 // the critical path of every FFC; when its workgroups share a CU with the
 // GEMM's, a higher priority lets their instructions issue first.
 #ifndef LAMA_SIDE_PRIO
