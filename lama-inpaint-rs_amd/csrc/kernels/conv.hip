@@ -321,11 +321,13 @@ __device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg_mem, 
 // 16-byte LDS store, no transpose), and each MFMA's B operand is one 4-byte
 // LDS read per lane: lane half g reads 32 consecutive pixels of channel
 // g*KC/2 + c.  The two halves' rows sit in separate regions whose bases
-// differ by 32 banks.  VEC: planes are 16-byte aligned with N % 4 == 0
-// (float4 loads); otherwise each run is four clamped scalar loads.
-template <int KC_, bool VEC_, int NPX_>
+// differ by 32 banks.  VW = 4: planes are 16-byte aligned with N % 4 == 0
+// (one float4 load per run); VW = 2: 8-byte aligned with N % 2 == 0 and
+// N >= 4 (two float2 loads); VW = 1: four clamped scalar loads.
+template <int KC_, int VW_, int NPX_>
 struct PwCfg {
-    static constexpr bool VEC = VEC_;
+    static constexpr int VW = VW_;  // activation load width: float4, float2 or scalar
+    static constexpr bool VEC = VW_ > 1;
     static constexpr int KC = KC_, NPX = NPX_, NACC = NPX / 64;
     static constexpr int WSTR = KC + 4;              // weight row stride, = 4 (mod 8)
     static constexpr int HALF = KC / 2 * NPX + 32;   // one lane half's channel rows
@@ -366,8 +368,9 @@ __device__ __forceinline__ void pw_make_slots(PwSlots<C> &sl, const ConvSeg &sg,
         const int idx = tid + it * LAMA_NT, ci = idx / (C::NPX / 4), q = idx % (C::NPX / 4);
         sl.xc[it] = ci;
         sl.xl[it] = (ci / (C::KC / 2)) * C::HALF + (ci % (C::KC / 2)) * C::NPX + 4 * q;
-        // runs past the plane read the last whole run (VEC) or clamp per element
-        sl.xp[it] = C::VEC ? min(ox0 + 4 * q, N - 4) : ox0 + 4 * q;
+        // runs past the plane read the last whole run (VW = 4; N % 4 == 0, so
+        // no run straddles the end) or clamp per float2 pair / element
+        sl.xp[it] = C::VW == 4 ? min(ox0 + 4 * q, N - 4) : ox0 + 4 * q;
         sl.xo[it] = 4u * (unsigned)(ci * N + sl.xp[it]);
     }
 }
@@ -391,12 +394,22 @@ __device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &
     const unsigned vlast = 4u * ((unsigned)min(sg.C - c0, C::KC) * (unsigned)N - 4u);
 #pragma unroll
     for (int it = 0; it < C::XITER; ++it) {
-        if constexpr (C::VEC) {
+        if constexpr (C::VW == 4) {
             const float4 v = *at_byte<float4>(src, min(sl.xo[it], vlast));
             st.x[4 * it] = v.x;
             st.x[4 * it + 1] = v.y;
             st.x[4 * it + 2] = v.z;
             st.x[4 * it + 3] = v.w;
+        } else if constexpr (C::VW == 2) {
+            // each pair clamped to the last pair: a run starting at N - 2 keeps
+            // its two valid pixels in place
+            const unsigned plast = vlast + 8u;
+            const float2 a = *at_byte<float2>(src, min(sl.xo[it], plast));
+            const float2 b = *at_byte<float2>(src, min(sl.xo[it] + 8u, plast));
+            st.x[4 * it] = a.x;
+            st.x[4 * it + 1] = a.y;
+            st.x[4 * it + 2] = b.x;
+            st.x[4 * it + 3] = b.y;
         } else {
             const LAMA_GLOBAL float *q = src + (long)min(sl.xc[it], clast) * N;
 #pragma unroll
@@ -746,13 +759,14 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
 // conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
-// N % 4 == 0; lama_conv1x1_s takes any N.
-#define LAMA_PW_KERNEL(NAME, KC, VEC, NPX, PREFETCH, D)                                                      \
+// N % 4 == 0, lama_conv1x1_v2 8-byte aligned planes with N % 2 == 0 and
+// N >= 4; lama_conv1x1_s takes any N.
+#define LAMA_PW_KERNEL(NAME, KC, VW, NPX, PREFETCH, D)                                                      \
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(LAMA_CONV_PARAMS) \
     {                                                                                                       \
         side_priority();                                                                                    \
         LAMA_CONV_STARTS;                                                                                   \
-        using C = PwCfg<KC, VEC, NPX>;                                                                      \
+        using C = PwCfg<KC, VW, NPX>;                                                                      \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \
@@ -762,13 +776,15 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 #ifndef LAMA_PW_DEPTH_RES
 #define LAMA_PW_DEPTH_RES LAMA_PW_DEPTH
 #endif
-LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, true, 64, false, LAMA_PW_DEPTH)
-LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, false, 64, false, LAMA_PW_DEPTH)
+LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, 4, 64, false, LAMA_PW_DEPTH)
+LAMA_PW_KERNEL(lama_conv1x1_v2, LAMA_PW_KC, 2, 64, false, LAMA_PW_DEPTH)
+LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, 1, 64, false, LAMA_PW_DEPTH)
 
 // The SpectralTransform conv2, whose epilogue adds the l2g partial and the
 // residual (fetched before the K loop).
-LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, true, 64, true, LAMA_PW_DEPTH_RES)
-LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, false, 64, true, LAMA_PW_DEPTH_RES)
+LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, 4, 64, true, LAMA_PW_DEPTH_RES)
+LAMA_PW_KERNEL(lama_conv1x1_res_v2, LAMA_PW_KC, 2, 64, true, LAMA_PW_DEPTH_RES)
+LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, 1, 64, true, LAMA_PW_DEPTH_RES)
 #undef LAMA_PW_KERNEL
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions

@@ -56,6 +56,7 @@ const char *const kSplitCtName[2][4] = {
 // F_CONV1 / F_CONV1R variants with per-element activation loads, for planes
 // whose length is not a multiple of 4 or that are not 16-byte aligned.
 const char *const kPwAnyName[2] = {"lama_conv1x1_s", "lama_conv1x1_res_s"};
+const char *const kPwV2Name[2] = {"lama_conv1x1_v2", "lama_conv1x1_res_v2"};
 
 // Single-block FFT kernels with the plane shape fixed at compile time.
 const char *const kFftCtName[2][2] = {{"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}};
@@ -279,7 +280,9 @@ bool Engine::open(std::string &err)
                        err))
                 return false;
     for (int f = 0; f < 2; ++f)
-        if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err)) return false;
+        if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err) ||
+            !check(hip_->hipModuleGetFunction(&fn_pw_v2_[f], module_, kPwV2Name[f]), kPwV2Name[f], err))
+            return false;
     if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err)) return false;
     wino_ = !(getenv("LAMA_FFC_WINO") && atoi(getenv("LAMA_FFC_WINO")) == 0);
     for (int s = 0; s < 2; ++s)
@@ -456,11 +459,15 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
 {
     if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
+    // the widest activation loads every plane of the launch allows
+    int vw = 4;
     for (size_t i = 0; i < n; ++i) {
         const ConvSeg &s = probs[i].s0;
-        if (((size_t)s.IH * s.IW) % 4 != 0 || (uintptr_t)s.src % 16 != 0) return fn_pw_any_[family == F_CONV1R];
+        const size_t N = (size_t)s.IH * s.IW;
+        if (N % 4 != 0 || (uintptr_t)s.src % 16 != 0) vw = std::min(vw, 2);
+        if (N % 2 != 0 || N < 4 || (uintptr_t)s.src % 8 != 0) vw = 1;
     }
-    return fn_[family];
+    return vw == 4 ? fn_[family] : vw == 2 ? fn_pw_v2_[family == F_CONV1R] : fn_pw_any_[family == F_CONV1R];
 }
 
 bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const

@@ -263,13 +263,16 @@ def test_graph_replays_match_eager(pkg, engine, monkeypatch):
     eng1.close()
 
 
-def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal):
+@pytest.mark.parametrize("h,w", [(600, 600), (600, 592)])
+def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal, h, w):
     """configs[4]'s --tile window: 600 x 600 (75 x 75 bottleneck, FFT lengths
     75 and 38 through the reference's opposite-sign rule) against the oracle,
-    every step."""
-    img, mask = _case(pkg, 600, 600, "rect")
+    every step.  600 x 592 gives bottleneck planes of 5550 and spectral planes
+    of 2850 values: even but not multiples of 4, so every 1x1 convolution
+    (conv1, FourierUnit, conv2 with its epilogue) takes the float2 loads."""
+    img, mask = _case(pkg, h, w, "rect")
     x = pkg.host_api.build_input(img, mask)
-    print("case 600x600 rect", flush=True)
+    print(f"case {h}x{w} rect", flush=True)
     got, got_steps = engine.forward_steps(x, list(range(29)))
     ref, ref_steps = oracle_cal.forward(x, steps=True)
     for s in range(29):

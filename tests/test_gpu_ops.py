@@ -39,6 +39,9 @@ def _oracle_bn_relu(y, s, t):
     (96, 130, 7, 12, 1, 1),    # 1x1 float4 loads: partial last tile, M % 64 != 0
     (50, 64, 2, 2, 1, 1),      # 1x1 plane of exactly one float4 run
     (33, 20, 1, 3, 1, 1),      # 1x1 plane shorter than a float4 run
+    (384, 384, 75, 38, 1, 1),  # FourierUnit conv at a 600x600 input (N = 2850: float2 loads)
+    (24, 40, 3, 2, 1, 1),      # 1x1 plane of 6 values: float2 loads, last run clamped
+    (20, 16, 1, 2, 1, 1),      # 1x1 plane of 2 values: shorter than a run, scalar loads
 ])
 def test_conv2d(engine, cin, cout, h, w, k, stride):
     rng = np.random.default_rng(cin * 1000 + cout + k)
