@@ -56,6 +56,38 @@ int lama_hip_forward(lama_hip_ctx *ctx, const float *input, int h, int w, float 
 int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int w,
                             float *d_output, void *stream, char *err, size_t errlen);
 
+/* The whole-image flow around cuda::run, on the device: the pad to a multiple
+ * of 8 (main.rs:241-242), build_input (main.rs:175-196), the forward, and the
+ * 8-bit composite of main.rs:272-307 fused into the output convolution's
+ * epilogue -- hole pixels (mask > 0) take trunc(clamp(v,0,1)*255 + 0.5), all
+ * others the source bytes.  `rgb` is HWC [h][w][3], `mask` [h][w] (the red
+ * channel of the mask PNG, image.rs), `out_rgb` HWC [h][w][3]; any h, w >= 1.
+ * `net_out` (may be NULL) receives the [3][H][W] sigmoid plane of the padded
+ * shape, H = h rounded up to a multiple of 8 (likewise W).  The --tile and
+ * --sections flows (main.rs:422-437, 538-552) paste a window's composite.
+ * Synchronous. */
+int lama_hip_inpaint(lama_hip_ctx *ctx, const uint8_t *rgb, const uint8_t *mask, int h, int w,
+                     uint8_t *out_rgb, float *net_out, char *err, size_t errlen);
+
+/* lama_hip_inpaint on device-resident buffers, enqueued on `stream` (NULL =
+ * the engine's own).  Asynchronous; lama_hip_synchronize waits for it. */
+int lama_hip_inpaint_device(lama_hip_ctx *ctx, const uint8_t *d_rgb, const uint8_t *d_mask, int h, int w,
+                            uint8_t *d_out_rgb, void *stream, char *err, size_t errlen);
+
+/* One FFC's SpectralTransform alone (Spectral::forward, cpu.rs:239-265, and
+ * FourierUnit::forward, cpu.rs:270-308; GPU spectral_forward, cuda.rs:1460-1539):
+ * out [384][h][w] = conv2(f + irfft2(ReLU(BN(FU(rfft2(f)))))), with
+ * f = ReLU(BN1(conv1(x))), x [384][h][w], for FFC `ffc` in 0..35 of the loaded
+ * weights (model.{5+ffc/2}.conv{1+ffc%2}).  `stages` (may be NULL, as may any
+ * entry) receives the LAMA_DUMP_SPECTRAL stages (cpu.rs:242-257): [0] f
+ * [192][h][w]; [1] the stacked spectrum [384][h][w/2+1]; [2] the FU conv after
+ * BN + ReLU [384][h][w/2+1]; [3] f + irfft2 [192][h][w].  Synchronous. */
+int lama_hip_spectral(lama_hip_ctx *ctx, int ffc, const float *x, int h, int w, float *out,
+                      float *const *stages, char *err, size_t errlen);
+/* The same on device buffers, enqueued on `stream` (NULL = the engine's). */
+int lama_hip_spectral_device(lama_hip_ctx *ctx, int ffc, const float *d_x, int h, int w, float *d_out,
+                             void *stream, char *err, size_t errlen);
+
 /* LAMA_DUMP_STEP (cuda.rs:1572-1574, 1647-1662): a forward that also copies
  * the activation after plan step i (local planes then global planes, the
  * layout of cpu.rs:536-546) into steps[i] when steps[i] is non-NULL,
@@ -74,7 +106,8 @@ int lama_hip_vram(uint64_t *free_bytes, uint64_t *total_bytes, char *name, size_
  * Families: 0 conv7x7, 1 conv3x3s2, 2 conv3x3 (FFC l2l + l2g), 3 conv1x1,
  * 4 convt, 5 rfft2, 6 irfft2, 7 tail, 8 finalize (FFC local branch
  * epilogue), 9 conv1x1res (SpectralTransform conv2 with the l2g addend),
- * 10 conv3x3g2l (FFC g2l).  A launch issued after a wait on another stream
+ * 10 conv3x3g2l (FFC g2l), 11 build_input (the inpaint entry points' device
+ * build_input).  A launch issued after a wait on another stream
  * is timed from that wait, so its time includes the wait. */
 int lama_hip_profile(lama_hip_ctx *ctx, uint32_t mask);
 void lama_hip_profile_reset(lama_hip_ctx *ctx);
@@ -83,7 +116,17 @@ void lama_hip_profile_reset(lama_hip_ctx *ctx);
  * Returns 1 for a valid i, 0 past the end. */
 int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, uint64_t *launches,
                           double *ms, double *flops, double *bytes);
-/* print_stats (cuda.rs:1785-1806): a summary to stderr. */
+/* print_op_stats / print_sub_stats / print_stats (cuda.rs:1738-1806): the
+ * per-family event timings to stderr as "op" lines (LAMA_PROFILE_OPS), "sub"
+ * lines (LAMA_PROFILE_SUB) and a "gpu totals" line (LAMA_PROFILE); the "op"
+ * lines when none of the three is set.  LAMA_PROFILE_OPS and LAMA_PROFILE_SUB
+ * turn the per-family timing on for every family when the context opens
+ * (events in the dispatch packets, no synchronisation).  The engine also
+ * honours, in lama_hip_forward: LAMA_DUMP_STEP=<n> (the activation after plan
+ * step n to /tmp/gpu_step_<n>.f32, little-endian f32, local planes then
+ * global), LAMA_PROFILE (per-step lines and upload / step loop / download
+ * times on stderr, cuda.rs:1560-1686) and LAMA_PROFILE_SYNC (each step's line
+ * after draining every stream: submit + device time). */
 void lama_hip_print_stats(lama_hip_ctx *ctx);
 /* Device memory one forward at h x w needs, for the --gpu capacity guard
  * (the role of mem.rs:26-36 estimated_bytes, exact for this engine): the
@@ -100,6 +143,10 @@ int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size
 int lama_hip_free(lama_hip_ctx *ctx, void *ptr);
 int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, size_t bytes, int kind,
                     char *err, size_t errlen); /* kind: 1 HtoD, 2 DtoH, 3 DtoD */
+/* Waits for the engine's own stream and for the last pass (forward,
+ * inpaint or SpectralTransform) that was enqueued on a caller's stream.  A
+ * context keeps one activation arena per shape: passes of one context on
+ * different caller streams must be ordered by the caller. */
 int lama_hip_synchronize(lama_hip_ctx *ctx, char *err, size_t errlen);
 
 /* Single kernel families on host buffers, for parity tests against the

@@ -189,7 +189,9 @@ struct FinalizeArgs {
     float *out;
 };
 
-// The 7x7 output convolution (64 -> 3, reflect pad 3, bias, sigmoid).
+// The 7x7 output convolution (64 -> 3, reflect pad 3, bias, sigmoid).  The
+// composite variant (lama_tail_u8) also reads the unpadded source image and
+// mask, h x w with h <= H, w <= W, and writes the 8-bit composite.
 struct TailArgs {
     const float *src;  // [Cin][H][W]
     const float *wt;   // [3][Cin][7][7]
@@ -197,4 +199,31 @@ struct TailArgs {
     float *out;        // [3][H][W]
     int Cin, H, W;
     int pad_;
+    const uint8_t *rgb;   // lama_tail_u8: source pixels, HWC [h][w][3]
+    const uint8_t *mask;  // lama_tail_u8: [h][w], hole where > 0
+    uint8_t *out_u8;      // lama_tail_u8: composite, HWC [h][w][3]
 };
+
+// Device build_input: the 8-bit image and mask (h x w, HWC RGB) to the
+// network input [4][H][W], H >= h, W >= w, reflect-padded bottom/right.
+struct InputArgs {
+    const uint8_t *rgb;
+    const uint8_t *mask;
+    float *out;
+    int H, W;
+};
+
+// PyTorch 'reflect' index for any i >= 0 (image.rs reflect_index: period
+// 2(n-1), the edge sample not repeated; n == 1 maps everything to 0).
+static inline
+#ifdef __HIP_DEVICE_COMPILE__
+    __device__
+#endif
+    int lama_reflect_full(int i, int n)
+{
+    if (n == 1) return 0;
+    const int period = 2 * (n - 1);
+    int m = i % period;
+    if (m < 0) m += period;
+    return m >= n ? period - m : m;
+}

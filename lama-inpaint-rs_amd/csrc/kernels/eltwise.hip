@@ -58,3 +58,28 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
         for (int e = 0; e < (int)(n - i); ++e) o[i + e] = out[e];
     }
 }
+
+// build_input (main.rs:175-196) on the device: the 8-bit h x w image (HWC
+// RGB) and mask to the network input [4][H][W], padded bottom/right by
+// reflection (image.rs:159-169).  Per pixel: m = (mask > 0), channel c =
+// (rgb_c / 255) * (1 - m) with a correctly rounded f32 division and a
+// separately rounded product, as the reference computes it; plane 3 = m.
+// One thread per output pixel: byte reads, four coalesced plane stores.
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_build_input(const InputArgs *__restrict__ args, int h, int w)
+{
+    const InputArgs &A = *args;
+    const long plane = (long)A.H * A.W;
+    const long i = (long)blockIdx.x * LAMA_NT + threadIdx.x;
+    if (i >= plane) return;
+    const int y = (int)(i / A.W), x = (int)(i - (long)y * A.W);
+    const long s = (long)lama_reflect_full(y, h) * w + lama_reflect_full(x, w);
+    const float m = gp(A.mask)[s] > 0 ? 1.0f : 0.0f;
+    const float keep = __fsub_rn(1.0f, m);
+    LAMA_GLOBAL float *o = gp(A.out);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const float v = __fdiv_rn((float)gp(A.rgb)[3 * s + c], 255.0f);
+        o[c * plane + i] = __fmul_rn(v, keep);
+    }
+    o[3 * plane + i] = m;
+}

@@ -19,7 +19,25 @@ constexpr int PR = TROWS + 6, PC = TCOLS + 6;
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
+// trunc(clamp(v, 0, 1) * 255 + 0.5) with the product and the sum each
+// rounded on its own (main.rs:303-305).  This code object is built with
+// -ffp-contract=fast, under which the backend fuses a multiply and an add into
+// one FMA (one rounding: a different result for some v) whatever the source
+// says; the empty asm statement hides the product from that combine.  NaN
+// clamps to 0, as the reference's saturating cast of NaN gives 0.
+__device__ __forceinline__ uint8_t composite_u8(float v)
+{
+    v = fminf(fmaxf(v, 0.f), 1.f);
+    float p = v * 255.0f;
+    __asm__ volatile("" : "+v"(p));
+    return (uint8_t)(int)(p + 0.5f);
+}
+
+// U8 = false: the sigmoid plane only.  U8 = true: also the 8-bit composite of
+// main.rs:272-307 over the h x w crop -- hole pixels (mask > 0) from the
+// network, every other pixel copied from the source bytes.
+template <bool U8>
+__device__ __forceinline__ void tail_body(const TailArgs *__restrict__ args, int h, int w)
 {
     constexpr int PE = PR * PC, PK = (PE + LAMA_NT - 1) / LAMA_NT;  // patch elements per thread
     __shared__ float patch[2][PE];
@@ -114,14 +132,38 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *
     float bias[3];
 #pragma unroll
     for (int co = 0; co < 3; ++co) bias[co] = gp(A.bias)[co];
+    float sg[3][PX];
 #pragma unroll
     for (int co = 0; co < 3; ++co)
 #pragma unroll
         for (int p = 0; p < PX; ++p) {
             const int ox = ox0 + tc + p;
-            if (ox < W) {
-                const float v = acc[co][p] + bias[co];
-                gp(A.out)[co * plane + (long)oy * W + ox] = 1.0f / (1.0f + expf(-v));
-            }
+            const float v = acc[co][p] + bias[co];
+            sg[co][p] = 1.0f / (1.0f + expf(-v));
+            if (ox < W) gp(A.out)[co * plane + (long)oy * W + ox] = sg[co][p];
         }
+    if constexpr (U8) {
+        if (oy >= h) return;
+#pragma unroll
+        for (int p = 0; p < PX; ++p) {
+            const int ox = ox0 + tc + p;
+            if (ox >= w) continue;
+            const long q = (long)oy * w + ox;
+            const bool hole = gp(A.mask)[q] > 0;
+#pragma unroll
+            for (int co = 0; co < 3; ++co)
+                gp(A.out_u8)[3 * q + co] = hole ? composite_u8(sg[co][p]) : gp(A.rgb)[3 * q + co];
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
+{
+    tail_body<false>(args, 0, 0);
+}
+
+// The tail with the 8-bit composite of the h x w crop fused in.
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail_u8(const TailArgs *__restrict__ args, int h, int w)
+{
+    tail_body<true>(args, h, w);
 }

@@ -140,15 +140,7 @@ extern "C" int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_
 
 extern "C" void lama_hip_print_stats(lama_hip_ctx *ctx)
 {
-    for (int i = 0; ctx; ++i) {
-        std::string n;
-        uint64_t l;
-        double m, f, b;
-        if (!ctx->eng.profile_read(i, n, l, m, f, b)) break;
-        if (!l) continue;
-        fprintf(stderr, "gpu op %-10s %6llu launches %9.3f ms  %8.2f TFLOP/s  %8.1f GB/s\n", n.c_str(),
-                (unsigned long long)l, m, m > 0 ? f / (m * 1e9) : 0.0, m > 0 ? b / (m * 1e6) : 0.0);
-    }
+    if (ctx) ctx->eng.print_stats();
 }
 
 extern "C" int lama_hip_plan_bytes(lama_hip_ctx *ctx, int h, int w, uint64_t *arena_bytes, uint64_t *weight_bytes,
@@ -184,7 +176,35 @@ extern "C" int lama_hip_memcpy(lama_hip_ctx *ctx, void *dst, const void *src, si
 
 extern "C" int lama_hip_synchronize(lama_hip_ctx *ctx, char *err, size_t errlen)
 {
-    GUARD(ctx->eng.check(ctx->eng.hip()->hipStreamSynchronize(ctx->eng.stream()), "hipStreamSynchronize", e_));
+    GUARD(ctx->eng.synchronize(e_));
+}
+
+extern "C" int lama_hip_inpaint(lama_hip_ctx *ctx, const uint8_t *rgb, const uint8_t *mask, int h, int w,
+                                uint8_t *out_rgb, float *net_out, char *err, size_t errlen)
+{
+    if (ctx && (!rgb || !mask || !out_rgb)) return fail(err, errlen, "lama_hip_inpaint: null buffer");
+    GUARD(ctx->eng.inpaint_host(rgb, mask, h, w, out_rgb, net_out, e_));
+}
+
+extern "C" int lama_hip_inpaint_device(lama_hip_ctx *ctx, const uint8_t *d_rgb, const uint8_t *d_mask, int h, int w,
+                                       uint8_t *d_out_rgb, void *stream, char *err, size_t errlen)
+{
+    if (ctx && (!d_rgb || !d_mask || !d_out_rgb)) return fail(err, errlen, "lama_hip_inpaint_device: null buffer");
+    GUARD(ctx->eng.inpaint_device(d_rgb, d_mask, h, w, d_out_rgb, (hipStream_t)stream, e_));
+}
+
+extern "C" int lama_hip_spectral(lama_hip_ctx *ctx, int ffc, const float *x, int h, int w, float *out,
+                                 float *const *stages, char *err, size_t errlen)
+{
+    if (ctx && (!x || !out)) return fail(err, errlen, "lama_hip_spectral: null buffer");
+    GUARD(ctx->eng.spectral_host(ffc, x, h, w, out, stages, e_));
+}
+
+extern "C" int lama_hip_spectral_device(lama_hip_ctx *ctx, int ffc, const float *d_x, int h, int w, float *d_out,
+                                        void *stream, char *err, size_t errlen)
+{
+    if (ctx && (!d_x || !d_out)) return fail(err, errlen, "lama_hip_spectral_device: null buffer");
+    GUARD(ctx->eng.spectral_device(ffc, d_x, h, w, d_out, (hipStream_t)stream, e_));
 }
 
 extern "C" int lama_hip_op_conv2d(lama_hip_ctx *ctx, const float *x, int cin, int h, int w, const float *wt,

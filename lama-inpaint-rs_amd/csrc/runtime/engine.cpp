@@ -18,12 +18,15 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <chrono>
+#include <cstdio>
 #include <functional>
 
 namespace lama {
 
-const char *const kFamilyName[F_COUNT] = {"conv7x7", "conv3x3s2", "conv3x3",  "conv1x1",    "convt",     "rfft2",
-                                          "irfft2",  "tail",      "finalize", "conv1x1res", "conv3x3g2l"};
+const char *const kFamilyName[F_COUNT] = {"conv7x7",  "conv3x3s2",  "conv3x3",    "conv1x1", "convt",
+                                          "rfft2",    "irfft2",     "tail",       "finalize", "conv1x1res",
+                                          "conv3x3g2l", "build_input"};
 
 size_t step_numel(int step, int h, int w)
 {
@@ -44,9 +47,9 @@ size_t step_numel(int step, int h, int w)
 
 namespace {
 
-const char *const kKernelName[F_COUNT] = {"lama_conv7x7", "lama_conv3x3s2", "lama_conv3x3", "lama_conv1x1",
-                                          "lama_convt",   "lama_rfft2",     "lama_irfft2",  "lama_tail",
-                                          "lama_finalize", "lama_conv1x1_res", "lama_conv3x3"};
+const char *const kKernelName[F_COUNT] = {"lama_conv7x7",     "lama_conv3x3s2", "lama_conv3x3",  "lama_conv1x1",
+                                          "lama_convt",       "lama_rfft2",     "lama_irfft2",   "lama_tail",
+                                          "lama_finalize",    "lama_conv1x1_res", "lama_conv3x3", "lama_build_input"};
 
 const char *const kSplitName[4] = {"lama_rfft2_rows", "lama_rfft2_cols", "lama_irfft2_cols", "lama_irfft2_rows"};
 const char *const kSplitCtName[2][4] = {
@@ -220,7 +223,10 @@ Engine::~Engine()
 {
     if (!hip_) return;
     for (auto &kv : plans_) free_plan(kv.second);
+    for (auto &kv : spec_plans_)
+        if (kv.second.arena) hip_->hipFree(kv.second.arena);
     if (warena_) hip_->hipFree(warena_);
+    if (ev_done_) hip_->hipEventDestroy(ev_done_);
     for (auto &p : pending_) {
         hip_->hipEventDestroy(p.a);
         hip_->hipEventDestroy(p.b);
@@ -283,7 +289,10 @@ bool Engine::open(std::string &err)
         if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err) ||
             !check(hip_->hipModuleGetFunction(&fn_pw_v2_[f], module_, kPwV2Name[f]), kPwV2Name[f], err))
             return false;
-    if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err)) return false;
+    if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err) ||
+        !check(hip_->hipModuleGetFunction(&fn_tail_u8_, module_, "lama_tail_u8"), "lama_tail_u8", err))
+        return false;
+    fn_build_in_ = fn_[F_INPUT];
     wino_ = !(getenv("LAMA_FFC_WINO") && atoi(getenv("LAMA_FFC_WINO")) == 0);
     for (int s = 0; s < 2; ++s)
         for (int f = 0; f < 2; ++f)
@@ -306,6 +315,18 @@ bool Engine::open(std::string &err)
 #endif
     for (auto &e : ev_)
         if (!check(hip_->hipEventCreateWithFlags(&e, LAMA_EV_FLAGS), "hipEventCreate", err)) return false;
+    if (!check(hip_->hipEventCreateWithFlags(&ev_done_, hipEventDisableTiming), "hipEventCreate", err)) return false;
+    // the reference engine's debug flags (cuda.rs:127-150, 1574): set = present
+    flag_profile_ = getenv("LAMA_PROFILE") != nullptr;
+    flag_profile_sync_ = getenv("LAMA_PROFILE_SYNC") != nullptr;
+    flag_profile_ops_ = getenv("LAMA_PROFILE_OPS") != nullptr;
+    flag_profile_sub_ = getenv("LAMA_PROFILE_SUB") != nullptr;
+    if (const char *d = getenv("LAMA_DUMP_STEP")) {
+        char *end = nullptr;
+        const long v = strtol(d, &end, 10);
+        dump_step_ = (end != d && *end == 0 && v >= 0 && v < kSteps) ? (int)v : -1;  // parse().ok()
+    }
+    if (flag_profile_ops_ || flag_profile_sub_) prof_mask_ = (1u << F_COUNT) - 1;
     return true;
 }
 
@@ -398,19 +419,29 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
     tail_b_ = A.add(3);
     std::copy(tb.begin(), tb.end(), A.h.begin() + tail_b_);
 
-    // one upload (cuda.rs:330-369 does one HtoD of the raw file)
-    if (warena_) {
-        hip_->hipFree(warena_);
-        warena_ = nullptr;
-    }
-    if (!check(hip_->hipMalloc((void **)&warena_, A.h.size() * 4), "hipMalloc(weights)", err)) return false;
-    warena_bytes_ = A.h.size() * 4;
-    if (!check(hip_->hipMemcpy(warena_, A.h.data(), A.h.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(weights)",
-               err))
+    // one upload (cuda.rs:330-369 does one HtoD of the raw file), into a new
+    // arena: the engine's state changes only once it has succeeded, so a
+    // failed load leaves the previous weights and their plans usable
+    float *fresh = nullptr;
+    if (!check(hip_->hipMalloc((void **)&fresh, A.h.size() * 4), "hipMalloc(weights)", err)) return false;
+    if (!check(hip_->hipMemcpy(fresh, A.h.data(), A.h.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(weights)",
+               err)) {
+        hip_->hipFree(fresh);
         return false;
-    // plans hold pointers into the old arena
+    }
+    // plans hold pointers into the old arena; no pass may still read it
+    if (!check(hip_->hipDeviceSynchronize(), "hipDeviceSynchronize", err)) {
+        hip_->hipFree(fresh);
+        return false;
+    }
     for (auto &kv : plans_) free_plan(kv.second);
     plans_.clear();
+    for (auto &kv : spec_plans_)
+        if (kv.second.arena) hip_->hipFree(kv.second.arena);
+    spec_plans_.clear();
+    if (warena_) hip_->hipFree(warena_);
+    warena_ = fresh;
+    warena_bytes_ = A.h.size() * 4;
     have_weights_ = true;
     return true;
 }
@@ -576,11 +607,29 @@ Plan *Engine::plan_for(int h, int w, std::string &err)
     Plan p;
     p.H = h;
     p.W = w;
-    if (!build_plan(p, err)) {
+    if (!build_plan(p, nullptr, err) || !upload_plan(p, nullptr, err)) {
         free_plan(p);
         return nullptr;
     }
-    return &(plans_[key] = p);
+    return &(plans_[key] = std::move(p));
+}
+
+// Copies what build_plan staged on the host (descriptors, twiddles) into the
+// plan's arena: synchronously when s is null, else enqueued on s.
+bool Engine::upload_plan(const Plan &p, hipStream_t s, std::string &err)
+{
+    char *base = (char *)p.arena;
+    const std::pair<size_t, std::pair<const void *, size_t>> parts[3] = {
+        {p.desc_off, {p.desc_host.data(), p.desc_host.size()}},
+        {p.twr_off, {p.twr_host.data(), p.twr_host.size() * 4}},
+        {p.twc_off, {p.twc_host.data(), p.twc_host.size() * 4}}};
+    for (const auto &q : parts) {
+        const hipError_t e = s ? hip_->hipMemcpyAsync(base + q.first, q.second.first, q.second.second,
+                                                      hipMemcpyHostToDevice, s)
+                               : hip_->hipMemcpy(base + q.first, q.second.first, q.second.second, hipMemcpyHostToDevice);
+        if (!check(e, "hipMemcpy(plan descriptors)", err)) return false;
+    }
+    return true;
 }
 
 // Byte offsets of every buffer of the per-shape activation arena (each
@@ -613,9 +662,13 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.tmp = take(fg.split ? fg.tmp_bytes : 0);
     L.twr = take(ntwr * 4);
     L.twc = take(ntwc * 4);
+    L.rgb8 = take(3 * P);
+    L.mask8 = take(P);
+    L.out8 = take(3 * P);
     const size_t n_conv = 4 + 36 * 9 + 4 * 3;      // problems
-    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 2;  // descriptor uploads, each 256-byte aligned
-    L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + sizeof(TailArgs) + n_puts * 256 + 4096);
+    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 4;  // descriptor uploads, each 256-byte aligned
+    L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + 2 * sizeof(TailArgs) + sizeof(InputArgs) +
+                  n_puts * 256 + 4096);
     return off;
 }
 
@@ -638,7 +691,11 @@ bool Engine::plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::s
     return true;
 }
 
-bool Engine::build_plan(Plan &p, std::string &err)
+// Lays out the activation arena of p's shape and records its launch list.
+// `arena` null: the engine allocates the arena; else the plan uses that
+// memory (at least p.arena_bytes).  The descriptors and twiddles are staged
+// in p.desc_host / twr_host / twc_host for upload_plan.
+bool Engine::build_plan(Plan &p, void *arena, std::string &err)
 {
     const int H = p.H, W = p.W, H2 = H / 2, W2 = W / 2, H4 = H / 4, W4 = W / 4, H8 = H / 8, W8 = W / 8;
     const int Wh = W8 / 2 + 1;
@@ -656,13 +713,22 @@ bool Engine::build_plan(Plan &p, std::string &err)
     const size_t o_in = lay.in, o_a1 = lay.a1, o_a2 = lay.a2, o_a3 = lay.a3, o_x = lay.x, o_y = lay.y, o_f = lay.f,
                  o_g = lay.g, o_s = lay.s, o_s2 = lay.s2, o_out = lay.out, o_gc = lay.gc, o_lq = lay.lq, o_tmp = lay.tmp,
                  o_twr = lay.twr, o_twc = lay.twc, o_desc = lay.desc;
-    if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
+    if (arena) {
+        p.arena = arena;
+        p.own_arena = false;
+    } else {
+        if (!check(hip_->hipMalloc(&p.arena, p.arena_bytes), "hipMalloc(activations)", err)) return false;
+        p.own_arena = true;
+    }
     char *base = (char *)p.arena;
     auto F = [&](size_t o) { return (float *)(base + o); };
     float *in = F(o_in), *a1 = F(o_a1), *a2 = F(o_a2), *a3 = F(o_a3), *X = F(o_x), *Y = F(o_y), *Fb = F(o_f),
           *G = F(o_g), *Sb = F(o_s), *S2 = F(o_s2), *out = F(o_out), *GC = F(o_gc), *LQ = F(o_lq);
     p.in = in;
     p.out = out;
+    p.rgb8 = (uint8_t *)(base + lay.rgb8);
+    p.mask8 = (uint8_t *)(base + lay.mask8);
+    p.out8 = (uint8_t *)(base + lay.out8);
     frow.tw = F(o_twr);
     fcol.tw = F(o_twc);
 
@@ -929,6 +995,34 @@ bool Engine::build_plan(Plan &p, std::string &err)
         L.flops = 2.0 * 64 * 3 * 49 * P;
         L.bytes = f4 * (64 * P + 3 * P);
         p.launches.push_back(L);
+        // the inpaint pass: the same tail with the 8-bit composite of the
+        // caller's h x w crop fused in (h, w are the launch's int parameters)
+        ta.rgb = p.rgb8;
+        ta.mask = p.mask8;
+        ta.out_u8 = p.out8;
+        L.fn = fn_tail_u8_;
+        L.arg = put(&ta, sizeof ta);
+        L.nparams = 3;
+        L.bytes += 7.0 * P;
+        p.tail_u8 = L;
+        // ... and build_input (main.rs:175-196) before the head
+        InputArgs ia{};
+        ia.rgb = p.rgb8;
+        ia.mask = p.mask8;
+        ia.out = in;
+        ia.H = H;
+        ia.W = W;
+        Launch B{};
+        B.fn = fn_build_in_;
+        B.family = F_INPUT;
+        B.stream = S_MAIN;
+        B.wait_ev = B.record_ev = -1;
+        B.grid = (unsigned)((P + LAMA_NT - 1) / LAMA_NT);
+        B.arg = put(&ia, sizeof ia);
+        B.nparams = 3;
+        B.step_end = -1;
+        B.bytes = 4.0 * P + f4 * 4 * P;
+        p.build_in = B;
     }
     if (bad_problem) {
         err = "internal: inconsistent launch descriptor";
@@ -949,12 +1043,13 @@ bool Engine::build_plan(Plan &p, std::string &err)
     p.step_src[26] = {a1, 64 * P};
     p.step_src[28] = {out, 3 * P};
 
-    if (!check(hip_->hipMemcpy(base + o_desc, desc.data(), desc.size(), hipMemcpyHostToDevice), "hipMemcpy(descriptors)", err))
-        return false;
-
-    if (!check(hip_->hipMemcpy((void *)frow.tw, twr.data(), twr.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err))
-        return false;
-    return check(hip_->hipMemcpy((void *)fcol.tw, twc.data(), twc.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err);
+    p.desc_host = std::move(desc);
+    p.desc_off = o_desc;
+    p.twr_host = std::move(twr);
+    p.twr_off = o_twr;
+    p.twc_host = std::move(twc);
+    p.twc_off = o_twc;
+    return true;
 }
 
 bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record)
@@ -1016,12 +1111,84 @@ static void host_reflect_pad(const float *src, int c, int h, int w, int pad, flo
         }
 }
 
-bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
+// Local and global activation shapes after plan step `step` (the reference's
+// LAMA_PROFILE / LAMA_DUMP_STEP lines, cuda.rs:1647-1686); c = 0: absent.
+static void step_shapes(int step, int h, int w, int l[3], int g[3])
+{
+    const int h8 = h / 8, w8 = w / 8;
+    g[0] = g[1] = g[2] = 0;
+    auto set = [](int *v, int c, int y, int x) {
+        v[0] = c;
+        v[1] = y;
+        v[2] = x;
+    };
+    switch (step) {
+    case 0: set(l, 4, h + 6, w + 6); break;
+    case 1: set(l, 64, h, w); break;
+    case 2: set(l, 128, h / 2, w / 2); break;
+    case 3: set(l, 256, h / 4, w / 4); break;
+    case 23: set(l, 512, h8, w8); break;
+    case 24: set(l, 256, h / 4, w / 4); break;
+    case 25: set(l, 128, h / 2, w / 2); break;
+    case 26: set(l, 64, h, w); break;
+    case 27: set(l, 64, h + 6, w + 6); break;
+    case 28: set(l, 3, h, w); break;
+    default:
+        set(l, 128, h8, w8);
+        set(g, 384, h8, w8);
+    }
+}
+
+static std::string global_desc(const int g[3])
+{
+    if (!g[0]) return "None";
+    return "Some((" + std::to_string(g[0]) + ", " + std::to_string(g[1]) + ", " + std::to_string(g[2]) + "))";
+}
+
+bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err, int u8_h, int u8_w)
 {
     // LAMA_STREAMS=1 puts the side-stream work on the main stream (profiling)
     static const bool single = getenv("LAMA_STREAMS") && atoi(getenv("LAMA_STREAMS")) == 1;
     hipStream_t st[S_COUNT] = {s, single ? s : side_, single ? s : g2l_};
-    for (const Launch &L : p.launches) {
+    // LAMA_PROFILE: one line per plan step (cuda.rs:1663-1686), the host time
+    // since the previous step -- submission only, unless LAMA_PROFILE_SYNC
+    // drains every stream at each step's end, which makes it submit + device
+    const bool per_step = flag_profile_ && !capturing_;
+    auto t_step = std::chrono::steady_clock::now();
+    int next_step = 0;
+    auto step_done = [&](int stp) -> bool {
+        if (!per_step) return true;
+        for (; next_step <= stp; ++next_step) {
+            if (flag_profile_sync_)
+                for (hipStream_t q : st)
+                    if (!check(hip_->hipStreamSynchronize(q), "hipStreamSynchronize", err)) return false;
+            const auto now = std::chrono::steady_clock::now();
+            const double dt = next_step == stp ? std::chrono::duration<double>(now - t_step).count() : 0.0;
+            if (next_step == stp) t_step = now;
+            int l[3], g[3];
+            step_shapes(next_step, p.H, p.W, l, g);
+            fprintf(stderr, "gpu step %2d: %6.3fs local %dx%dx%d global %s\n", next_step, dt, l[0], l[1], l[2],
+                    global_desc(g).c_str());
+        }
+        return true;
+    };
+    if (u8_h > 0) {
+        Launch B = p.build_in;
+        B.ps.s[0] = u8_h;
+        B.ps.s[1] = u8_w;
+        if (!launch(B, st[S_MAIN], err)) return false;
+    }
+    if (!step_done(0)) return false;
+    for (const Launch &L0 : p.launches) {
+        const Launch *Lp = &L0;
+        Launch T;
+        if (u8_h > 0 && L0.family == F_TAIL) {
+            T = p.tail_u8;
+            T.ps.s[0] = u8_h;
+            T.ps.s[1] = u8_w;
+            Lp = &T;
+        }
+        const Launch &L = *Lp;
         hipStream_t ls = st[L.stream];
         if (L.wait_ev >= 0 && !check(hip_->hipStreamWaitEvent(ls, ev_[L.wait_ev], 0), "hipStreamWaitEvent", err))
             return false;
@@ -1033,6 +1200,7 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err)
         if (L.record_ev >= 0 && explicit_rec &&
             !check(hip_->hipEventRecord(ev_[L.record_ev], ls), "hipEventRecord", err))
             return false;
+        if (L.step_end >= 0 && !step_done(L.step_end == 22 ? 23 : L.step_end == 26 ? 27 : L.step_end)) return false;
         if (!steps || L.step_end < 0) continue;
         int done[2] = {L.step_end, L.step_end == 22 ? 23 : -1};
         for (int stp : done) {
@@ -1062,7 +1230,7 @@ void Engine::free_plan(Plan &p)
 {
     if (p.graph) hip_->hipGraphExecDestroy(p.graph);
     p.graph = nullptr;
-    if (p.arena) hip_->hipFree(p.arena);
+    if (p.arena && p.own_arena) hip_->hipFree(p.arena);
     p.arena = nullptr;
 }
 
@@ -1108,18 +1276,63 @@ bool Engine::use_graph() const
     return on && prof_mask_ == 0;
 }
 
+// cuda.rs:1647-1662: /tmp/gpu_step_<n>.f32 (little-endian f32, as
+// to_le_bytes) and the "gpu dumped step" line; a failed write is ignored, as
+// there.
+static void write_step_dump(int n, const std::vector<float> &d, int h, int w)
+{
+    const std::string path = "/tmp/gpu_step_" + std::to_string(n) + ".f32";
+    if (FILE *f = fopen(path.c_str(), "wb")) {
+        fwrite(d.data(), 4, d.size(), f);
+        fclose(f);
+    }
+    int l[3], g[3];
+    step_shapes(n, h, w, l, g);
+    fprintf(stderr, "gpu dumped step %d: local %dx%dx%d global %s\n", n, l[0], l[1], l[2], global_desc(g).c_str());
+}
+
 bool Engine::forward_host(const float *in, int h, int w, float *out, float *const *steps, std::string &err)
 {
+    using clk = std::chrono::steady_clock;
+    auto secs = [](clk::time_point a) { return std::chrono::duration<double>(clk::now() - a).count(); };
+    const auto t_run = clk::now();
     Plan *p = plan_for(h, w, err);
     if (!p) return false;
+    // LAMA_DUMP_STEP=<n> (cuda.rs:1572-1574, 1647-1662): the activation after
+    // plan step n, local planes then global, to /tmp/gpu_step_<n>.f32
+    std::vector<float> dump;
+    float *dsteps[kSteps] = {};
+    if (dump_step_ >= 0 && !steps) {
+        dump.resize(step_numel(dump_step_, h, w));
+        dsteps[dump_step_] = dump.data();
+        steps = dsteps;
+    }
     if (steps && steps[0]) host_reflect_pad(in, 4, h, w, 3, steps[0]);
+    auto t = clk::now();
     if (!check(hip_->hipMemcpyAsync(p->in, in, 4ul * h * w * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(input)", err))
         return false;
-    if (!(steps || !use_graph() ? run(*p, stream_, steps, err) : replay(*p, stream_, err))) return false;
-    if (!check(hip_->hipMemcpyAsync(out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(output)", err))
+    if (flag_profile_) {
+        if (!check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err)) return false;
+        fprintf(stderr, "gpu input upload: %.3fs\n", secs(t));
+    }
+    t = clk::now();
+    if (!(steps || flag_profile_ || !use_graph() ? run(*p, stream_, steps, err) : replay(*p, stream_, err))) return false;
+    if (flag_profile_) {
+        if (!check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err)) return false;
+        fprintf(stderr, "gpu step loop: %.3fs\n", secs(t));
+    }
+    t = clk::now();
+    if (!check(hip_->hipMemcpyAsync(out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(output)", err) ||
+        !check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err))
         return false;
-    return check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err);
+    if (flag_profile_) {
+        fprintf(stderr, "gpu output download: %.3fs (%zu floats)\n", secs(t), (size_t)3 * h * w);
+        fprintf(stderr, "gpu run total: %.3fs\n", secs(t_run));
+    }
+    if (!dump.empty()) write_step_dump(dump_step_, dump, h, w);
+    return true;
 }
+
 
 bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err)
 {
@@ -1129,7 +1342,280 @@ bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipSt
     if (!check(hip_->hipMemcpyAsync(p->in, d_in, 4ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(input)", err))
         return false;
     if (!(use_graph() ? replay(*p, s, err) : run(*p, s, nullptr, err))) return false;
-    return check(hip_->hipMemcpyAsync(d_out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err);
+    if (!check(hip_->hipMemcpyAsync(d_out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err))
+        return false;
+    return mark_done(s, err);
+}
+
+// A pass enqueued on a caller's stream: synchronize() must also wait for it.
+bool Engine::mark_done(hipStream_t s, std::string &err)
+{
+    if (s == stream_) return true;
+    if (!check(hip_->hipEventRecord(ev_done_, s), "hipEventRecord", err)) return false;
+    done_pending_ = true;
+    return true;
+}
+
+bool Engine::synchronize(std::string &err)
+{
+    if (done_pending_) {
+        if (!check(hip_->hipEventSynchronize(ev_done_), "hipEventSynchronize", err)) return false;
+        done_pending_ = false;
+    }
+    return check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err);
+}
+
+// The image sizes the inpaint entry points take, and their padded shape
+// (main.rs:241-242: up to the next multiple of 8).
+static bool inpaint_shape(int h, int w, int &H, int &W, std::string &err)
+{
+    if (h < 1 || w < 1) {
+        err = "image " + std::to_string(w) + "x" + std::to_string(h) + " is empty";
+        return false;
+    }
+    H = h + (8 - h % 8) % 8;
+    W = w + (8 - w % 8) % 8;
+    return true;
+}
+
+bool Engine::inpaint_host(const uint8_t *rgb, const uint8_t *mask, int h, int w, uint8_t *out, float *net_out,
+                          std::string &err)
+{
+    int H, W;
+    if (!inpaint_shape(h, w, H, W, err)) return false;
+    Plan *p = plan_for(H, W, err);
+    if (!p) return false;
+    const size_t px = (size_t)h * w;
+    if (!check(hip_->hipMemcpyAsync(p->rgb8, rgb, 3 * px, hipMemcpyHostToDevice, stream_), "hipMemcpy(image)", err) ||
+        !check(hip_->hipMemcpyAsync(p->mask8, mask, px, hipMemcpyHostToDevice, stream_), "hipMemcpy(mask)", err))
+        return false;
+    // LAMA_DUMP_STEP, as in forward_host; step 0 (the padded input) is the
+    // device-built input, reflect-padded on the host
+    std::vector<float> dump;
+    float *dsteps[kSteps] = {};
+    if (dump_step_ > 0) {
+        dump.resize(step_numel(dump_step_, H, W));
+        dsteps[dump_step_] = dump.data();
+    }
+    if (!run(*p, stream_, dump_step_ > 0 ? dsteps : nullptr, err, h, w)) return false;
+    if (dump_step_ == 0) {
+        std::vector<float> x((size_t)4 * H * W);
+        dump.resize(step_numel(0, H, W));
+        if (!check(hip_->hipMemcpyAsync(x.data(), p->in, x.size() * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(dump)",
+                   err) ||
+            !check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err))
+            return false;
+        host_reflect_pad(x.data(), 4, H, W, 3, dump.data());
+    }
+    if (!check(hip_->hipMemcpyAsync(out, p->out8, 3 * px, hipMemcpyDeviceToHost, stream_), "hipMemcpy(output)", err))
+        return false;
+    if (net_out && !check(hip_->hipMemcpyAsync(net_out, p->out, 3ul * H * W * 4, hipMemcpyDeviceToHost, stream_),
+                          "hipMemcpy(output)", err))
+        return false;
+    if (!check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err)) return false;
+    if (!dump.empty()) write_step_dump(dump_step_, dump, H, W);
+    return true;
+}
+
+bool Engine::inpaint_device(const uint8_t *d_rgb, const uint8_t *d_mask, int h, int w, uint8_t *d_out, hipStream_t s,
+                            std::string &err)
+{
+    int H, W;
+    if (!inpaint_shape(h, w, H, W, err)) return false;
+    Plan *p = plan_for(H, W, err);
+    if (!p) return false;
+    if (!s) s = stream_;
+    const size_t px = (size_t)h * w;
+    if (!check(hip_->hipMemcpyAsync(p->rgb8, d_rgb, 3 * px, hipMemcpyDeviceToDevice, s), "hipMemcpy(image)", err) ||
+        !check(hip_->hipMemcpyAsync(p->mask8, d_mask, px, hipMemcpyDeviceToDevice, s), "hipMemcpy(mask)", err))
+        return false;
+    if (!run(*p, s, nullptr, err, h, w)) return false;
+    if (!check(hip_->hipMemcpyAsync(d_out, p->out8, 3 * px, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err))
+        return false;
+    return mark_done(s, err);
+}
+
+// The per-shape plan of the SpectralTransform entry point: the five
+// launches (seven with split FFTs) of each FFC's SpectralTransform on one
+// stream, over one set of buffers.
+SpecPlan *Engine::spec_plan_for(int h, int w, std::string &err)
+{
+    if (!have_weights_) {
+        err = "no weights loaded";
+        return nullptr;
+    }
+    if (h < 1 || w < 1 || (size_t)h * w > ((size_t)1 << 24)) {
+        err = "SpectralTransform plane " + std::to_string(w) + "x" + std::to_string(h) + " is empty or above 2^24 pixels";
+        return nullptr;
+    }
+    auto key = std::make_pair(h, w);
+    auto it = spec_plans_.find(key);
+    if (it != spec_plans_.end()) return &it->second;
+    const int Wh = w / 2 + 1;
+    const size_t P = (size_t)h * w, PS = (size_t)h * Wh;
+    FftLen frow, fcol;
+    std::vector<float> twr, twc;
+    FftGeom fg;
+    if (!fft_len(w, frow, twr, err) || !fft_len(h, fcol, twc, err) || !fft_geom(192, h, w, fg, err)) return nullptr;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off = (off + bytes + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_x = take(384 * P * 4), o_f = take(192 * P * 4), o_s = take(384 * PS * 4), o_s2 = take(384 * PS * 4),
+                 o_g = take(192 * P * 4), o_out = take(384 * P * 4), o_tmp = take(fg.split ? fg.tmp_bytes : 0),
+                 o_twr = take(twr.size() * 4), o_twc = take(twc.size() * 4);
+    const size_t o_desc = take(36 * 3 * 256 + 2 * 256 + 36 * 3 * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + 4096);
+    SpecPlan sp;
+    sp.H = h;
+    sp.W = w;
+    sp.arena_bytes = off;
+    if (!check(hip_->hipMalloc(&sp.arena, off), "hipMalloc(SpectralTransform)", err)) return nullptr;
+    char *base = (char *)sp.arena;
+    auto F = [&](size_t o) { return (float *)(base + o); };
+    sp.x = F(o_x);
+    sp.f = F(o_f);
+    sp.s = F(o_s);
+    sp.s2 = F(o_s2);
+    sp.g = F(o_g);
+    sp.out = F(o_out);
+    std::vector<char> desc;
+    auto put = [&](const void *src, size_t bytes) {
+        size_t o = (desc.size() + 255) / 256 * 256;
+        desc.resize(o + bytes);
+        std::memcpy(desc.data() + o, src, bytes);
+        return (void *)(base + o_desc + o);
+    };
+    FftArgs fa{};
+    fa.row = frow;
+    fa.col = fcol;
+    fa.row.tw = F(o_twr);
+    fa.col.tw = F(o_twc);
+    fa.C = 192;
+    fa.H = h;
+    fa.W = w;
+    fa.Wh = Wh;
+    fa.scale = (float)(1.0 / std::sqrt((double)h * w));
+    fa.rows_per_block = fg.rows_per_block;
+    fa.cols_per_block = fg.cols_per_block;
+    fa.tmp = fg.split ? F(o_tmp) : nullptr;
+    fa.in = sp.f;
+    fa.out = sp.s;
+    void *d_rfft = put(&fa, sizeof fa);
+    fa.in = sp.s2;
+    fa.out = sp.g;
+    fa.feat = sp.f;
+    void *d_irfft = put(&fa, sizeof fa);
+    // a pointwise problem over a flat plane of N pixels: out[M][N] = W src[C][N]
+    auto pw = [&](const float *src, const Packed &pk, int C, int M, int N, size_t bn, float *o, bool bn_relu) {
+        ConvProblem q{};
+        q.s0.src = src;
+        q.s0.wt = wp(pk.off);
+        q.s0.C = C;
+        q.s0.IH = 1;
+        q.s0.IW = N;
+        q.s0.nchunk = pk.nchunk;
+        q.s0.wrow = pk.wrow;
+        q.M = M;
+        q.OH = 1;
+        q.OW = N;
+        q.tiles_x = (N + 63) / 64;
+        q.tiles_y = 1;
+        q.mblocks = (M + 63) / 64;
+        q.nblocks = q.tiles_x * q.mblocks;
+        q.scale = bn_relu ? wp(bn) : nullptr;
+        q.shift = bn_relu ? wp(bn + M) : nullptr;
+        q.relu = bn_relu ? 1 : 0;
+        q.out = o;
+        q.out_cstride = (long)N;
+        q.outW = N;
+        q.oy_mul = q.ox_mul = 1;
+        return q;
+    };
+    auto conv = [&](std::vector<Launch> &out, const ConvProblem &q, double flops, double bytes) {
+        Launch L{};
+        L.fn = conv_fn(F_CONV1, &q, 1);
+        L.family = F_CONV1;
+        L.stream = S_MAIN;
+        L.wait_ev = L.record_ev = L.step_end = -1;
+        L.grid = (unsigned)q.nblocks;
+        L.arg = put(&q, sizeof q);
+        L.ps = prob_starts(&q, 1);
+        L.nparams = 2;
+        L.flops = flops;
+        L.bytes = bytes;
+        out.push_back(L);
+    };
+    for (int k = 0; k < 36; ++k) {
+        const FfcW &Fw = ffc_[k];
+        std::vector<Launch> &v = sp.launches[k];
+        conv(v, pw(sp.x, Fw.conv1, 384, 192, (int)P, Fw.bn1, sp.f, true), 2.0 * 384 * 192 * P,
+             4.0 * (384 * P + 192 * P + 192 * 384));
+        Plan tmp;
+        push_fft(tmp, false, fg, d_rfft, S_MAIN, 4.0 * 192 * P, 8.0 * 192 * PS);
+        conv(tmp.launches, pw(sp.s, Fw.fu, 384, 384, (int)PS, Fw.fu_bn, sp.s2, true), 2.0 * 384 * 384 * PS,
+             4.0 * (2 * 384 * PS + 384 * 384));
+        push_fft(tmp, true, fg, d_irfft, S_MAIN, 8.0 * 192 * PS, 8.0 * 192 * P);
+        conv(tmp.launches, pw(sp.g, Fw.conv2, 192, 384, (int)P, 0, sp.out, false), 2.0 * 192 * 384 * P,
+             4.0 * (192 * P + 384 * P + 384 * 192));
+        v.insert(v.end(), tmp.launches.begin(), tmp.launches.end());
+    }
+    if (desc.size() > off - o_desc) {
+        hip_->hipFree(sp.arena);
+        err = "internal: descriptor region overflow";
+        return nullptr;
+    }
+    if (!check(hip_->hipMemcpy(base + o_desc, desc.data(), desc.size(), hipMemcpyHostToDevice), "hipMemcpy(descriptors)", err) ||
+        !check(hip_->hipMemcpy(base + o_twr, twr.data(), twr.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err) ||
+        !check(hip_->hipMemcpy(base + o_twc, twc.data(), twc.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(twiddles)", err)) {
+        hip_->hipFree(sp.arena);
+        return nullptr;
+    }
+    return &(spec_plans_[key] = std::move(sp));
+}
+
+bool Engine::spectral_device(int k, const float *d_x, int h, int w, float *d_out, hipStream_t s, std::string &err)
+{
+    if (k < 0 || k >= 36) {
+        err = "SpectralTransform index " + std::to_string(k) + " is outside 0..35";
+        return false;
+    }
+    SpecPlan *sp = spec_plan_for(h, w, err);
+    if (!sp) return false;
+    if (!s) s = stream_;
+    const size_t P = (size_t)h * w;
+    if (!check(hip_->hipMemcpyAsync(sp->x, d_x, 384 * P * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(input)", err))
+        return false;
+    for (const Launch &L : sp->launches[k])
+        if (!launch(L, s, err)) return false;
+    if (!check(hip_->hipMemcpyAsync(d_out, sp->out, 384 * P * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err))
+        return false;
+    return mark_done(s, err);
+}
+
+bool Engine::spectral_host(int k, const float *x, int h, int w, float *out, float *const *stages, std::string &err)
+{
+    if (k < 0 || k >= 36) {
+        err = "SpectralTransform index " + std::to_string(k) + " is outside 0..35";
+        return false;
+    }
+    SpecPlan *sp = spec_plan_for(h, w, err);
+    if (!sp) return false;
+    const size_t P = (size_t)h * w, PS = (size_t)h * (w / 2 + 1);
+    if (!check(hip_->hipMemcpyAsync(sp->x, x, 384 * P * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(input)", err))
+        return false;
+    for (const Launch &L : sp->launches[k])
+        if (!launch(L, stream_, err)) return false;
+    if (!check(hip_->hipMemcpyAsync(out, sp->out, 384 * P * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(output)", err))
+        return false;
+    const std::pair<const float *, size_t> src[4] = {{sp->f, 192 * P}, {sp->s, 384 * PS}, {sp->s2, 384 * PS}, {sp->g, 192 * P}};
+    for (int i = 0; stages && i < 4; ++i)
+        if (stages[i] && !check(hip_->hipMemcpyAsync(stages[i], src[i].first, src[i].second * 4, hipMemcpyDeviceToHost,
+                                                     stream_),
+                                "hipMemcpy(stage)", err))
+            return false;
+    return check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err);
 }
 
 int Engine::launch_count(int h, int w)
@@ -1173,6 +1659,38 @@ bool Engine::profile_read(int i, std::string &name, uint64_t &launches, double &
     flops = prof_flops_[i];
     bytes = prof_bytes_[i];
     return true;
+}
+
+void Engine::print_stats()
+{
+    collect_events();
+    const bool any = flag_profile_ops_ || flag_profile_sub_ || flag_profile_;
+    if (flag_profile_ops_ || !any) {
+        double total = 0;
+        for (int f = 0; f < F_COUNT; ++f) {
+            if (!prof_launches_[f]) continue;
+            total += prof_ms_[f] / 1e3;
+            fprintf(stderr, "op %-14s %5llu calls %7.3fs  (%lld us avg, 1 launches/call)\n", kFamilyName[f],
+                    (unsigned long long)prof_launches_[f], prof_ms_[f] / 1e3,
+                    (long long)(prof_ms_[f] * 1e3 / (double)prof_launches_[f]));
+        }
+        fprintf(stderr, "op total %.3fs\n", total);
+    }
+    if (flag_profile_sub_)
+        for (int f = 0; f < F_COUNT; ++f) {
+            if (!prof_launches_[f]) continue;
+            const double t = prof_ms_[f] / 1e3;
+            fprintf(stderr, "sub %-9s %4llu calls %7.3fs  (%lld us avg)  %.1f MFLOP  %.0f GFLOP/s  %.0f MB moved\n",
+                    kFamilyName[f], (unsigned long long)prof_launches_[f], t,
+                    (long long)(t * 1e6 / (double)prof_launches_[f]), prof_flops_[f] / 1e6,
+                    prof_flops_[f] / 1e9 / std::max(t, 1e-9), prof_bytes_[f] / 1e6);
+        }
+    if (flag_profile_) {
+        size_t arena = 0;
+        for (auto &kv : plans_) arena += kv.second.arena_bytes;
+        fprintf(stderr, "gpu totals: %zu planned shape(s), %zu MB of activation arenas, %zu MB of resident weights\n",
+                plans_.size(), arena >> 20, warena_bytes_ >> 20);
+    }
 }
 
 // ---------------------------------------------------------------- single ops

@@ -14,7 +14,8 @@ namespace lama {
 
 // F_CONV3G: the FFC's g2l launches, the same kernel as F_CONV3 (l2l + l2g);
 // a family of its own so that profiling keeps the two launches apart.
-enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_CONV1R, F_CONV3G, F_COUNT };
+// F_INPUT: the device build_input of the inpaint entry points.
+enum Family { F_CONV7, F_CONV3S2, F_CONV3, F_CONV1, F_CONVT, F_RFFT, F_IRFFT, F_TAIL, F_FINAL, F_CONV1R, F_CONV3G, F_INPUT, F_COUNT };
 extern const char *const kFamilyName[F_COUNT];
 
 // Number of plan steps of the reference (model.rs:135-207) and the size in
@@ -70,18 +71,38 @@ struct FftGeom {
 };
 
 struct ArenaLayout {
-    size_t in, a1, a2, a3, x, y, f, g, s, s2, out, gc, lq, tmp, twr, twc, desc;
+    size_t in, a1, a2, a3, x, y, f, g, s, s2, out, gc, lq, tmp, twr, twc, rgb8, mask8, out8, desc;
 };
 
 struct Plan {
     int H = 0, W = 0;
     void *arena = nullptr;
     size_t arena_bytes = 0;
+    bool own_arena = true;  // false: the arena is memory the engine did not allocate
     float *in = nullptr, *out = nullptr;
+    // 8-bit staging of the inpaint entry points (image, mask, composite), each
+    // sized for H x W; a call uses its h x w prefix
+    uint8_t *rgb8 = nullptr, *mask8 = nullptr, *out8 = nullptr;
     std::vector<std::pair<const float *, size_t>> step_src;  // per step (nullptr: host-derived)
     std::vector<Launch> launches;
+    Launch build_in{}, tail_u8{};  // device build_input, and the tail with the composite fused
+    // what build_plan uploads into the arena (kept for a re-upload)
+    std::vector<char> desc_host;
+    std::vector<float> twr_host, twc_host;
+    size_t desc_off = 0, twr_off = 0, twc_off = 0;
     hipGraphExec_t graph = nullptr;  // the launch list captured once, replayed per forward
     bool graph_failed = false;
+};
+
+// The isolated SpectralTransform of each FFC (conv1 -> rfft2 -> FU conv ->
+// irfft2 -> conv2) over [384][h][w] planes, for the SpectralTransform entry
+// point: one arena per plane shape, the launches of all 36 FFCs.
+struct SpecPlan {
+    int H = 0, W = 0;
+    void *arena = nullptr;
+    size_t arena_bytes = 0;
+    float *x = nullptr, *f = nullptr, *s = nullptr, *s2 = nullptr, *g = nullptr, *out = nullptr;
+    std::vector<Launch> launches[36];
 };
 
 class Engine {
@@ -91,11 +112,33 @@ public:
     bool load_weights(const uint8_t *blob, size_t len, const lama_tensor_info *t, size_t n, std::string &err);
     bool forward_host(const float *in, int h, int w, float *out, float *const *steps, std::string &err);
     bool forward_device(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err);
+    // The whole-image flow of main.rs:241-307 on the device: pad to a multiple
+    // of 8, build_input, forward, 8-bit composite.  rgb HWC [h][w][3], mask
+    // [h][w], out HWC [h][w][3]; net_out (host, optional) receives the
+    // [3][H][W] sigmoid plane of the padded shape.
+    bool inpaint_host(const uint8_t *rgb, const uint8_t *mask, int h, int w, uint8_t *out, float *net_out,
+                      std::string &err);
+    bool inpaint_device(const uint8_t *d_rgb, const uint8_t *d_mask, int h, int w, uint8_t *d_out, hipStream_t s,
+                        std::string &err);
+    // The SpectralTransform of FFC k (0..35) alone over x [384][h][w]:
+    // out [384][h][w] = conv2(f + irfft2(FU(rfft2(f)))), f = ReLU(BN1(conv1 x)).
+    // stages (host, optional, entries may be NULL): [0] f [192][h][w],
+    // [1] spectrum [384][h][w/2+1], [2] FU conv after BN + ReLU [384][h][w/2+1],
+    // [3] f + irfft2 [192][h][w].
+    bool spectral_host(int k, const float *x, int h, int w, float *out, float *const *stages, std::string &err);
+    bool spectral_device(int k, const float *d_x, int h, int w, float *d_out, hipStream_t s, std::string &err);
+    // Waits for the engine stream and for the last pass enqueued on a caller's stream.
+    bool synchronize(std::string &err);
 
     // profiling (families whose bit is set get per-launch events)
     void set_profile(uint32_t mask) { prof_mask_ = mask; }
     void profile_reset();
     bool profile_read(int i, std::string &name, uint64_t &launches, double &ms, double &flops, double &bytes);
+    // The summaries of cuda.rs:1738-1806 to stderr, from the per-family
+    // event timings: "op" lines (LAMA_PROFILE_OPS), "sub" lines
+    // (LAMA_PROFILE_SUB), the "gpu totals" line (LAMA_PROFILE); with none of
+    // the flags set, the "op" lines.
+    void print_stats();
     int launch_count(int h, int w);
     // Device bytes of one forward at h x w: the activation arena of that shape
     // (exact, from its layout) and the resident weights (0 before loading).
@@ -126,8 +169,14 @@ private:
     };
 
     Plan *plan_for(int h, int w, std::string &err);
-    bool build_plan(Plan &p, std::string &err);
-    bool run(Plan &p, hipStream_t s, float *const *steps, std::string &err);
+    bool build_plan(Plan &p, void *arena, std::string &err);
+    bool upload_plan(const Plan &p, hipStream_t s, std::string &err);
+    bool mark_done(hipStream_t s, std::string &err);
+    // u8_h > 0: the inpaint pass of an u8_h x u8_w image (build_input first,
+    // the tail with the composite fused in)
+    bool run(Plan &p, hipStream_t s, float *const *steps, std::string &err, int u8_h = 0, int u8_w = 0);
+    SpecPlan *spec_plan_for(int h, int w, std::string &err);
+    bool step_hooks(Plan &p, const float *in, std::string &err);
     bool replay(Plan &p, hipStream_t s, std::string &err);
     static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, ArenaLayout &L);
     bool use_graph() const;
@@ -157,6 +206,11 @@ private:
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr, g2l_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};
+    hipEvent_t ev_done_ = nullptr;  // the end of the last pass enqueued on a caller's stream
+    bool done_pending_ = false;
+    // the reference's debug flags (cuda.rs:127-150), read at open
+    bool flag_profile_ = false, flag_profile_sync_ = false, flag_profile_ops_ = false, flag_profile_sub_ = false;
+    int dump_step_ = -1;  // LAMA_DUMP_STEP
     bool capturing_ = false;  // run() is recording a graph
 
     // weights
@@ -171,6 +225,8 @@ private:
     const float *wp(size_t off) const { return warena_ + off; }
 
     std::map<std::pair<int, int>, Plan> plans_;
+    std::map<std::pair<int, int>, SpecPlan> spec_plans_;
+    hipFunction_t fn_build_in_ = nullptr, fn_tail_u8_ = nullptr;
 
     // profiling
     uint32_t prof_mask_ = 0;

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 HIP_SO = os.path.join(HERE, "lib", "liblama_hip.so")
 
 FAMILIES = ["conv7x7", "conv3x3s2", "conv3x3", "conv1x1", "convt", "rfft2", "irfft2", "tail", "finalize",
-            "conv1x1res", "conv3x3g2l"]
+            "conv1x1res", "conv3x3g2l", "build_input"]
 N_STEPS = 29
 
 _lib = None
@@ -58,6 +58,12 @@ def lib():
         L.lama_hip_op_rfft2.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, cp, sz]
         L.lama_hip_op_irfft2.argtypes = [vp, fp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, cp, sz]
         L.lama_hip_op_tail.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, fp, fp, cp, sz]
+        u8p = ctypes.POINTER(ctypes.c_uint8)
+        L.lama_hip_inpaint.argtypes = [vp, u8p, u8p, ctypes.c_int, ctypes.c_int, u8p, fp, cp, sz]
+        L.lama_hip_inpaint_device.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, cp, sz]
+        L.lama_hip_spectral.argtypes = [vp, ctypes.c_int, fp, ctypes.c_int, ctypes.c_int, fp, ctypes.POINTER(fp),
+                                        cp, sz]
+        L.lama_hip_spectral_device.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, vp, vp, cp, sz]
         _lib = L
     return _lib
 
@@ -129,6 +135,43 @@ class Engine:
 
     def forward_device(self, d_in, h, w, d_out, stream=None):
         self._check(lib().lama_hip_forward_device(self.ctx, d_in, h, w, d_out, stream, self._err, 4096))
+
+    def inpaint(self, rgb, mask, net_out=False):
+        """The whole-image flow on the device (lama_hip_inpaint): u8 HWC image
+        and [h][w] mask -> the u8 HWC composite; with net_out=True also the
+        [3][H][W] sigmoid plane of the padded shape."""
+        rgb = np.ascontiguousarray(rgb, np.uint8)
+        mask = np.ascontiguousarray(mask, np.uint8)
+        h, w = mask.shape
+        assert rgb.shape == (h, w, 3)
+        out = np.empty((h, w, 3), np.uint8)
+        net = np.empty((3, h + (-h) % 8, w + (-w) % 8), np.float32) if net_out else None
+        u8 = ctypes.POINTER(ctypes.c_uint8)
+        self._check(lib().lama_hip_inpaint(self.ctx, rgb.ctypes.data_as(u8), mask.ctypes.data_as(u8), h, w,
+                                           out.ctypes.data_as(u8), _f(net), self._err, 4096))
+        return (out, net) if net_out else out
+
+    def inpaint_device(self, d_rgb, d_mask, h, w, d_out, stream=None):
+        self._check(lib().lama_hip_inpaint_device(self.ctx, d_rgb, d_mask, h, w, d_out, stream, self._err, 4096))
+
+    def spectral(self, k, x, stages=False):
+        """FFC k's SpectralTransform alone over x [384][h][w] (lama_hip_spectral);
+        with stages=True also (f, spectrum, FU conv output, f + irfft2)."""
+        x = _c(x)
+        _, h, w = x.shape
+        out = np.empty((384, h, w), np.float32)
+        arr = None
+        st = None
+        if stages:
+            wh = w // 2 + 1
+            st = [np.empty((192, h, w), np.float32), np.empty((384, h, wh), np.float32),
+                  np.empty((384, h, wh), np.float32), np.empty((192, h, w), np.float32)]
+            arr = (ctypes.POINTER(ctypes.c_float) * 4)(*[_f(a) for a in st])
+        self._check(lib().lama_hip_spectral(self.ctx, k, _f(x), h, w, _f(out), arr, self._err, 4096))
+        return (out, st) if stages else out
+
+    def spectral_device(self, k, d_x, h, w, d_out, stream=None):
+        self._check(lib().lama_hip_spectral_device(self.ctx, k, d_x, h, w, d_out, stream, self._err, 4096))
 
     # device buffers
     def malloc(self, nbytes):

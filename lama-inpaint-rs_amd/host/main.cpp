@@ -242,29 +242,31 @@ void check_capacity(Engine &eng, int h, int w, const char *hint)
                    w, h, mib(need).c_str(), mib(free_b).c_str(), mib(total_b).c_str(), name, hint)};
 }
 
-// main.rs:318-361, without a CPU engine to fall back to
-std::vector<float> infer(Engine &eng, const std::vector<float> &input, int h, int w, const Args &args)
+// main.rs:318-361, without a CPU engine to fall back to.  The pass runs as
+// lama_hip_inpaint: build_input (main.rs:175-196, with the pad to a multiple
+// of 8), the forward and the 8-bit composite (main.rs:272-307) all on the
+// device; the result is the h x w composite of this image and mask.
+Rgb infer(Engine &eng, const Rgb &img, const Gray &mask, const Args &args)
 {
     if (args.force_cpu)
         throw Fail{"--cpu was requested, but this is the MI355X build (no CPU engine is compiled in).\n"
                    "Run without --cpu."};
     try {
         eng.load();
-        std::vector<float> out((size_t)3 * h * w);
-        if (lama_hip_forward(eng.ctx, input.data(), h, w, out.data(), eng.err, sizeof eng.err)) throw Fail{eng.err};
-        if (getenv("LAMA_PROFILE_OPS")) lama_hip_print_stats(eng.ctx);
+        Rgb out;
+        out.w = img.w;
+        out.h = img.h;
+        out.d.resize((size_t)img.w * img.h * 3);
+        if (lama_hip_inpaint(eng.ctx, img.d.data(), mask.d.data(), img.h, img.w, out.d.data(), nullptr, eng.err,
+                             sizeof eng.err))
+            throw Fail{eng.err};
+        if (getenv("LAMA_PROFILE_OPS") || getenv("LAMA_PROFILE_SUB") || getenv("LAMA_PROFILE"))
+            lama_hip_print_stats(eng.ctx);
         return out;
     } catch (const Fail &f) {
         if (args.force_gpu) throw Fail{"gpu inference failed: " + f.msg};
         throw Fail{"gpu unavailable (" + f.msg + ") and this build has no CPU engine to fall back to"};
     }
-}
-
-std::vector<float> build_input(const Rgb &img, const Gray &mask, int pad_h, int pad_w)
-{
-    std::vector<float> in((size_t)4 * (img.h + pad_h) * (img.w + pad_w));
-    lama_build_input(img.d.data(), mask.d.data(), img.h, img.w, pad_h, pad_w, in.data());
-    return in;
 }
 
 // main.rs:779-799
@@ -288,13 +290,6 @@ Gray crop_gray(const Gray &img, const lama_tile &t)
     return o;
 }
 
-// trunc(clamp(v, 0, 1) * 255 + 0.5), main.rs:303-305
-inline uint8_t to_u8(float v)
-{
-    v = v < 0.f ? 0.f : (v > 1.f ? 1.f : v);
-    return (uint8_t)(v * 255.0f + 0.5f);
-}
-
 void run_tiled(Engine &eng, const Rgb &src, const Gray &mask, const Args &args)
 {
     const auto t_start = Clock::now();
@@ -312,17 +307,16 @@ void run_tiled(Engine &eng, const Rgb &src, const Gray &mask, const Args &args)
     if (args.force_gpu)
         check_capacity(eng, side + pad, side + pad,
                        "Use --sections, which fills the mask in 512x512 passes, or run without --tile.");
-    const auto input = build_input(sub, sub_mask, pad, pad);
     const auto t0 = Clock::now();
-    const auto out = infer(eng, input, side + pad, side + pad, args);
+    const Rgb comp = infer(eng, sub, sub_mask, args);
     log(fmt("inference %dx%d in %.2fs", side, side, since(t0)));
-    const size_t plane = (size_t)(side + pad) * (side + pad);
+    // paste the window's hole pixels (main.rs:422-437)
     Rgb img = src;
     for (int y = 0; y < side; ++y)
         for (int x = 0; x < side; ++x) {
             if (sub_mask.d[(size_t)y * side + x] == 0) continue;
-            const size_t pi = (size_t)y * (side + pad) + x, o = ((size_t)(t.y0 + y) * src.w + t.x0 + x) * 3;
-            for (int c = 0; c < 3; ++c) img.d[o + c] = to_u8(out[c * plane + pi]);
+            const size_t o = ((size_t)(t.y0 + y) * src.w + t.x0 + x) * 3, q = ((size_t)y * side + x) * 3;
+            for (int c = 0; c < 3; ++c) img.d[o + c] = comp.d[q + c];
         }
     write_rgb(args.output, img);
     log("wrote " + args.output);
@@ -344,8 +338,6 @@ void run_sections(Engine &eng, const Rgb &src, const Gray &mask, const Args &arg
     const int side = std::max(1, std::min(TILE_MIN, std::min(width, height)));
     log(fmt("sections: %zu passes, %dx%d window each, rim inward", n, side, side));
     Rgb working = src;
-    const int pad = (PAD_MOD - side % PAD_MOD) % PAD_MOD;
-    const size_t plane = (size_t)(side + pad) * (side + pad);
     for (size_t i = 0; i < n; ++i) {
         const lama_section &s = sections[i];
         const int64_t cx = (s.x0 + s.x1) / 2, cy = (s.y0 + s.y1) / 2;
@@ -363,17 +355,17 @@ void run_sections(Engine &eng, const Rgb &src, const Gray &mask, const Args &arg
                 const int64_t gx = win.x0 + x, gy = win.y0 + y;
                 if (!(gx >= s.x0 && gx < s.x1 && gy >= s.y0 && gy < s.y1)) sub_mask.d[(size_t)y * side + x] = 0;
             }
-        const auto input = build_input(sub, sub_mask, pad, pad);
         const auto t0 = Clock::now();
-        const auto out = infer(eng, input, side + pad, side + pad, args);
+        const Rgb comp = infer(eng, sub, sub_mask, args);
         log(fmt("  pass %zu/%zu: %dx%d window at (%ld,%ld), %.2fs", i + 1, n, side, side, (long)win.x0, (long)win.y0,
                 since(t0)));
+        // write back this section's mask pixels only (main.rs:538-552)
         for (int64_t gy = s.y0; gy < s.y1; ++gy)
             for (int64_t gx = s.x0; gx < s.x1; ++gx) {
                 if (mask.d[(size_t)gy * width + gx] == 0) continue;
-                const size_t pi = (size_t)(gy - win.y0) * (side + pad) + (gx - win.x0);
+                const size_t q = ((size_t)(gy - win.y0) * side + (gx - win.x0)) * 3;
                 const size_t o = ((size_t)gy * width + gx) * 3;
-                for (int c = 0; c < 3; ++c) working.d[o + c] = to_u8(out[c * plane + pi]);
+                for (int c = 0; c < 3; ++c) working.d[o + c] = comp.d[q + c];
             }
         if (const char *dir = getenv("LAMA_DUMP_SECTIONS")) {
             char p[4096];
@@ -421,15 +413,9 @@ void run(const Args &args)
     if (args.force_gpu)
         check_capacity(eng, height + pad_h, width + pad_w,
                        "Use --tile to run on a window around the mask, or --sections for a large mask.");
-    const auto input = build_input(src, mask, pad_h, pad_w);
     const auto t0 = Clock::now();
-    const auto out = infer(eng, input, height + pad_h, width + pad_w, args);
+    const Rgb img = infer(eng, src, mask, args);
     log(fmt("inference %dx%d in %.2fs", width, height, since(t0)));
-    Rgb img;
-    img.w = width;
-    img.h = height;
-    img.d.resize((size_t)width * height * 3);
-    lama_composite(src.d.data(), mask.d.data(), height, width, pad_h, pad_w, out.data(), img.d.data());
     write_rgb(args.output, img);
     log("wrote " + args.output);
     log(fmt("total %.2fs", since(t_start)));

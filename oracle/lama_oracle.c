@@ -838,6 +838,17 @@ static Acts avg_pool2x2(const Acts *x)
     return o;
 }
 
+/* The LAMA_DUMP_SPECTRAL stages (cpu.rs:242-257) of the next
+ * spectral_forward, when set: [0] conv1 + BN + ReLU, [1] the stacked
+ * spectrum, [2] the FU conv after BN + ReLU, [3] f + FU(f).  Test hook only. */
+static float *const *g_spec_dump = NULL;
+
+static void spec_dump(int i, const Acts *a)
+{
+    if (g_spec_dump && g_spec_dump[i])
+        memcpy(g_spec_dump[i], a->data, sizeof(float) * (size_t)a->c * a->h * a->w);
+}
+
 /* cpu.rs:270-308 -- FourierUnit: per-channel rfft2 (stacked re/im planes,
  * channel-major pairs), 1x1 conv + BN + ReLU, per-channel irfft2. */
 static Acts fourier_unit(Spectral *sp, const Acts *x)
@@ -848,11 +859,13 @@ static Acts fourier_unit(Spectral *sp, const Acts *x)
 #pragma omp parallel for schedule(dynamic, 1)
     for (int c = 0; c < sp->half; ++c)
         or_rfft2_ortho(x->data + (long)c * h * w, h, w, spec.data + 2 * c * cplane);
+    spec_dump(1, &spec);
     Acts conv = conv1x1_acts(&sp->fu_conv, &spec);
     acts_free(&spec);
     bn_calibrate((Bn *)&sp->fu_bn, &conv);
     bn_apply(sp->fu_bn.scale, sp->fu_bn.shift, &conv);
     relu_inplace(&conv);
+    spec_dump(2, &conv);
     Acts out = acts_new(sp->half, h, w);
 #pragma omp parallel for schedule(dynamic, 1)
     for (int c = 0; c < sp->half; ++c)
@@ -870,10 +883,12 @@ static Acts spectral_forward(Spectral *sp, const Acts *x)
     bn_calibrate((Bn *)&sp->bn1, &feat);
     bn_apply(sp->bn1.scale, sp->bn1.shift, &feat);
     relu_inplace(&feat);
+    spec_dump(0, &feat);
     Acts fu = fourier_unit(sp, &feat);
     Acts sum = acts_new(sp->half, feat.h, feat.w);
     long n = (long)sp->half * feat.h * feat.w;
     for (long i = 0; i < n; ++i) sum.data[i] = feat.data[i] + fu.data[i];
+    spec_dump(3, &sum);
     acts_free(&feat);
     acts_free(&fu);
     Acts out = conv1x1_acts(&sp->conv2, &sum);
@@ -1059,6 +1074,33 @@ OR_EXPORT int or_net_forward(void *p, const float *input, int h, int w, float *o
     acts_free(&local);
     if (has_global) acts_free(&global);
     return 0;
+}
+
+/* The SpectralTransform of FFC k (0..35: resblock k/2, its conv1 or conv2
+ * FFC) alone over x [384][h][w] -> out [384][h][w] (Spectral::forward,
+ * cpu.rs:239-265), with the stages of g_spec_dump when `stages` is non-NULL.
+ * Returns nonzero for an index past the net's FFCs. */
+OR_EXPORT int or_net_spectral(void *p, int k, const float *x, int h, int w, float *out, float *const *stages)
+{
+    Net *net = (Net *)p;
+    int r = 0;
+    for (int si = 0; si < net->n; ++si) {
+        Step *st = &net->steps[si];
+        if (st->kind != ST_RES) continue;
+        if (r++ != k / 2) continue;
+        Ffc *f = k % 2 ? &st->ffc2 : &st->ffc;
+        if (!f->has_spectral) return 1;
+        Acts xa = acts_new(f->sp.conv1.cin, h, w);
+        memcpy(xa.data, x, sizeof(float) * (size_t)xa.c * h * w);
+        g_spec_dump = stages;
+        Acts o = spectral_forward(&f->sp, &xa);
+        g_spec_dump = NULL;
+        memcpy(out, o.data, sizeof(float) * (size_t)o.c * o.h * o.w);
+        acts_free(&xa);
+        acts_free(&o);
+        return 0;
+    }
+    return 1;
 }
 
 /* ------------------------------------------------- input and composite */

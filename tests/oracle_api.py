@@ -45,6 +45,8 @@ def lib():
         L.or_build_input.argtypes = [u8p, u8p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp]
         L.or_composite.argtypes = [u8p, u8p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, u8p]
         L.or_num_threads.restype = ctypes.c_int
+        L.or_net_spectral.argtypes = [ctypes.c_void_p, ctypes.c_int, fp, ctypes.c_int, ctypes.c_int, fp,
+                                      ctypes.POINTER(fp)]
         _lib = L
     return _lib
 
@@ -215,6 +217,24 @@ class OracleNet:
                 bufs[i] = _f(d)
         lib().or_net_forward(self._net, _f(x), h, w, _f(out), bufs)
         return (out, dumps) if steps else out
+
+    def spectral(self, k, x, stages=False):
+        """FFC k's SpectralTransform alone (Spectral::forward, cpu.rs:239-265)
+        over x [384][h][w]; with stages=True also (f, spectrum, FU conv output,
+        f + FU(f)), the LAMA_DUMP_SPECTRAL stages."""
+        x = f32(x)
+        _, h, w = x.shape
+        out = np.empty((384, h, w), np.float32)
+        st = None
+        arr = None
+        if stages:
+            wh = w // 2 + 1
+            st = [np.empty((192, h, w), np.float32), np.empty((384, h, wh), np.float32),
+                  np.empty((384, h, wh), np.float32), np.empty((192, h, w), np.float32)]
+            arr = (ctypes.POINTER(ctypes.c_float) * 4)(*[_f(a) for a in st])
+        if lib().or_net_spectral(self._net, k, _f(x), h, w, _f(out), arr):
+            raise ValueError(f"no SpectralTransform {k}")
+        return (out, st) if stages else out
 
     def __del__(self):
         if getattr(self, "_net", None):

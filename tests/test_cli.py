@@ -219,3 +219,51 @@ def test_plan_rejects_unsupported_shapes(pkg, engine):
         with pytest.raises(pkg.hip_engine.HipError, match=msg):
             engine.plan_bytes(h, w)
     assert engine.plan_bytes(8192, 16384)[0] > 0  # exactly 2^27 pixels plans
+
+
+@pytest.mark.gpu
+def test_cli_sections_config4_2048_with_1024_hole(H, engine, tmp_path, weights_dir):
+    """BASELINE configs[4] --sections as specified: a 2048 x 2048 image with a
+    seeded 1024 x 1024 hole, filled as 16 sections of 256 x 256 in 512 x 512
+    windows, rim inward; bit-exact with the restated pass loop."""
+    img = H.synth_image(2048, 2048, 1)
+    mask, (x0, y0) = H.synth_mask_rect(2048, 2048, 1024, 1024, 2)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    out = str(tmp_path / "o.png")
+    print("case sections 2048 / 1024 hole", flush=True)
+    r = run_cli("--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["cal"], "--sections",
+                timeout=600)
+    assert r.returncode == 0, r.stderr
+    assert b"sections: 16 passes, 512x512 window each" in r.stderr
+    got = H.png_read_rgb(out)
+    assert np.array_equal(got, _sections_by_hand(H, engine, img, mask))
+    assert np.array_equal(got[mask == 0], img[mask == 0])
+
+
+@pytest.mark.gpu
+def test_cli_dump_step_matches_the_oracle(H, tmp_path, weights_dir):
+    """LAMA_DUMP_STEP=<n> (cuda.rs:1572-1574, 1647-1662): the CLI's pass
+    writes /tmp/gpu_step_<n>.f32 in the reference's layout (local planes, then
+    global); it matches the oracle's step n within the per-layer bound.
+    LAMA_PROFILE adds the per-step lines (cuda.rs:1663-1686)."""
+    import oracle_api as O
+    img = H.synth_image(64, 80, 2)
+    mask, _ = H.synth_mask_rect(64, 80, 24, 16, 3)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    ref, ref_steps = O.OracleNet(O.read_safetensors(weights_dir["cal"])).forward(H.build_input(img, mask),
+                                                                                 steps=True)
+    for n in (7, 26):
+        path = f"/tmp/gpu_step_{n}.f32"
+        if os.path.exists(path):
+            os.remove(path)
+        env = dict(os.environ, LAMA_DUMP_STEP=str(n), LAMA_PROFILE="1", LAMA_PROFILE_SYNC="1")
+        r = subprocess.run([CLI, "--image", ip, "--mask", mp, "--output", str(tmp_path / "o.png"), "--weights",
+                            weights_dir["cal"]], capture_output=True, timeout=300, env=env)
+        assert r.returncode == 0, r.stderr
+        got = np.fromfile(path, dtype="<f4")
+        assert got.shape == ref_steps[n].shape
+        assert float(np.linalg.norm(got - ref_steps[n]) / np.linalg.norm(ref_steps[n])) < 1e-3
+        assert f"gpu dumped step {n}:".encode() in r.stderr
+        assert b"gpu step 28:" in r.stderr and b"gpu step  0:" in r.stderr
+        assert b"gpu step  7:" in r.stderr and b"global Some((384, 8, 10))" in r.stderr
+        assert b"gpu totals:" in r.stderr

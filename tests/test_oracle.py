@@ -231,3 +231,43 @@ def test_net_load_reports_missing_tensor(cal_weights):
     del w["model.7.conv2.ffc.convg2g.fu.bn.running_var"]
     with pytest.raises(RuntimeError, match="missing tensor in weight blob: model.7.conv2.ffc.convg2g.fu.bn.running_var"):
         O.OracleNet(w)
+
+
+@pytest.mark.parametrize("k,hw", [(0, (32, 32)), (7, (16, 32)), (35, (32, 16))])
+def test_spectral_block_matches_independent_torch_model(weights_dir, k, hw):
+    """or_net_spectral (Spectral::forward, cpu.rs:239-265, the isolated
+    SpectralTransform of BASELINE configs[2]) against the torch model's
+    SpectralTransform on N(0,1) inputs with the plain fixture weights: every
+    LAMA_DUMP_SPECTRAL stage (f, spectrum, FU conv, f + ifft) and the output.
+    Power-of-two planes, where torch's FFT sign is the reference's."""
+    pytest.importorskip("torch")
+    import torch_ffc
+    W = O.read_safetensors(weights_dir["plain"])
+    h, w = hw
+    x = np.random.default_rng(100 + k).standard_normal((384, h, w)).astype(np.float32)
+    out, st = O.OracleNet(W).spectral(k, x, stages=True)
+    tout, tst = torch_ffc.spectral_block(W, k, x)
+    for i in range(4):
+        assert rel_err(st[i], tst[i]) < 1e-5, i
+    assert rel_err(out, tout) < 1e-5
+    # the wrong FFC's weights fail the same comparison
+    other = O.OracleNet(W).spectral((k + 1) % 36, x)
+    assert rel_err(other, tout) > 0.1
+
+
+@pytest.mark.parametrize("h,w,pad_h,pad_w", [(13, 11, 3, 5), (16, 8, 0, 0), (3, 5, 5, 3), (1, 1, 7, 7)])
+def test_host_build_input_and_composite_equal_the_oracle(pkg, h, w, pad_h, pad_w):
+    """The product host rules (liblama_host: lama_build_input, lama_composite,
+    main.rs:175-196, 272-307) against the oracle's restatement, bit for bit,
+    over every byte value and with bottom/right padding (including a pad
+    wider than the image, which wraps the reflection)."""
+    H = pkg.host_api
+    rng = np.random.default_rng(h * 100 + w)
+    rgb = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    rgb.reshape(-1)[:min(256, rgb.size)] = np.arange(min(256, rgb.size), dtype=np.uint8)
+    mask = rng.integers(0, 256, (h, w), dtype=np.uint8)
+    mask.reshape(-1)[::3] = 0
+    assert np.array_equal(H.build_input(rgb, mask, pad_h, pad_w), O.build_input(rgb, mask, pad_h, pad_w))
+    net = rng.uniform(-0.1, 1.1, (3, h + pad_h, w + pad_w)).astype(np.float32)
+    net.reshape(-1)[:4] = [0.0, 1.0, np.float32(0.5) / 255, np.float32(254.5) / 255]
+    assert np.array_equal(H.composite(rgb, mask, net, pad_h, pad_w), O.composite(rgb, mask, net, pad_h, pad_w))

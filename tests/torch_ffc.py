@@ -12,31 +12,57 @@ import torch
 import torch.nn.functional as F
 
 
-def forward(W, x):
-    """W: {name: np.ndarray}; x: [4][h][w] -> (out [3][h][w], {step: activation})."""
+def _ops(W):
     t = lambda n: torch.from_numpy(np.array(W[n], np.float32))  # noqa: E731
-    steps = {}
 
     def bn(y, p):
         return F.batch_norm(y, t(p + ".running_mean"), t(p + ".running_var"), t(p + ".weight"), t(p + ".bias"),
                             False, 0.0, 1e-5)
 
+    def fourier_unit(y, p, st=None):
+        b, c, h, w = y.shape
+        ff = torch.fft.rfftn(y, dim=(-2, -1), norm="ortho")
+        ff = torch.stack((ff.real, ff.imag), dim=2).reshape(b, 2 * c, h, w // 2 + 1)  # [c0.re, c0.im, ...]
+        if st is not None:
+            st.append(ff)
+        ff = F.relu(bn(F.conv2d(ff, t(p + ".conv_layer.weight")), p + ".bn"))
+        if st is not None:
+            st.append(ff)
+        ff = ff.reshape(b, c, 2, h, w // 2 + 1)
+        return torch.fft.irfftn(torch.complex(ff[:, :, 0], ff[:, :, 1]), s=(h, w), dim=(-2, -1), norm="ortho")
+
+    def spectral(y, p, st=None):
+        f = F.relu(bn(F.conv2d(y, t(p + ".conv1.0.weight")), p + ".conv1.1"))
+        if st is not None:
+            st.append(f)
+        s = f + fourier_unit(f, p + ".fu", st)
+        if st is not None:
+            st.append(s)
+        return F.conv2d(s, t(p + ".conv2.weight"))
+
+    return t, bn, spectral
+
+
+def spectral_block(W, k, x):
+    """FFC k's SpectralTransform (model.{5 + k//2}.conv{1 + k%2}) over x
+    [384][h][w] -> (out, [f, spectrum, FU conv after BN + ReLU, f + ifft])."""
+    _, _, spectral = _ops(W)
+    st = []
+    with torch.no_grad():
+        y = spectral(torch.from_numpy(np.ascontiguousarray(x, np.float32))[None],
+                     f"model.{5 + k // 2}.conv{1 + k % 2}.ffc.convg2g", st)
+    return y[0].numpy(), [a[0].numpy() for a in st]
+
+
+def forward(W, x):
+    """W: {name: np.ndarray}; x: [4][h][w] -> (out [3][h][w], {step: activation})."""
+    t, bn, spectral = _ops(W)
+    steps = {}
+
     def conv(y, w, pad, stride):
         if pad:
             y = F.pad(y, (pad, pad, pad, pad), mode="reflect")
         return F.conv2d(y, w, stride=stride)
-
-    def fourier_unit(y, p):
-        b, c, h, w = y.shape
-        ff = torch.fft.rfftn(y, dim=(-2, -1), norm="ortho")
-        ff = torch.stack((ff.real, ff.imag), dim=2).reshape(b, 2 * c, h, w // 2 + 1)  # [c0.re, c0.im, ...]
-        ff = F.relu(bn(F.conv2d(ff, t(p + ".conv_layer.weight")), p + ".bn"))
-        ff = ff.reshape(b, c, 2, h, w // 2 + 1)
-        return torch.fft.irfftn(torch.complex(ff[:, :, 0], ff[:, :, 1]), s=(h, w), dim=(-2, -1), norm="ortho")
-
-    def spectral(y, p):
-        f = F.relu(bn(F.conv2d(y, t(p + ".conv1.0.weight")), p + ".conv1.1"))
-        return F.conv2d(f + fourier_unit(f, p + ".fu"), t(p + ".conv2.weight"))
 
     def ffc(xl, xg, pf, pb):
         ol = conv(xl, t(pf + ".convl2l.weight"), 1, 1) + conv(xg, t(pf + ".convg2l.weight"), 1, 1)
