@@ -56,6 +56,26 @@ int lama_hip_forward(lama_hip_ctx *ctx, const float *input, int h, int w, float 
 int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int w,
                             float *d_output, void *stream, char *err, size_t errlen);
 
+/* lama_hip_forward_device that allocates nothing.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * The pass's activations, partial sums, FFT scratch and launch descriptors
+ * live in a device array of LAMA_SCRATCH_BYTES = 192 MiB (`lama_scratch`, a
+ * code object of its own that lama_hip_open loads once per device per
+ * process; the device holds it until the process ends).  Shapes whose arena
+ * exceeds it are rejected with an error: up to 512 x 512 fits (177 MiB).
+ * The call makes no hipMalloc, hipFree, event or graph creation (and no
+ * per-family profiling); the caller passes device input and output as for
+ * lama_hip_forward_device.  Every context on a GPU shares that GPU's array,
+ * which keeps the last call's contents; no kernel of the pass reads what the
+ * pass has not written, and the launch descriptors are re-uploaded on
+ * `stream` whenever another context or shape used the array last.  Calls
+ * that overlap on one GPU (different streams, threads or contexts) race on
+ * the array: the caller orders them.  Asynchronous on `stream` (NULL = the
+ * engine's own); lama_hip_synchronize waits for it. */
+int lama_hip_forward_device_noalloc(lama_hip_ctx *ctx, const float *d_input, int h, int w,
+                                    float *d_output, void *stream, char *err, size_t errlen);
+
 /* The whole-image flow around cuda::run, on the device: the pad to a multiple
  * of 8 (main.rs:241-242), build_input (main.rs:175-196), the forward, and the
  * 8-bit composite of main.rs:272-307 fused into the output convolution's

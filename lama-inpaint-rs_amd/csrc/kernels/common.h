@@ -12,6 +12,9 @@
 #define LAMA_PW_KC 16
 #endif
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
+// Bytes of the no-allocation entry point's device array: the activation arena
+// and descriptors of one forward of up to 512 x 512 (177.2 MiB at 512 x 512).
+#define LAMA_SCRATCH_BYTES (192u << 20)
 // LDS bytes of the two ping-pong buffers of a split-mode FFT block (row pairs
 // or columns per block = this / (2 * 8 * plane side)).  32 KB rather than 64:
 // a block then fits on a CU beside the FFC GEMM's two workgroups (51 KB each),

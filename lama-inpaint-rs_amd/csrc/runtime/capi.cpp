@@ -17,6 +17,11 @@ __asm__(".section .rodata\n"
         ".global lama_hsaco_end\n"
         "lama_hsaco_end:\n"
         ".byte 0\n"
+        ".balign 4096\n"
+        ".global lama_scratch_hsaco_start\n"
+        "lama_scratch_hsaco_start:\n"
+        ".incbin \"" LAMA_SCRATCH_HSACO_PATH "\"\n"
+        ".byte 0\n"
         ".previous\n");
 
 struct lama_hip_ctx {
@@ -81,6 +86,13 @@ extern "C" int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, 
                                        void *stream, char *err, size_t errlen)
 {
     GUARD(ctx->eng.forward_device(d_input, h, w, d_output, (hipStream_t)stream, e_));
+}
+
+extern "C" int lama_hip_forward_device_noalloc(lama_hip_ctx *ctx, const float *d_input, int h, int w,
+                                               float *d_output, void *stream, char *err, size_t errlen)
+{
+    if (ctx && (!d_input || !d_output)) return fail(err, errlen, "lama_hip_forward_device_noalloc: null buffer");
+    GUARD(ctx->eng.forward_device_noalloc(d_input, h, w, d_output, (hipStream_t)stream, e_));
 }
 
 extern "C" int lama_hip_forward_steps(lama_hip_ctx *ctx, const float *input, int h, int w, float *output,

@@ -22,7 +22,25 @@
 #include <cstdio>
 #include <functional>
 
+#include <atomic>
+#include <mutex>
+
 namespace lama {
+
+// The no-allocation entry point's device array, per device: the code object
+// that defines it (loaded once per process, never unloaded), its address on
+// that device, and whose descriptors it holds -- the engine id and shape of
+// the last forward_device_noalloc on the device (0: none).
+struct DeviceScratch {
+    hipModule_t mod = nullptr;
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    uint64_t owner = 0;
+    int h = 0, w = 0;
+};
+static std::mutex g_scratch_mu;
+static std::map<int, DeviceScratch> g_scratch;
+static std::atomic<uint64_t> g_engine_ids{0};
 
 const char *const kFamilyName[F_COUNT] = {"conv7x7",  "conv3x3s2",  "conv3x3",    "conv1x1", "convt",
                                           "rfft2",    "irfft2",     "tail",       "finalize", "conv1x1res",
@@ -219,9 +237,17 @@ bool is_pow2(int n) { return n > 0 && (n & (n - 1)) == 0; }
 
 }  // namespace
 
+void Engine::release_scratch_owner()
+{
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch.find(device_);
+    if (it != g_scratch.end() && it->second.owner == id_) it->second.owner = 0;
+}
+
 Engine::~Engine()
 {
     if (!hip_) return;
+    if (id_) release_scratch_owner();
     for (auto &kv : plans_) free_plan(kv.second);
     for (auto &kv : spec_plans_)
         if (kv.second.arena) hip_->hipFree(kv.second.arena);
@@ -249,6 +275,7 @@ bool Engine::check(hipError_t e, const char *what, std::string &err)
 
 extern "C" const unsigned char lama_hsaco_start[];
 extern "C" const unsigned char lama_hsaco_end[];
+extern "C" const unsigned char lama_scratch_hsaco_start[];
 
 bool Engine::open(std::string &err)
 {
@@ -276,6 +303,36 @@ bool Engine::open(std::string &err)
         return false;
     }
     if (!check(hip_->hipModuleLoadData(&module_, lama_hsaco_start), "hipModuleLoadData", err)) return false;
+    // The no-allocation entry point's array: set up once per device per
+    // process, with that device current -- its code object is loaded and the
+    // array's address on this device looked up (hipModuleGetGlobal, the
+    // module-loaded form of hipGetSymbolAddress); every later use goes through
+    // that address.
+    id_ = ++g_engine_ids;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        DeviceScratch &d = g_scratch[device_];
+        if (!d.ptr) {
+            hipModule_t m = nullptr;
+            if (!check(hip_->hipModuleLoadData(&m, lama_scratch_hsaco_start), "hipModuleLoadData(scratch)", err))
+                return false;
+            hipDeviceptr_t p = nullptr;
+            size_t n = 0;
+            if (!check(hip_->hipModuleGetGlobal(&p, &n, m, "lama_scratch"), "hipModuleGetGlobal(lama_scratch)", err)) {
+                hip_->hipModuleUnload(m);
+                return false;
+            }
+            if (!p || n < LAMA_SCRATCH_BYTES) {
+                hip_->hipModuleUnload(m);
+                err = "lama_scratch: " + std::to_string(n) + " bytes, expected " + std::to_string(LAMA_SCRATCH_BYTES);
+                return false;
+            }
+            d.mod = m;
+            d.ptr = p;
+            d.bytes = n;
+        }
+        scratch_ = d.ptr;
+    }
     for (int f = 0; f < F_COUNT; ++f)
         if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
     for (int f = 0; f < 4; ++f)
@@ -439,6 +496,8 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
     for (auto &kv : spec_plans_)
         if (kv.second.arena) hip_->hipFree(kv.second.arena);
     spec_plans_.clear();
+    na_plan_ = Plan{};  // its descriptors point into the old weights
+    release_scratch_owner();
     if (warena_) hip_->hipFree(warena_);
     warena_ = fresh;
     warena_bytes_ = A.h.size() * 4;
@@ -1345,6 +1404,64 @@ bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipSt
     if (!check(hip_->hipMemcpyAsync(d_out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err))
         return false;
     return mark_done(s, err);
+}
+
+// forward_device on the device's scratch array instead of an allocated arena.
+// Host work only (plan layout, descriptor staging) plus copies and launches on
+// `s`: no device allocation, no event or graph creation (profiling is off for
+// these passes).  The descriptors are re-uploaded (on `s`) whenever another
+// context or another shape used the array last.
+bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err)
+{
+    if (!have_weights_) {
+        err = "no weights loaded";
+        return false;
+    }
+    if (!shape_ok(h, w, err)) return false;
+    if (!scratch_) {
+        err = "the no-allocation scratch array was not set up";
+        return false;
+    }
+    if (!s) s = stream_;
+    const bool fresh = !(na_plan_.arena && na_plan_.H == h && na_plan_.W == w);
+    if (fresh) {
+        uint64_t need = 0, wb = 0;
+        if (!plan_bytes(h, w, need, wb, err)) return false;
+        if (need > LAMA_SCRATCH_BYTES) {
+            err = "input " + std::to_string(w) + "x" + std::to_string(h) + " needs " + std::to_string(need >> 20) +
+                  " MiB of device memory; the no-allocation entry point's array holds " +
+                  std::to_string(LAMA_SCRATCH_BYTES >> 20) + " MiB (up to 512x512)";
+            return false;
+        }
+        Plan p;
+        p.H = h;
+        p.W = w;
+        if (!build_plan(p, scratch_, err)) return false;
+        na_plan_ = std::move(p);
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        DeviceScratch &d = g_scratch[device_];
+        if (fresh || d.owner != id_ || d.h != h || d.w != w) {
+            if (!upload_plan(na_plan_, s, err)) {
+                d.owner = 0;
+                return false;
+            }
+            d.owner = id_;
+            d.h = h;
+            d.w = w;
+        }
+    }
+    const uint32_t prof = prof_mask_;
+    prof_mask_ = 0;
+    const bool ok =
+        check(hip_->hipMemcpyAsync(na_plan_.in, d_in, 4ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(input)",
+              err) &&
+        run(na_plan_, s, nullptr, err) &&
+        check(hip_->hipMemcpyAsync(d_out, na_plan_.out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s),
+              "hipMemcpy(output)", err);
+    prof_mask_ = prof;
+    return ok && mark_done(s, err);
 }
 
 // A pass enqueued on a caller's stream: synchronize() must also wait for it.

@@ -129,6 +129,10 @@ public:
     bool spectral_device(int k, const float *d_x, int h, int w, float *d_out, hipStream_t s, std::string &err);
     // Waits for the engine stream and for the last pass enqueued on a caller's stream.
     bool synchronize(std::string &err);
+    // forward_device with no device allocation: the activation arena and the
+    // launch descriptors live in the device's lama_scratch array (one per device
+    // per process, shared by every context on it; see lama_hip.h).
+    bool forward_device_noalloc(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err);
 
     // profiling (families whose bit is set get per-launch events)
     void set_profile(uint32_t mask) { prof_mask_ = mask; }
@@ -225,6 +229,13 @@ private:
     const float *wp(size_t off) const { return warena_ + off; }
 
     std::map<std::pair<int, int>, Plan> plans_;
+    // the no-allocation entry point: its plan (arena = this device's scratch
+    // array), the array's address, and this engine's identity in the
+    // process-wide record of which context's descriptors the array holds
+    Plan na_plan_;
+    void *scratch_ = nullptr;
+    uint64_t id_ = 0;
+    void release_scratch_owner();
     std::map<std::pair<int, int>, SpecPlan> spec_plans_;
     hipFunction_t fn_build_in_ = nullptr, fn_tail_u8_ = nullptr;
 

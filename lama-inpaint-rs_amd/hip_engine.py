@@ -58,6 +58,7 @@ def lib():
         L.lama_hip_op_rfft2.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, cp, sz]
         L.lama_hip_op_irfft2.argtypes = [vp, fp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, cp, sz]
         L.lama_hip_op_tail.argtypes = [vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, fp, fp, cp, sz]
+        L.lama_hip_forward_device_noalloc.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, cp, sz]
         u8p = ctypes.POINTER(ctypes.c_uint8)
         L.lama_hip_inpaint.argtypes = [vp, u8p, u8p, ctypes.c_int, ctypes.c_int, u8p, fp, cp, sz]
         L.lama_hip_inpaint_device.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, cp, sz]
@@ -135,6 +136,10 @@ class Engine:
 
     def forward_device(self, d_in, h, w, d_out, stream=None):
         self._check(lib().lama_hip_forward_device(self.ctx, d_in, h, w, d_out, stream, self._err, 4096))
+
+    def forward_device_noalloc(self, d_in, h, w, d_out, stream=None):
+        """lama_hip_forward_device on the device's scratch array: no allocation."""
+        self._check(lib().lama_hip_forward_device_noalloc(self.ctx, d_in, h, w, d_out, stream, self._err, 4096))
 
     def inpaint(self, rgb, mask, net_out=False):
         """The whole-image flow on the device (lama_hip_inpaint): u8 HWC image
