@@ -86,7 +86,9 @@ def main():
     # The dominant kernel is timed with HIP events on its own stream during the
     # timed region, on every --sample-every-th pass (the events ride in the
     # dispatch packets; sampling keeps their cost out of `value`).
-    dom = "conv3x3"
+    # both launches of each FFC: A = l2l + l2g (family conv3x3) and B = g2l
+    # (family conv3x3g2l), one kernel
+    dom_fams = ["conv3x3", "conv3x3g2l"]
     # the FFC 3x3 convolutions run as Winograd F(2,3) along x unless
     # LAMA_FFC_WINO=0 selects the direct implicit GEMM; FLOPs are the
     # convolution's algorithmic count either way (Winograd issues 2/3 of them
@@ -97,7 +99,7 @@ def main():
     eng.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        eng.profile([dom] if i % args.sample_every == 0 else ())
+        eng.profile(dom_fams if i % args.sample_every == 0 else ())
         eng.forward_device(d_in, S, S, d_out)
     eng.synchronize()
     elapsed = time.perf_counter() - t0
@@ -154,9 +156,25 @@ def main():
     eng.free(d_ys)
 
     ms = elapsed * 1e3 / args.steps
-    d = prof[dom]
-    launch_ms = d["ms"] / max(1, d["launches"])
-    flops_launch = d["flops"] / max(1, d["launches"])
+    # the dominant kernel's launches, A and B, each timed by its kernel-clock
+    # window (first workgroup start to last workgroup end: the interval a
+    # kernel trace reports for the dispatch).  The HIP event interval is
+    # reported beside it for A (which waits on no other stream): it also holds
+    # the launch's dispatch latency.  B's event interval would start at its
+    # cross-stream wait.
+    dA, dB = prof["conv3x3"], prof["conv3x3g2l"]
+    n_clock = dA.get("clock_launches", 0) + dB.get("clock_launches", 0)
+    n_dom = dA["launches"] + dB["launches"]
+    flops_launch = (dA["flops"] + dB["flops"]) / max(1, n_dom)
+    launch_ms_events_a = dA["ms"] / max(1, dA["launches"])
+    if n_clock == n_dom and n_clock > 0:
+        launch_ms = (dA["clock_ms"] + dB["clock_ms"]) / n_clock
+        clock_a = dA["clock_ms"] / dA["clock_launches"]
+        clock_b = dB["clock_ms"] / dB["clock_launches"]
+    else:  # no stamps read: A's events alone
+        launch_ms = launch_ms_events_a
+        flops_launch = dA["flops"] / max(1, dA["launches"])
+        clock_a = clock_b = None
     achieved = flops_launch / (launch_ms * 1e-3) / 1e12
     traffic = None
     if args.traffic and os.path.exists(args.traffic):
@@ -180,7 +198,8 @@ def main():
     # conv1x1 and first convt) is timed from the wait, so it includes it
     per_family = {f: {"ms_per_pass": round(v["ms"] / 3, 4), "launches_per_pass": v["launches"] // 3,
                       "tflops": round(v["flops"] / (v["ms"] * 1e9), 2) if v["ms"] > 0 else None,
-                      "gbps": round(v["bytes"] / (v["ms"] * 1e6), 1) if v["ms"] > 0 else None}
+                      "gbps": round(v["bytes"] / (v["ms"] * 1e6), 1) if v["ms"] > 0 else None,
+                      "clock_ms_per_pass": round(v["clock_ms"] / 3, 4) if v.get("clock_launches") else None}
                   for f, v in fam.items()}
 
     cpu = None
@@ -233,15 +252,20 @@ def main():
                      "kernel": (dom_kernel + (" (FFC 3x3 convolutions as Winograd F(2,3) along x, 256 workgroups of "
                                               "64 channels x 2 rows x 64 px" if wino else
                                               " (FFC 3x3 implicit GEMMs, 512 workgroups of 64 channels x 64 px")
-                                + "; timed: each FFC's l2l+l2g launch, the larger of its two, which waits on no "
-                                  "other stream; it overlaps the FFC's g2l launch and spectral branch on two other "
-                                  "streams, so its duration includes the time it shares the CUs with them; the g2l "
-                                  "launch (family conv3x3g2l, same kernel) is issued after a cross-stream wait, "
-                                  "which its event interval would include; achieved counts the convolution's "
-                                  "algorithmic FLOPs)"),
+                                + "; timed: both launches of every FFC of the sampled passes, A = l2l + l2g "
+                                  "(4.83 GFLOP) and B = g2l (3.62 GFLOP), each from its first workgroup's start "
+                                  "to its last workgroup's end on the device clock; they overlap each other and "
+                                  "the spectral branch on three streams, so a duration includes the time the "
+                                  "launch shares the CUs; achieved counts the convolution's algorithmic FLOPs)"),
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
                      "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5),
+                     "launch_ms_source": ("kernel clock (s_memrealtime stamps of every workgroup)"
+                                          if clock_a is not None else "HIP events (A launches)"),
+                     "launches_timed": int(n_dom),
+                     "launch_ms_a": round(clock_a, 5) if clock_a is not None else None,
+                     "launch_ms_b": round(clock_b, 5) if clock_b is not None else None,
+                     "launch_ms_a_events": round(launch_ms_events_a, 5),
                      "mfma_issued_frac": round(achieved * (2.0 / 3.0 if wino else 1.0) / PEAK_FP32_MFMA, 4)},
         # all conv families' algorithmic (direct-convolution) FLOPs over the
         # pass's wall time, and the MFMA work actually executed (Winograd

@@ -36,6 +36,14 @@ typedef struct lama_hip_ctx lama_hip_ctx;
 int lama_hip_open(lama_hip_ctx **out, char *err, size_t errlen);
 void lama_hip_close(lama_hip_ctx *ctx);
 
+/* The plan this engine implements, as the reference's model::describe
+ * (model.rs:260-274) prints it: "29 steps, 40 FFC_BN_ACT calls, 18
+ * resblocks", the Big-LaMa generator of model::build (model.rs:117-257).
+ * cuda::run takes the Model it runs; this engine's plan is fixed, so the
+ * caller compares describe(model) with this string and reports a plan
+ * mismatch instead of running another network's weights through it. */
+const char *lama_hip_plan_signature(void);
+
 /* Replaces the weight side of load_steps (cuda.rs:330-387 blob_arena,
  * 595-693 Staging, 695-734 load_conv, 737-830 BN fold, 903-962 load_steps):
  * `blob` is the whole safetensors file and `table` its tensor index with
@@ -136,6 +144,13 @@ void lama_hip_profile_reset(lama_hip_ctx *ctx);
  * Returns 1 for a valid i, 0 past the end. */
 int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, uint64_t *launches,
                           double *ms, double *flops, double *bytes);
+/* Family i's profiled launches timed on the device clock instead of by
+ * events: each workgroup of a profiled convolution launch records its start
+ * and end (s_memrealtime); a launch lasts from its first workgroup start to
+ * its last workgroup end, the window a kernel trace reports, without the
+ * dispatch latency the event interval includes.  Conv families only (0-4, 9,
+ * 10); returns 1 for a valid i, 0 past the end. */
+int lama_hip_profile_read_clock(lama_hip_ctx *ctx, int i, uint64_t *launches, double *ms);
 /* print_op_stats / print_sub_stats / print_stats (cuda.rs:1738-1806): the
  * per-family event timings to stderr as "op" lines (LAMA_PROFILE_OPS), "sub"
  * lines (LAMA_PROFILE_SUB) and a "gpu totals" line (LAMA_PROFILE); the "op"

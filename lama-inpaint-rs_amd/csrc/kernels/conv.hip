@@ -652,9 +652,23 @@ __device__ __forceinline__ int find_problem(const ProbStarts &ps, int &b)
 // Parameters of every conv kernel: the problem table and the first workgroup
 // of problems 1..3 as separate scalars, so all of them are preloaded into
 // SGPRs with the dispatch (-amdgpu-kernarg-preload-count) instead of being
-// fetched from the kernarg segment at the head of the prologue.
-#define LAMA_CONV_PARAMS const ConvProblem *__restrict__ probs, int ps1, int ps2, int ps3
+// fetched from the kernarg segment at the head of the prologue.  `stamp`
+// (null unless the launch is profiled) receives the workgroup's start and end
+// on the constant-rate device clock (s_memrealtime), written by thread 0 to
+// stamp[2 * blockIdx.x] and stamp[2 * blockIdx.x + 1] with ordinary vector
+// stores: the host takes the launch's duration as the last end minus the
+// first start, the window a kernel trace reports.
+#define LAMA_CONV_PARAMS \
+    const ConvProblem *__restrict__ probs, int ps1, int ps2, int ps3, unsigned long long *__restrict__ stamp
 #define LAMA_CONV_STARTS const ProbStarts ps{0, {ps1, ps2, ps3}}
+#define LAMA_STAMP_BEGIN const unsigned long long stamp_t0 = stamp ? __builtin_amdgcn_s_memrealtime() : 0ull
+#define LAMA_STAMP_END                                                      \
+    do {                                                                    \
+        if (stamp && threadIdx.x == 0) {                                    \
+            stamp[2 * blockIdx.x] = stamp_t0;                               \
+            stamp[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();  \
+        }                                                                   \
+    } while (0)
 
 using CfgHead = Cfg<7, 7, 1, true, 4, 2, 32>;
 using CfgDown = Cfg<3, 3, 2, true, 8, 2, 32>;
@@ -679,15 +693,20 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(LAMA_CONV_PAR
     __shared__ __attribute__((aligned(16))) float lds[C::W_LDS + 2 * C::P_LDS];
     __shared__ float epl[192];
     float *const wl = lds, *const pl0 = lds + C::W_LDS, *const pl1 = pl0 + C::P_LDS;
+    LAMA_STAMP_BEGIN;
     const ConvProblem &P = probs[0];
     const ConvSeg sg = P.s0;
     const int ntiles = P.nblocks;
     int t = blockIdx.x;
-    if (t >= ntiles) return;  // whole workgroup
+    if (t >= ntiles) {  // whole workgroup
+        LAMA_STAMP_END;
+        return;
+    }
     if (sg.nchunk != 1 || P.mblocks != 1) {
         // more than 4 input channels or 64 output channels (single-op tests):
         // one tile at a time through the generic path
         for (; t < ntiles; t += gridDim.x) conv_tile<C, false, 1>(P, t, lds, epl);
+        LAMA_STAMP_END;
         return;
     }
     auto origin = [&](int tile, int &oy0, int &ox0) {
@@ -732,17 +751,20 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(LAMA_CONV_PAR
         load_p<C>(nxt, sl, sg, 0);
         __syncthreads();
     }
+    LAMA_STAMP_END;
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_PARAMS)
 {
     LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
     __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     conv_tile<CfgDown, false>(probs[pi], b, lds, epl);
+    LAMA_STAMP_END;
 }
 
 // FFC spatial convolutions: 3x3 stride 1 reflect pad 1, with an optional 1x1
@@ -750,11 +772,13 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_P
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PARAMS)
 {
     LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(CfgFfc::LDS, CfgFfc1::LDS)];
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     conv_tile<CfgFfc, true>(probs[pi], b, lds, epl);
+    LAMA_STAMP_END;
 }
 
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
@@ -766,12 +790,14 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
     {                                                                                                       \
         side_priority();                                                                                    \
         LAMA_CONV_STARTS;                                                                                   \
+        LAMA_STAMP_BEGIN;                                                                                   \
         using C = PwCfg<KC, VW, NPX>;                                                                      \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \
         int pi = find_problem(ps, b);                                                             \
         pw_tile<C, PREFETCH, D>(probs[pi], b, lds, epl);                                                     \
+        LAMA_STAMP_END;                                                                                     \
     }
 #ifndef LAMA_PW_DEPTH_RES
 #define LAMA_PW_DEPTH_RES LAMA_PW_DEPTH
@@ -793,6 +819,7 @@ LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, 1, 64, true, LAMA_PW_DEPTH_RES)
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(LAMA_CONV_PARAMS)
 {
     LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
     __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
     __shared__ float epl[192];
     int b = blockIdx.x;
@@ -803,4 +830,5 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(LAMA_CONV_PARAM
     case 2: conv_tile<CfgT10, false>(probs[2], b, lds, epl); break;
     default: conv_tile<CfgT11, false>(probs[3], b, lds, epl); break;
     }
+    LAMA_STAMP_END;
 }

@@ -227,9 +227,11 @@ __device__ __forceinline__ void wino_tile(const ConvProblem &P, int b, float *ld
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3w(LAMA_CONV_PARAMS)
 {
     LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
     __shared__ __attribute__((aligned(16))) float lds[2 * WCfg::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     wino_tile(probs[pi], b, lds, epl);
+    LAMA_STAMP_END;
 }

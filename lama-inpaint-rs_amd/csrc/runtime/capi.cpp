@@ -70,6 +70,14 @@ extern "C" int lama_hip_open(lama_hip_ctx **out, char *err, size_t errlen)
 
 extern "C" void lama_hip_close(lama_hip_ctx *ctx) { delete ctx; }
 
+extern "C" const char *lama_hip_plan_signature(void)
+{
+    // model::describe (model.rs:260-274) of the one plan this engine runs:
+    // ReflectPad, model.1-4, 18 resblocks, Concat, 3 upsamples, ReflectPad,
+    // OutConv; 4 + 2 * 18 FFC_BN_ACT calls
+    return "29 steps, 40 FFC_BN_ACT calls, 18 resblocks";
+}
+
 extern "C" int lama_hip_load_weights(lama_hip_ctx *ctx, const void *blob, size_t blob_len,
                                      const lama_tensor_info *table, size_t n, char *err, size_t errlen)
 {
@@ -147,6 +155,16 @@ extern "C" int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_
     if (ms) *ms = m;
     if (flops) *flops = f;
     if (bytes) *bytes = b;
+    return 1;
+}
+
+extern "C" int lama_hip_profile_read_clock(lama_hip_ctx *ctx, int i, uint64_t *launches, double *ms)
+{
+    uint64_t l = 0;
+    double m = 0;
+    if (!ctx || !ctx->eng.profile_read_clock(i, l, m)) return 0;
+    if (launches) *launches = l;
+    if (ms) *ms = m;
     return 1;
 }
 

@@ -253,6 +253,7 @@ Engine::~Engine()
         if (kv.second.arena) hip_->hipFree(kv.second.arena);
     if (warena_) hip_->hipFree(warena_);
     if (ev_done_) hip_->hipEventDestroy(ev_done_);
+    if (stamp_buf_) hip_->hipFree(stamp_buf_);
     for (auto &p : pending_) {
         hip_->hipEventDestroy(p.a);
         hip_->hipEventDestroy(p.b);
@@ -359,6 +360,9 @@ bool Engine::open(std::string &err)
         int lds = 0;
         if (hip_->hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_) == hipSuccess && lds > 0)
             max_lds_ = (size_t)lds;
+        int khz = 0;  // the rate of the s_memrealtime clock the stamps read
+        if (hip_->hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_) == hipSuccess && khz > 0)
+            clock_khz_ = khz;
     }
     if (!check(hip_->hipStreamCreate(&stream_), "hipStreamCreate", err) ||
         !check(hip_->hipStreamCreate(&side_), "hipStreamCreate", err) ||
@@ -1111,14 +1115,41 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     return true;
 }
 
+static bool is_conv_family(int f)
+{
+    return f == F_CONV7 || f == F_CONV3S2 || f == F_CONV3 || f == F_CONV1 || f == F_CONVT || f == F_CONV1R ||
+           f == F_CONV3G;
+}
+
 bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record)
 {
     void *arg = L.arg;
     ProbStarts ps = L.ps;
-    // conv kernels: the table, then the three problem starts as scalars
-    void *params[4] = {&arg, &ps.s[0], &ps.s[1], &ps.s[2]};
     const bool prof = (prof_mask_ >> L.family) & 1u;
+    // conv kernels: the table, the three problem starts as scalars, and the
+    // kernel-clock stamp array (profiled launches only); the other kernels
+    // read the leading parameters they declare
+    unsigned long long *stamp = nullptr;
     Pending pe{};
+    pe.stamp_off = -1;
+    if (prof && is_conv_family(L.family) && !capturing_) {
+        const size_t need = 2 * (size_t)L.grid;
+        if (!stamp_buf_) {
+            stamp_cap_ = (size_t)4 << 20;  // 32 MiB of u64 entries
+            if (!check(hip_->hipMalloc((void **)&stamp_buf_, stamp_cap_ * 8), "hipMalloc(stamps)", err) ||
+                !check(hip_->hipMemset(stamp_buf_, 0, stamp_cap_ * 8), "hipMemset(stamps)", err)) {
+                stamp_buf_ = nullptr;
+                return false;
+            }
+        }
+        if (stamp_used_ + need <= stamp_cap_) {
+            stamp = stamp_buf_ + stamp_used_;
+            pe.stamp_off = (long)stamp_used_;
+            pe.grid = L.grid;
+            stamp_used_ += need;
+        }
+    }
+    void *params[5] = {&arg, &ps.s[0], &ps.s[1], &ps.s[2], &stamp};
     if (prof) {
         for (hipEvent_t *e : {&pe.a, &pe.b}) {
             if (!event_pool_.empty()) {
@@ -1754,15 +1785,45 @@ void Engine::collect_events()
         event_pool_.push_back(pe.a);
         event_pool_.push_back(pe.b);
     }
+    // kernel-clock durations: the last workgroup end minus the first start
+    if (stamp_used_ && clock_khz_ > 0) {
+        std::vector<unsigned long long> st(stamp_used_);
+        if (hip_->hipMemcpy(st.data(), stamp_buf_, stamp_used_ * 8, hipMemcpyDeviceToHost) == hipSuccess) {
+            for (auto &pe : pending_) {
+                if (pe.stamp_off < 0) continue;
+                unsigned long long t0 = ~0ull, t1 = 0;
+                for (unsigned b = 0; b < pe.grid; ++b) {
+                    const unsigned long long a = st[pe.stamp_off + 2 * b], e = st[pe.stamp_off + 2 * b + 1];
+                    if (!a) continue;  // a workgroup that wrote nothing
+                    t0 = std::min(t0, a);
+                    t1 = std::max(t1, e);
+                }
+                if (t1 <= t0) continue;
+                prof_clock_n_[pe.family] += 1;
+                prof_clock_ms_[pe.family] += (double)(t1 - t0) / clock_khz_;
+            }
+        }
+        hip_->hipMemset(stamp_buf_, 0, stamp_used_ * 8);
+        stamp_used_ = 0;
+    }
     pending_.clear();
+}
+
+bool Engine::profile_read_clock(int i, uint64_t &launches, double &ms)
+{
+    if (i < 0 || i >= F_COUNT) return false;
+    collect_events();
+    launches = prof_clock_n_[i];
+    ms = prof_clock_ms_[i];
+    return true;
 }
 
 void Engine::profile_reset()
 {
     collect_events();
     for (int f = 0; f < F_COUNT; ++f) {
-        prof_launches_[f] = 0;
-        prof_ms_[f] = prof_flops_[f] = prof_bytes_[f] = 0;
+        prof_launches_[f] = prof_clock_n_[f] = 0;
+        prof_ms_[f] = prof_flops_[f] = prof_bytes_[f] = prof_clock_ms_[f] = 0;
     }
 }
 

@@ -143,6 +143,9 @@ public:
     // (LAMA_PROFILE_SUB), the "gpu totals" line (LAMA_PROFILE); with none of
     // the flags set, the "op" lines.
     void print_stats();
+    // Family i's profiled conv launches timed by their kernel-clock stamps
+    // (first workgroup start to last workgroup end; the conv families only).
+    bool profile_read_clock(int i, uint64_t &launches, double &ms);
     int launch_count(int h, int w);
     // Device bytes of one forward at h x w: the activation arena of that shape
     // (exact, from its layout) and the resident weights (0 before loading).
@@ -245,7 +248,16 @@ private:
         hipEvent_t a, b;
         int family;
         double flops, bytes;
+        long stamp_off;  // first entry of the launch's kernel-clock stamps, or -1
+        unsigned grid;
     };
+    // kernel-clock stamps of profiled conv launches: [2 * workgroup] entries
+    // per launch (start, end), zero where unwritten; allocated on first use
+    unsigned long long *stamp_buf_ = nullptr;
+    size_t stamp_cap_ = 0, stamp_used_ = 0;
+    double clock_khz_ = 0;  // device wall-clock rate
+    uint64_t prof_clock_n_[F_COUNT] = {};
+    double prof_clock_ms_[F_COUNT] = {};
     std::vector<Pending> pending_;
     std::vector<hipEvent_t> event_pool_;
     uint64_t prof_launches_[F_COUNT] = {};

@@ -44,6 +44,8 @@ def lib():
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_print_stats.argtypes = [vp]
+        L.lama_hip_profile_read_clock.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
+                                                  ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_launch_count.argtypes = [vp, ctypes.c_int, ctypes.c_int]
         L.lama_hip_plan_bytes.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
                                           ctypes.POINTER(ctypes.c_uint64), cp, sz]
@@ -219,7 +221,10 @@ class Engine:
         i = 0
         while lib().lama_hip_profile_read(self.ctx, i, name, 64, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl),
                                           ctypes.byref(by)):
-            out[name.value.decode()] = dict(launches=n.value, ms=ms.value, flops=fl.value, bytes=by.value)
+            cn, cms = ctypes.c_uint64(), ctypes.c_double()
+            lib().lama_hip_profile_read_clock(self.ctx, i, ctypes.byref(cn), ctypes.byref(cms))
+            out[name.value.decode()] = dict(launches=n.value, ms=ms.value, flops=fl.value, bytes=by.value,
+                                            clock_launches=cn.value, clock_ms=cms.value)
             i += 1
         return out
 

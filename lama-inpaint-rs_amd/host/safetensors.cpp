@@ -4,6 +4,7 @@
 // "__metadata__": {...}}, then the payloads; offsets are relative to the
 // payload section and are turned into absolute file offsets here so that a
 // verbatim copy of the file addresses each tensor at base + offset.
+#include <cstdint>
 #include "lama_host.h"
 
 #include <fcntl.h>
@@ -79,16 +80,32 @@ struct Json {
         ++p;
         return true;
     }
+    // A JSON integer, parsed within [p, end): the header is not
+    // NUL-terminated, so nothing may read past `end`; values that do not fit
+    // in int64 are an error.
     bool integer(int64_t &v)
     {
         ws();
-        char *e = nullptr;
-        v = strtoll(p, &e, 10);
-        if (e == p) {
+        bool neg = false;
+        if (p < end && (*p == '-' || *p == '+')) {
+            neg = *p == '-';
+            ++p;
+        }
+        if (p >= end || *p < '0' || *p > '9') {
             error = "expected integer";
             return false;
         }
-        p = e;
+        uint64_t u = 0;
+        while (p < end && *p >= '0' && *p <= '9') {
+            const unsigned d = (unsigned)(*p - '0');
+            if (u > (UINT64_MAX - d) / 10 || u * 10 + d > (uint64_t)INT64_MAX + (neg ? 1u : 0u)) {
+                error = "integer out of range";
+                return false;
+            }
+            u = u * 10 + d;
+            ++p;
+        }
+        v = neg ? (int64_t)(0 - u) : (int64_t)u;
         return true;
     }
     bool skip()  // skip any value
@@ -284,9 +301,22 @@ extern "C" int lama_store_open(const char *path, int map, lama_store **out, char
             set_err(err, errlen, "tensor " + r.name + ": data_offsets outside the file");
             return 1;
         }
-        int64_t n = 1;
-        for (auto d : r.shape) n *= d;
-        if ((uint64_t)n * 4 != (uint64_t)(r.offs[1] - r.offs[0])) {
+        // dimensions are non-negative and their product (in bytes) fits the payload
+        uint64_t n = 1;
+        bool shape_ok = true;
+        for (auto d : r.shape) {
+            if (d < 0 || (d > 0 && n > (UINT64_MAX / 4) / (uint64_t)d)) {
+                shape_ok = false;
+                break;
+            }
+            n *= (uint64_t)d;
+        }
+        if (!shape_ok) {
+            lama_store_close(s);
+            set_err(err, errlen, "tensor " + r.name + ": invalid shape");
+            return 1;
+        }
+        if (n * 4 != (uint64_t)(r.offs[1] - r.offs[0])) {
             lama_store_close(s);
             set_err(err, errlen, "tensor " + r.name + ": size does not match its shape");
             return 1;

@@ -112,3 +112,13 @@ def test_null_context_is_an_error_not_a_crash():
     assert L.lama_hip_open(None, err, 256) == 1 and b"null output" in err.value
     L.lama_hip_close.argtypes = [ctypes.c_void_p]
     L.lama_hip_close(None)
+
+
+def test_plan_signature_is_the_reference_describe_of_big_lama():
+    """lama_hip_plan_signature is model::describe (model.rs:260-274) of the
+    plan model::build makes: 29 steps (pad, model.1-4, 18 resblocks, concat,
+    3 upsamples, pad, out conv), 4 + 2 * 18 FFC_BN_ACT calls, 18 resblocks."""
+    L = ctypes.CDLL(os.path.join(LIB, "liblama_hip.so"))
+    L.lama_hip_plan_signature.restype = ctypes.c_char_p
+    steps = 1 + 4 + 18 + 1 + 3 + 1 + 1
+    assert L.lama_hip_plan_signature().decode() == f"{steps} steps, {4 + 2 * 18} FFC_BN_ACT calls, 18 resblocks"

@@ -383,6 +383,32 @@ def test_store_rejects_non_f32_and_bad_offsets(H, tmp_path):
         H.Store(str(tmp_path / "missing.safetensors"))
 
 
+def _raw_st(path, header_bytes, payload=b""):
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(header_bytes)) + header_bytes + payload)
+
+
+def test_store_rejects_malformed_headers(H, tmp_path):
+    """A header whose last token is a number running up to the end of the file
+    (no NUL after it), negative or overflowing dimensions, and integers beyond
+    int64: each is an error with a message, read within the header's bytes."""
+    p = str(tmp_path / "h.safetensors")
+    cases = [
+        b'{"a":{"dtype":"F32","shape":[4],"data_offsets":[0,16',  # truncated inside a number
+        b'{"a":{"dtype":"F32","shape":[-4],"data_offsets":[0,16]}}',
+        b'{"a":{"dtype":"F32","shape":[4611686018427387904,4],"data_offsets":[0,16]}}',
+        b'{"a":{"dtype":"F32","shape":[4],"data_offsets":[0,99999999999999999999999]}}',
+        b'{"a":{"dtype":"F32","shape":[-1,-4],"data_offsets":[0,16]}}',
+    ]
+    for hdr in cases:
+        _raw_st(p, hdr, b"\0" * 16)
+        with pytest.raises(RuntimeError):
+            H.Store(p)
+    # the well-formed version of the same header loads
+    _raw_st(p, b'{"a":{"dtype":"F32","shape":[4],"data_offsets":[0,16]}}', b"\0" * 16)
+    assert len(H.Store(p)) == 1
+
+
 def test_store_reads_metadata_and_orders_by_offset(H, tmp_path):
     p = str(tmp_path / "meta.safetensors")
     a = np.arange(6, dtype=np.float32).reshape(2, 3)
