@@ -89,12 +89,19 @@ def main():
     # both launches of each FFC: A = l2l + l2g (family conv3x3) and B = g2l
     # (family conv3x3g2l), one kernel
     dom_fams = ["conv3x3", "conv3x3g2l"]
-    # the FFC 3x3 convolutions run as Winograd F(2,3) along x unless
-    # LAMA_FFC_WINO=0 selects the direct implicit GEMM; FLOPs are the
-    # convolution's algorithmic count either way (Winograd issues 2/3 of them
-    # as MFMA work)
-    wino = os.environ.get("LAMA_FFC_WINO", "1") != "0"
-    dom_kernel = "lama_conv3x3w" if wino else "lama_conv3x3"
+    # the FFC 3x3 convolutions run as Winograd F(4,3) along x in 32-pixel
+    # blocks (LAMA_FFC_WINO=2: F(2,3); 0: the direct implicit GEMM;
+    # LAMA_W4_TILE=64: F(4,3) in 64-pixel blocks); FLOPs are the convolution's
+    # algorithmic count in every case, of which F(4,3) issues 1/2 and F(2,3)
+    # 2/3 as MFMA work
+    wv = os.environ.get("LAMA_FFC_WINO", "4")
+    wino = 0 if wv == "0" else 2 if wv == "2" else 4
+    w4_wide = os.environ.get("LAMA_W4_TILE", "") == "64"
+    dom_kernel = {0: "lama_conv3x3", 2: "lama_conv3x3w", 4: "lama_conv3x3w4" if w4_wide else "lama_conv3x3w4n"}[wino]
+    issued = {0: 1.0, 2: 2.0 / 3.0, 4: 0.5}[wino]
+    geometry = {0: "512 workgroups of 64 channels x 64 px", 2: "256 workgroups of 64 channels x 2 rows x 64 px",
+                4: "256 workgroups of 64 channels x " + ("2 rows x 64 px" if w4_wide else "4 rows x 32 px")}[wino]
+    method = {0: "direct implicit GEMM", 2: "Winograd F(2,3) along x", 4: "Winograd F(4,3) along x"}[wino]
     eng.profile_reset()
     eng.synchronize()
     t0 = time.perf_counter()
@@ -190,7 +197,7 @@ def main():
     # executed MFMA work: the Winograd FFC families issue 2/3 of their
     # algorithmic (direct-convolution) FLOPs
     wino_fams = ("conv3x3", "conv3x3g2l")
-    conv_flops_exec = conv_flops - (sum(fam[f]["flops"] for f in wino_fams) / 3 / 3.0 if wino else 0.0)
+    conv_flops_exec = conv_flops - sum(fam[f]["flops"] for f in wino_fams) / 3 * (1.0 - issued)
     fft_ms = sum(fam[f]["ms"] for f in ("rfft2", "irfft2")) / 3
     fft_bytes = sum(fam[f]["bytes"] for f in ("rfft2", "irfft2")) / 3
     # event time per family; a launch issued after a cross-stream wait (every
@@ -249,9 +256,7 @@ def main():
                                   256: " (BASELINE configs[0] shape)"}.get(S, ""),
                    "h": S, "w": S, "mask_coverage": round(coverage, 4), "launches_per_pass": eng.launch_count(S, S)},
         "roofline": {"bound": "mfma",
-                     "kernel": (dom_kernel + (" (FFC 3x3 convolutions as Winograd F(2,3) along x, 256 workgroups of "
-                                              "64 channels x 2 rows x 64 px" if wino else
-                                              " (FFC 3x3 implicit GEMMs, 512 workgroups of 64 channels x 64 px")
+                     "kernel": (dom_kernel + f" (FFC 3x3 convolutions as {method}, {geometry}"
                                 + "; timed: both launches of every FFC of the sampled passes, A = l2l + l2g "
                                   "(4.83 GFLOP) and B = g2l (3.62 GFLOP), each from its first workgroup's start "
                                   "to its last workgroup's end on the device clock; they overlap each other and "
@@ -266,7 +271,7 @@ def main():
                      "launch_ms_a": round(clock_a, 5) if clock_a is not None else None,
                      "launch_ms_b": round(clock_b, 5) if clock_b is not None else None,
                      "launch_ms_a_events": round(launch_ms_events_a, 5),
-                     "mfma_issued_frac": round(achieved * (2.0 / 3.0 if wino else 1.0) / PEAK_FP32_MFMA, 4)},
+                     "mfma_issued_frac": round(achieved * issued / PEAK_FP32_MFMA, 4)},
         # all conv families' algorithmic (direct-convolution) FLOPs over the
         # pass's wall time, and the MFMA work actually executed (Winograd
         # families at 2/3) over the same time

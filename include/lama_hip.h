@@ -151,6 +151,20 @@ int lama_hip_profile_read(lama_hip_ctx *ctx, int i, char *name, size_t namelen, 
  * dispatch latency the event interval includes.  Conv families only (0-4, 9,
  * 10); returns 1 for a valid i, 0 past the end. */
 int lama_hip_profile_read_clock(lama_hip_ctx *ctx, int i, uint64_t *launches, double *ms);
+/* A launch's place on the device clock (lama_hip_timeline_read). */
+typedef struct lama_launch_time {
+    int32_t family;   /* kernel family, as lama_hip_profile numbers them */
+    int32_t stream;   /* 0 the pass's stream, 1 the SpectralTransform stream, 2 the g2l stream */
+    double start_us;  /* first workgroup start, from the first recorded launch's start (-1: none) */
+    double end_us;    /* last workgroup end */
+} lama_launch_time;
+/* Timeline of launches without a tracer (whose interception changes how the
+ * three streams overlap): while enabled, every launch's workgroups store
+ * kernel-clock stamps (no events, no synchronisation).  enable != 0 starts a
+ * new recording, 0 stops.  lama_hip_timeline_read waits for the device and
+ * returns up to `max` launches in issue order (the count, or -1 on error). */
+int lama_hip_timeline(lama_hip_ctx *ctx, int enable);
+int lama_hip_timeline_read(lama_hip_ctx *ctx, lama_launch_time *out, int max);
 /* print_op_stats / print_sub_stats / print_stats (cuda.rs:1738-1806): the
  * per-family event timings to stderr as "op" lines (LAMA_PROFILE_OPS), "sub"
  * lines (LAMA_PROFILE_SUB) and a "gpu totals" line (LAMA_PROFILE); the "op"

@@ -12,6 +12,10 @@
 #define LAMA_PW_KC 16
 #endif
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
+// pointwise convolutions: all M blocks of a pixel strip on one XCD
+#ifndef LAMA_PW_XCD
+#define LAMA_PW_XCD 1
+#endif
 // Bytes of the no-allocation entry point's device array: the activation arena
 // and descriptors of one forward of up to 512 x 512 (177.2 MiB at 512 x 512).
 #define LAMA_SCRATCH_BYTES (192u << 20)
@@ -55,6 +59,10 @@ static inline constexpr int lama_convt_kc(int phase)
 #ifndef LAMA_WINO_KC
 #define LAMA_WINO_KC 4
 #endif
+// Floats per output channel and K chunk of the F(4,3) Winograd weights: the
+// 6 positions x 3 kernel rows x 4 channels, padded to whole float4 slots of
+// one workgroup's staging round
+#define LAMA_WINO4_WKP 80
 // output tile of the 7x7 tail kernel (rows x columns) and the adjacent
 // pixels each of its threads computes
 #ifndef LAMA_TAIL_ROWS
@@ -96,6 +104,29 @@ __device__ __forceinline__ LAMA_GLOBAL T *gp(T *p)
     return (LAMA_GLOBAL T *)p;
 }
 
+// Kernel-clock stamps (profiling): every kernel's fifth parameter is an
+// array that, when non-null, receives each workgroup's start and end on the
+// constant-rate device clock (s_memrealtime), stored by thread 0 at
+// [2 * blockIdx.x] and [2 * blockIdx.x + 1] with ordinary vector stores.  The
+// kernels with fewer leading parameters take unused ints in their place, so
+// the engine passes one parameter layout to every kernel.
+#define LAMA_STAMP_PARAMS int, int, int, unsigned long long *__restrict__ stamp
+struct StampScope {
+    unsigned long long *p, t0;
+    __device__ __forceinline__ explicit StampScope(unsigned long long *p_)
+        : p(p_), t0(p_ ? __builtin_amdgcn_s_memrealtime() : 0ull)
+    {
+    }
+    __device__ __forceinline__ ~StampScope()
+    {
+        if (p && threadIdx.x == 0) {
+            p[2 * blockIdx.x] = t0;
+            p[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+};
+#define LAMA_STAMP_SCOPE const StampScope stamp_scope_(stamp)
+
 // PyTorch 'reflect' index for |overshoot| < n (one reflection), clamped into
 // [0, n).  Exact for every input position a stored output reads (pad < n,
 // or n == 1); positions read only by out-of-range tile pixels are clamped.
@@ -132,7 +163,7 @@ struct alignas(16) ProbStarts {
 // One output problem: out[co][oy'][ox'] for co < M, (oy, ox) on the OH x OW
 // GEMM grid, stored at oy' = oy*oy_mul + oy_off, ox' = ox*ox_mul + ox_off
 // (the conv-transpose phases interleave four grids into one plane).
-// Epilogue: v = acc (+bias) (+addend) -> *scale + shift -> ReLU -> (+res)
+// Epilogue: v = acc (+bias) (+addends) -> *scale + shift -> ReLU -> (+res)
 // -> store; `addend` and `res` are indexed like `out`.
 struct ConvProblem {
     ConvSeg s0, s1;  // s1.nchunk == 0 when absent; s1 is always 1x1
@@ -145,7 +176,15 @@ struct ConvProblem {
     long out_cstride;  // floats between output channel planes
     int outW;          // output row stride
     int oy_mul, oy_off, ox_mul, ox_off;
-    int pad_;
+    // K split (the F(4,3) kernels): the problem's nblocks are ksplit slices
+    // of mblocks * tiles_x * tiles_y blocks; slice ks covers input channels
+    // [ks * kchunks * KC, +kchunks * KC) and stores its raw partial at
+    // out + ks * out_kstride.  ksplit <= 1: no split.
+    int ksplit, kchunks;
+    long out_kstride;
+    // the epilogue adds naddend planes, addend + i * addend_kstride
+    int naddend;
+    long addend_kstride;
 };
 
 // FFT length descriptor.  Twiddles tw[k] = exp(-2*pi*i*k/n) in f32 (computed
@@ -184,8 +223,10 @@ struct FftArgs {
 #define LAMA_G2L_RANGES 4  // K ranges of the FFC g2l GEMM (384 input channels)
 #endif
 #define LAMA_FIN_PARTS (1 + LAMA_G2L_RANGES)  // K partials of the FFC local GEMM: l2l, then g2l's K ranges
+#define LAMA_KSPLIT_MAX 4                      // the F(4,3) kernels' K split of the FFC GEMMs
+#define LAMA_FIN_MAX (LAMA_FIN_PARTS * LAMA_KSPLIT_MAX)
 struct FinalizeArgs {
-    const float *part[LAMA_FIN_PARTS];
+    const float *part[LAMA_FIN_MAX];
     int nparts, C;
     long plane;
     const float *scale, *shift, *res;

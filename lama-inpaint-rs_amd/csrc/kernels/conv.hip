@@ -505,12 +505,21 @@ __device__ __forceinline__ void epilogue_prefetch(EpiPre &e, const ConvProblem &
     const int p = wn * 32 + j;
     const int oy = min(oy0 + p / TC, P.OH - 1), ox = min(ox0 + p % TC, P.OW - 1);
     const long pix = (long)(oy * P.oy_mul + P.oy_off) * P.outW + (long)ox * P.ox_mul + P.ox_off;
+    long o[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int co = min(m0 + wm * 32 + 8 * (r >> 2) + 4 * g + (r & 3), P.M - 1);
-        const long o = (long)co * P.out_cstride + pix;
-        e.add[r] = P.addend ? gp(P.addend)[o] : 0.f;
-        e.res[r] = P.res ? gp(P.res)[o] : 0.f;
+        o[r] = (long)co * P.out_cstride + pix;
+        e.res[r] = P.res ? gp(P.res)[o[r]] : 0.f;
+        e.add[r] = 0.f;
+    }
+    // the addend's K slices, summed in order (uniform guards: one slice's 16
+    // loads in flight at a time, 16 registers beyond the sums)
+#pragma unroll
+    for (int i = 0; i < LAMA_KSPLIT_MAX; ++i) {
+        if (i >= P.naddend) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e.add[r] += gp(P.addend)[o[r] + i * P.addend_kstride];
     }
 }
 
@@ -547,8 +556,8 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, con
         if (P.bias) x += epl[cl];
         if (PREFETCH)
             x += e.add[r];
-        else if (P.addend)
-            x += gp(P.addend)[o];
+        else
+            for (int i = 0; i < P.naddend; ++i) x += gp(P.addend)[o + i * P.addend_kstride];
         if (P.scale) x = x * epl[64 + cl] + epl[128 + cl];
         if (P.relu) x = fmaxf(x, 0.f);
         if (PREFETCH)
@@ -606,7 +615,19 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
 template <class C, bool PREFETCH, int D>
 __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds, float *epl)
 {
-    const int mb = b % P.mblocks, t = b / P.mblocks;
+    int mb = b % P.mblocks, t = b / P.mblocks;
+#if LAMA_PW_XCD
+    // XCD-aware order: workgroups are dealt to the eight XCDs round-robin
+    // (XCD = blockIdx.x mod 8, here b, the launch's only problem), and each
+    // XCD has an L2 of its own; giving all M blocks of pixel strip t to XCD
+    // t mod 8 makes each strip travel from HBM into one L2 once, instead of
+    // once per M block
+    if (P.tiles_x % 8 == 0) {
+        const int j = b >> 3;
+        mb = j % P.mblocks;
+        t = (j / P.mblocks) * 8 + (b & 7);
+    }
+#endif
     const int m0 = mb * 64, ox0 = t * C::NPX;
     const int wn = (threadIdx.x >> 6) & 1;
     const float ep = epi_param_load(P, m0);

@@ -8,13 +8,14 @@
 
 #include "common.h"
 
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const FinalizeArgs *__restrict__ args)
+// NP partials, a compile-time count: every load is issued before any
+// arithmetic, and the partials are summed in order
+template <int NP>
+__device__ __forceinline__ void finalize_body(const FinalizeArgs &A)
 {
-    const FinalizeArgs &A = *args;
     const long n = (long)A.C * A.plane;
     const long i = ((long)blockIdx.x * LAMA_NT + threadIdx.x) * 4;
     if (i >= n) return;
-    // every load of the four elements is issued before any arithmetic or store
     long idx[4];
     int ch[4];
 #pragma unroll
@@ -22,11 +23,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
         idx[e] = min(i + e, n - 1);
         ch[e] = (int)(idx[e] / A.plane);
     }
-    float part[LAMA_FIN_PARTS][4], sc[4], sh[4], rs[4];
-    const int np = A.nparts;
+    float part[NP][4], sc[4], sh[4], rs[4];
 #pragma unroll
-    for (int q = 0; q < LAMA_FIN_PARTS; ++q) {
-        const LAMA_GLOBAL float *pq = gp(A.part[min(q, np - 1)]);
+    for (int q = 0; q < NP; ++q) {
+        const LAMA_GLOBAL float *pq = gp(A.part[q]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[q][e] = pq[idx[e]];
     }
@@ -44,8 +44,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
     for (int e = 0; e < 4; ++e) {
         float v = 0.f;
 #pragma unroll
-        for (int q = 0; q < LAMA_FIN_PARTS; ++q)
-            if (q < np) v += part[q][e];
+        for (int q = 0; q < NP; ++q) v += part[q][e];
         float x = fmaxf(v * sc[e] + sh[e], 0.f);
         if (A.res) x += rs[e];
         out[e] = x;
@@ -59,14 +58,29 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_finalize(const Finali
     }
 }
 
+// The FFC local branch's finish over 5, 10 or 20 partials (K split 1, 2, 4),
+// one kernel each so that each holds only its own partials in registers.
+#define LAMA_FINALIZE(NAME, NP)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const FinalizeArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
+    {                                                                                                            \
+        LAMA_STAMP_SCOPE;                                                                                        \
+        finalize_body<NP>(*args);                                                                                \
+    }
+LAMA_FINALIZE(lama_finalize, LAMA_FIN_PARTS)
+LAMA_FINALIZE(lama_finalize10, 2 * LAMA_FIN_PARTS)
+LAMA_FINALIZE(lama_finalize20, 4 * LAMA_FIN_PARTS)
+#undef LAMA_FINALIZE
+
 // build_input (main.rs:175-196) on the device: the 8-bit h x w image (HWC
 // RGB) and mask to the network input [4][H][W], padded bottom/right by
 // reflection (image.rs:159-169).  Per pixel: m = (mask > 0), channel c =
 // (rgb_c / 255) * (1 - m) with a correctly rounded f32 division and a
 // separately rounded product, as the reference computes it; plane 3 = m.
 // One thread per output pixel: byte reads, four coalesced plane stores.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_build_input(const InputArgs *__restrict__ args, int h, int w)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_build_input(const InputArgs *__restrict__ args, int h, int w, int,
+                                                                unsigned long long *__restrict__ stamp)
 {
+    LAMA_STAMP_SCOPE;
     const InputArgs &A = *args;
     const long plane = (long)A.H * A.W;
     const long i = (long)blockIdx.x * LAMA_NT + threadIdx.x;

@@ -251,9 +251,10 @@ __device__ __forceinline__ void put_twiddles(const FftArgs &A, const TwFetch &f,
 }  // namespace
 
 // One block per channel: real [C][H][W] -> stacked [2C][H][W/2+1], ortho.
-extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
     side_priority();
+    LAMA_STAMP_SCOPE;
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
@@ -329,9 +330,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
 
 // One block per channel: stacked [2C][H][W/2+1] -> real [C][H][W], ortho,
 // plus feat: out = feat + irfft2(in).
-extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
     side_priority();
+    LAMA_STAMP_SCOPE;
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int c = blockIdx.x, H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2;
@@ -447,9 +449,10 @@ __device__ __forceinline__ void load_table(const float *tw, int n, float2 *dst)
 }  // namespace
 
 // real [C][H][W] -> tmp: x transforms of row pairs, split into half spectra.
-extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
     side_priority();
+    LAMA_STAMP_SCOPE;
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2, PB = A.rows_per_block;
@@ -477,9 +480,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const 
 }
 
 // tmp -> stacked [2C][H][Wh]: y transforms of the kept columns, ortho scale.
-extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
     side_priority();
+    LAMA_STAMP_SCOPE;
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, Wh = A.Wh, CB = A.cols_per_block;
@@ -504,9 +508,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const 
 }
 
 // stacked [2C][H][Wh] -> tmp: inverse y transforms of the stored columns.
-extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
     side_priority();
+    LAMA_STAMP_SCOPE;
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, Wh = A.Wh, CB = A.cols_per_block;
@@ -530,9 +535,10 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const
 
 // tmp -> real [C][H][W]: complex-to-real x transforms of row pairs, ortho
 // scale, plus feat.
-extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const FftArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
     side_priority();
+    LAMA_STAMP_SCOPE;
     extern __shared__ float2 sm[];
     const FftArgs &A = *args;
     const int H = A.H, W = A.W, Wh = A.Wh, HP = (H + 1) / 2, PB = A.rows_per_block;
@@ -777,15 +783,17 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
 }  // namespace
 
 #define LAMA_FFT_CT(N)                                                                                          \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_##N(const FftArgs *__restrict__ args)  \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
     {                                                                                                           \
         side_priority();                                                                                        \
+        LAMA_STAMP_SCOPE;                                                                                       \
         extern __shared__ float2 sm[];                                                                          \
         rfft2_ct<N>(*args, sm);                                                                                 \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_##N(const FftArgs *__restrict__ args) \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
     {                                                                                                           \
         side_priority();                                                                                        \
+        LAMA_STAMP_SCOPE;                                                                                       \
         extern __shared__ float2 sm[];                                                                          \
         irfft2_ct<N>(*args, sm);                                                                                \
     }
@@ -975,15 +983,17 @@ __device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
 }  // namespace
 
 #define LAMA_FFT_SPLIT_CT(N)                                                                                         \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows_##N(const FftArgs *__restrict__ args)  \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
     {                                                                                                                \
         side_priority();                                                                                             \
+        LAMA_STAMP_SCOPE;                                                                                            \
         extern __shared__ float2 sm[];                                                                               \
         rfft2_rows_ct<N>(*args, sm);                                                                                 \
     }                                                                                                                \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols_##N(const FftArgs *__restrict__ args)  \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
     {                                                                                                                \
         side_priority();                                                                                             \
+        LAMA_STAMP_SCOPE;                                                                                            \
         extern __shared__ float2 sm[];                                                                               \
         using S = SplitCt<N>;                                                                                        \
         const int c = blockIdx.x / S::CCH, ch = blockIdx.x % S::CCH;                                                 \
@@ -992,9 +1002,10 @@ __device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
         else                                                                                                         \
             rfft2_cols_ct<N, 1>(*args, sm, c, ch * S::CB);                                                           \
     }                                                                                                                \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols_##N(const FftArgs *__restrict__ args) \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
     {                                                                                                                \
         side_priority();                                                                                             \
+        LAMA_STAMP_SCOPE;                                                                                            \
         extern __shared__ float2 sm[];                                                                               \
         using S = SplitCt<N>;                                                                                        \
         const int c = blockIdx.x / S::CCH, ch = blockIdx.x % S::CCH;                                                 \
@@ -1003,9 +1014,10 @@ __device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
         else                                                                                                         \
             irfft2_cols_ct<N, 1>(*args, sm, c, ch * S::CB);                                                          \
     }                                                                                                                \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows_##N(const FftArgs *__restrict__ args) \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
     {                                                                                                                \
         side_priority();                                                                                             \
+        LAMA_STAMP_SCOPE;                                                                                            \
         extern __shared__ float2 sm[];                                                                               \
         irfft2_rows_ct<N>(*args, sm);                                                                                \
     }

@@ -157,13 +157,16 @@ __device__ __forceinline__ void tail_body(const TailArgs *__restrict__ args, int
     }
 }
 
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail(const TailArgs *__restrict__ args, LAMA_STAMP_PARAMS)
 {
+    LAMA_STAMP_SCOPE;
     tail_body<false>(args, 0, 0);
 }
 
 // The tail with the 8-bit composite of the h x w crop fused in.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail_u8(const TailArgs *__restrict__ args, int h, int w)
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_tail_u8(const TailArgs *__restrict__ args, int h, int w, int,
+                                                            unsigned long long *__restrict__ stamp)
 {
+    LAMA_STAMP_SCOPE;
     tail_body<true>(args, h, w);
 }

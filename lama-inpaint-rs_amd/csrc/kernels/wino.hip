@@ -211,7 +211,7 @@ __device__ __forceinline__ void wino_tile(const ConvProblem &P, int b, float *ld
             if (e == 1 && !second) break;
             float x = y[e];
             if (P.bias) x += epl[cl];
-            if (P.addend) x += gp(P.addend)[o + e];
+            for (int i = 0; i < P.naddend; ++i) x += gp(P.addend)[o + e + i * P.addend_kstride];
             if (P.scale) x = x * epl[64 + cl] + epl[128 + cl];
             if (P.relu) x = fmaxf(x, 0.f);
             if (P.res) x += gp(P.res)[o + e];

@@ -1,0 +1,335 @@
+// FFC 3x3 convolutions (stride 1, reflect pad 1) as a one-dimensional
+// Winograd F(4,3) along x, on FP32 MFMA.
+//
+// Each output quad (x .. x+3) of a row is computed from the six input columns
+// d0..d5 = in[x-1 .. x+4] of each kernel row ky, with the interpolation points
+// 0, 1, -1, 2, -2 and infinity (Lavin & Gray, "Fast Algorithms for
+// Convolutional Neural Networks", 2016):
+//     V = B^T d   (input transform, while the rows are staged in LDS)
+//         V0 = 4 d0 - 5 d2 + d4          V3 = -2 d1 - d2 + 2 d3 + d4
+//         V1 = -4 (d1 + d2) + d3 + d4    V4 = 2 d1 - d2 - 2 d3 + d4
+//         V2 = 4 (d1 - d2) - d3 + d4     V5 = 4 d1 - 5 d3 + d5
+//     U = G g     (weight transform, on the host in f64)
+//         U = (g0/4, -(g0+g1+g2)/6, -(g0-g1+g2)/6, g0/24+g1/12+g2/6, g0/24-g1/12+g2/6, g2)
+//     m_u = sum over (ci, ky) of U_u * V_u                   (six GEMMs)
+//     out = A^T m (output transform, in the epilogue)
+//         out0 = m0 + m1 + m2 + m3 + m4      out2 = m1 + m2 + 4 (m3 + m4)
+//         out1 = m1 - m2 + 2 (m3 - m4)       out3 = m1 - m2 + 8 (m3 - m4) + m5
+// 6 multiplications per 4 outputs and kernel row instead of the 12 of the
+// direct sum: half the direct convolution's MFMA work, 3/4 of F(2,3)'s.
+//
+// A workgroup computes 64 output channels x RW rows x 4*NTR pixels (32
+// Winograd tiles: RW rows of NTR tiles, NTR = 16 or 8, so 64- or 32-pixel
+// wide blocks).  Wave (wm, wu) owns channels wm*32 .. +32 and the positions
+// u = 3*wu .. 3*wu+2 as three 32 x 32 accumulators of v_mfma_f32_32x32x2f32:
+// GEMM rows are output channels, GEMM columns the block's 32 tiles, K =
+// (ci, ky).  K is walked in chunks of LAMA_WINO_KC = 4 input channels; per
+// chunk the block stages in LDS the transformed weights [64 co][u][ky][4]
+// (rows padded to 80 floats) and the transformed input [rows][u][tiles][4
+// (+2 pad)], with the two-stage pipeline of the F(2,3) kernel and an even
+// chunk count.  In the epilogue the two position halves of each channel half
+// swap partial sums of the output transform through LDS, so that each wave
+// finishes two of the four pixels of every tile.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace {
+
+template <int NTR_>
+struct W4Cfg {
+    static constexpr int KC = LAMA_WINO_KC;      // input channels per chunk
+    static constexpr int NU = 6, KY = 3;         // Winograd positions, kernel rows
+    static constexpr int NUW = NU / 2;           // positions per wave
+    static constexpr int NTR = NTR_;             // tiles per output row
+    static constexpr int RW = 32 / NTR;          // output rows per block
+    static constexpr int TR = RW, TC = 4 * NTR;  // output rows x pixels per block
+    static constexpr int IR = TR + 2;            // input rows per block
+    static constexpr int WK = NU * KY * KC;      // weights per output channel and chunk (72)
+    static constexpr int WKP = LAMA_WINO4_WKP;   // packed (padded) weights per channel and chunk
+    static constexpr int WSTR = WKP + 4;         // LDS row stride (= 4 mod 8)
+    static constexpr int H = KC / 2;             // channels per lane half and MFMA K slot
+    static constexpr int KCP = KC + 2;           // LDS floats per (row, u, tile)
+    static constexpr int W_LDS = 64 * WSTR;
+    static constexpr int NITEM = KC * IR * NTR;  // (ci, row, tile) input items per chunk
+    static constexpr int VITER = (NITEM + LAMA_NT - 1) / LAMA_NT;
+    static constexpr int V_LDS = IR * NU * NTR * KCP + NU * 64;  // + a dummy tail for items past NITEM
+    static constexpr int LDS = W_LDS + V_LDS;    // floats per stage
+    static constexpr int WITER = 64 * WKP / 4 / LAMA_NT;  // weight float4s per thread
+    // epilogue exchange: per channel half, two pixels x 16 registers x 64 lanes from each position half
+    static constexpr int X_LDS = 2 * 2 * 2 * 16 * 64;
+    static_assert(WITER * LAMA_NT * 4 == 64 * WKP, "whole weight float4s");
+    static_assert(WKP >= WK && WKP % 16 == 0, "padded weight rows");
+    static_assert(NTR * RW == 32, "32 tiles per block");
+    static_assert(X_LDS <= 2 * LDS, "the exchange fits in the staging buffers");
+    static_assert(KC == 4, "two channels per lane half");
+};
+
+template <class C>
+struct W4Slots {
+    int wg[C::WITER], wl[C::WITER];  // weights: float offset in the row, LDS offset
+    unsigned po[C::VITER][6];        // input: byte offsets of d0..d5 from the chunk's first plane
+    int vl[C::VITER];                // input: LDS offset of V_0 (V_u at + u * NTR * KCP)
+};
+
+template <class C>
+struct W4Stage {
+    float w[4 * C::WITER];
+    float d[C::VITER][6];
+};
+
+template <class C>
+__device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int m0, int M, int oy0, int ox0)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it) {
+        const int idx = tid + it * LAMA_NT, row = idx / (C::WKP / 4), c4 = idx % (C::WKP / 4);
+        sl.wl[it] = row * C::WSTR + c4 * 4;
+        sl.wg[it] = min(m0 + row, M - 1) * sg.wrow + c4 * 4;
+    }
+    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+#pragma unroll
+    for (int it = 0; it < C::VITER; ++it) {
+        // items past NITEM (a partial last round) read clamped, valid
+        // addresses and land in the dummy tail of the V region
+        const int idx = tid + it * LAMA_NT, q = min(idx, C::NITEM - 1);
+        const int t = q % C::NTR, r = (q / C::NTR) % C::IR, ci = q / (C::NTR * C::IR);
+        const int iy = reflect1(oy0 - 1 + r, sg.IH);
+#pragma unroll
+        for (int c = 0; c < 6; ++c) {
+            const int ix = reflect1(ox0 + 4 * t - 1 + c, sg.IW);
+            sl.po[it][c] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + ix));
+        }
+        sl.vl[it] = idx < C::NITEM ? (r * C::NU * C::NTR + t) * C::KCP + ci
+                                   : C::IR * C::NU * C::NTR * C::KCP + (idx - C::NITEM) % 64;
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void w4_load(W4Stage<C> &st, const W4Slots<C> &sl, const ConvSeg &sg, int ck)
+{
+    const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::WKP;
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it) {
+        const float4 v = *at_byte<float4>(wt, 4u * (unsigned)sl.wg[it]);
+        st.w[4 * it] = v.x;
+        st.w[4 * it + 1] = v.y;
+        st.w[4 * it + 2] = v.z;
+        st.w[4 * it + 3] = v.w;
+    }
+    // channels past C (zero weights) read the last float of the source; the
+    // zero chunk that pads the count to even reads within channel C - 1
+    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const int c0 = min(ck * C::KC, sg.C - 1);
+    const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
+#pragma unroll
+    for (int it = 0; it < C::VITER; ++it)
+#pragma unroll
+        for (int c = 0; c < 6; ++c) st.d[it][c] = *at_byte<float>(src, min(sl.po[it][c], last));
+}
+
+template <class C>
+__device__ __forceinline__ void w4_store(const W4Stage<C> &st, const W4Slots<C> &sl, float *lds)
+{
+#pragma unroll
+    for (int it = 0; it < C::WITER; ++it)
+        *reinterpret_cast<float4 *>(lds + sl.wl[it]) =
+            make_float4(st.w[4 * it], st.w[4 * it + 1], st.w[4 * it + 2], st.w[4 * it + 3]);
+    float *vl = lds + C::W_LDS;
+    constexpr int S = C::NTR * C::KCP;  // LDS distance between positions
+#pragma unroll
+    for (int it = 0; it < C::VITER; ++it) {
+        const float d0 = st.d[it][0], d1 = st.d[it][1], d2 = st.d[it][2], d3 = st.d[it][3], d4 = st.d[it][4],
+                    d5 = st.d[it][5];
+        const int o = sl.vl[it];
+        // dummy items (o in the tail) write six words within the tail's 6 * 64
+        const int st_ = o >= C::IR * C::NU * C::NTR * C::KCP ? 64 : S;
+        vl[o] = 4.f * d0 - 5.f * d2 + d4;
+        vl[o + st_] = d3 + d4 - 4.f * (d1 + d2);
+        vl[o + 2 * st_] = 4.f * (d1 - d2) - d3 + d4;
+        vl[o + 3 * st_] = 2.f * (d3 - d1) - d2 + d4;
+        vl[o + 4 * st_] = 2.f * (d1 - d3) - d2 + d4;
+        vl[o + 5 * st_] = 4.f * d1 - 5.f * d3 + d5;
+    }
+}
+
+// MFMAs of one chunk for wave (wm, wu): for each (ky, u) of the wave's three
+// positions, lane half g reads its two channels of the weights and of the
+// input (one 8-byte read each) and feeds one to each of two MFMAs as the
+// MFMA's K slot g; the reads of the next (ky, u) are issued first.
+template <class C>
+__device__ __forceinline__ void w4_compute(f32x16 (&acc)[C::NUW], const float *lds)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wu = wave & 1, g = lane >> 5, j = lane & 31;
+    const int r = j / C::NTR, t = j % C::NTR;  // the MFMA column's output row and tile within the block
+    const float *wrow = lds + (wm * 32 + j) * C::WSTR + C::H * g;
+    const float *vrow = lds + C::W_LDS + t * C::KCP + C::H * g;
+    float a[2][C::H], b[2][C::H];
+    auto rd = [&](int s, int buf) {
+        const int ky = s / C::NUW, u = C::NUW * wu + s % C::NUW;
+        lds_vec<C::H>(a[buf], wrow + (u * C::KY + ky) * C::KC);
+        lds_vec<C::H>(b[buf], vrow + ((r + ky) * C::NU + u) * C::NTR * C::KCP);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int s = 0; s < C::KY * C::NUW; ++s) {
+        const int cur = s & 1;
+        if (s + 1 < C::KY * C::NUW) rd(s + 1, cur ^ 1);
+        const int q = s % C::NUW;
+#pragma unroll
+        for (int c = 0; c < C::H; ++c)
+            acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][c], b[cur][c], acc[q], 0, 0, 0);
+    }
+}
+
+// One 64-channel x RW-row x 4*NTR-pixel block of problem P (s1 absent).
+template <class C>
+__device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds, float *epl)
+{
+    // K slice of a split problem: the blocks of slice ks follow those of ks - 1
+    int ks = 0;
+    if (P.ksplit > 1) {
+        const int per = P.mblocks * P.tiles_x * P.tiles_y;
+        ks = b / per;
+        b -= ks * per;
+    }
+    const int mb = b % P.mblocks, tt = b / P.mblocks;
+    const int tx = tt % P.tiles_x, ty = tt / P.tiles_x;
+    const int m0 = mb * 64, oy0 = ty * C::TR, ox0 = tx * C::TC;
+    const float ep = epi_param_load(P, m0);
+    f32x16 acc[C::NUW];
+#pragma unroll
+    for (int q = 0; q < C::NUW; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
+    ConvSeg sg = P.s0;  // held in registers across the barriers
+    if (P.ksplit > 1) {
+        const int c0 = ks * P.kchunks * C::KC;
+        sg.src += (long)c0 * sg.IH * sg.IW;
+        sg.wt += (long)ks * P.kchunks * C::WKP;
+        sg.C -= c0;
+        sg.nchunk = P.kchunks;
+    }
+    const int n = sg.nchunk, last = n - 1;
+    W4Slots<C> sl;
+    w4_slots<C>(sl, sg, m0, P.M, oy0, ox0);
+    float *l0 = lds, *l1 = lds + C::LDS;
+    W4Stage<C> r0, r1;
+    w4_load<C>(r0, sl, sg, 0);
+    w4_load<C>(r1, sl, sg, min(1, last));
+    w4_store<C>(r0, sl, l0);
+    w4_load<C>(r0, sl, sg, min(2, last));
+    __syncthreads();
+    // n is even (the weights are packed in pairs of chunks): one loop exit
+    for (int ck = 0; ck < n; ck += 2) {
+        w4_compute<C>(acc, l0);
+        w4_store<C>(r1, sl, l1);
+        w4_load<C>(r1, sl, sg, min(ck + 3, last));
+        __syncthreads();
+        w4_compute<C>(acc, l1);
+        w4_store<C>(r0, sl, l0);
+        w4_load<C>(r0, sl, sg, min(ck + 4, last));
+        __syncthreads();
+    }
+    // output transform: wave wu = 0 holds m0..m2, wu = 1 holds m3..m5.
+    // Partials  p = (m0 + m1 + m2, m1 - m2, m1 + m2, m1 - m2)   (wu = 0)
+    //           q = (m3 + m4, 2 (m3 - m4), 4 (m3 + m4), 8 (m3 - m4) + m5)   (wu = 1)
+    // and out_i = p_i + q_i; wave wu finishes pixels 2 wu and 2 wu + 1 of each
+    // tile, after taking the other half's two partials through LDS.
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wu = wave & 1, g = lane >> 5, j = lane & 31;
+    float mine[2][16], give[2][16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float a = acc[0][r], b2 = acc[1][r], c = acc[2][r];
+        float v[4];
+        if (wu == 0) {
+            v[0] = a + b2 + c;
+            v[1] = b2 - c;
+            v[2] = b2 + c;
+            v[3] = b2 - c;
+        } else {
+            v[0] = a + b2;
+            v[1] = 2.f * (a - b2);
+            v[2] = 4.f * (a + b2);
+            v[3] = 8.f * (a - b2) + c;
+        }
+        mine[0][r] = v[2 * wu];
+        mine[1][r] = v[2 * wu + 1];
+        give[0][r] = v[2 - 2 * wu];
+        give[1][r] = v[3 - 2 * wu];
+    }
+    // X[wm][from wu][pixel e][r][lane]: the staging buffers are free once
+    // every wave has left the K loop
+    float *xl = lds;
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xl[(((wm * 2 + wu) * 2 + e) * 16 + r) * 64 + lane] = give[e][r];
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mine[e][r] += xl[(((wm * 2 + (wu ^ 1)) * 2 + e) * 16 + r) * 64 + lane];
+    // the fused epilogue of the direct kernels on pixels 4t + 2wu + e
+    const int oy = oy0 + j / C::NTR, ox = ox0 + 4 * (j % C::NTR) + 2 * wu;
+    if (oy >= P.OH || ox >= P.OW) return;
+    const bool second = ox + 1 < P.OW;
+    const long pix = (long)oy * P.outW + ox;
+    LAMA_GLOBAL float *out = gp(P.out) + (long)ks * P.out_kstride;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int cl = wm * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m0 + cl >= P.M) continue;
+        const long o = (long)(m0 + cl) * P.out_cstride + pix;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            if (e == 1 && !second) break;
+            float x = mine[e][r];
+            if (P.bias) x += epl[cl];
+            for (int i = 0; i < P.naddend; ++i) x += gp(P.addend)[o + e + i * P.addend_kstride];
+            if (P.scale) x = x * epl[64 + cl] + epl[128 + cl];
+            if (P.relu) x = fmaxf(x, 0.f);
+            if (P.res) x += gp(P.res)[o + e];
+            out[o + e] = x;
+        }
+    }
+}
+
+}  // namespace
+
+// FFC spatial convolutions (3x3, stride 1, reflect pad 1) as Winograd F(4,3)
+// along x, in 64-pixel (lama_conv3x3w4) or 32-pixel (lama_conv3x3w4n) wide
+// blocks; problems of a grouped launch are found as in the direct kernels.
+// Register budget of the F(4,3) kernels: at 120 the compiler keeps the
+// accumulators in VGPRs and fits the kernel in 170 registers (220 without
+// the bound), so a third wave -- a SpectralTransform kernel's -- fits on a
+// SIMD beside two of these: 252.2 vs 250.9 passes/s at 512x512.
+#ifndef LAMA_W4_NUM_VGPR
+#define LAMA_W4_NUM_VGPR 120
+#endif
+#if LAMA_W4_NUM_VGPR > 0
+#define LAMA_W4_REGS __attribute__((amdgpu_num_vgpr(LAMA_W4_NUM_VGPR)))
+#else
+#define LAMA_W4_REGS
+#endif
+#define LAMA_W4_KERNEL(NAME, NTR)                                                          \
+    extern "C" __global__ void __launch_bounds__(LAMA_NT) LAMA_W4_REGS NAME(LAMA_CONV_PARAMS) \
+    {                                                                                      \
+        LAMA_CONV_STARTS;                                                                  \
+        LAMA_STAMP_BEGIN;                                                                  \
+        using C = W4Cfg<NTR>;                                                              \
+        __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                     \
+        __shared__ float epl[192];                                                         \
+        int b = blockIdx.x;                                                                \
+        int pi = find_problem(ps, b);                                                      \
+        w4_tile<C>(probs[pi], b, lds, epl);                                                \
+        LAMA_STAMP_END;                                                                    \
+    }
+LAMA_W4_KERNEL(lama_conv3x3w4, 16)
+LAMA_W4_KERNEL(lama_conv3x3w4n, 8)
+#undef LAMA_W4_KERNEL

@@ -2,6 +2,7 @@
 // compiled into one module that the engine loads with hipModuleLoadData.
 #include "kernels/conv.hip"
 #include "kernels/wino.hip"
+#include "kernels/wino4.hip"
 #include "kernels/fft.hip"
 #include "kernels/tail.hip"
 #include "kernels/eltwise.hip"

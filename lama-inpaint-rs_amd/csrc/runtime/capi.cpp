@@ -168,6 +168,18 @@ extern "C" int lama_hip_profile_read_clock(lama_hip_ctx *ctx, int i, uint64_t *l
     return 1;
 }
 
+extern "C" int lama_hip_timeline(lama_hip_ctx *ctx, int enable)
+{
+    std::string e;
+    return ctx && ctx->eng.set_timeline(enable != 0, e) ? 0 : 1;
+}
+
+extern "C" int lama_hip_timeline_read(lama_hip_ctx *ctx, lama_launch_time *out, int max)
+{
+    std::string e;
+    return ctx && out && max >= 0 ? ctx->eng.timeline_read(out, max, e) : -1;
+}
+
 extern "C" void lama_hip_print_stats(lama_hip_ctx *ctx)
 {
     if (ctx) ctx->eng.print_stats();

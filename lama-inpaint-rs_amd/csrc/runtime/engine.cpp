@@ -92,9 +92,13 @@ ProbStarts prob_starts(const ConvProblem *q, size_t n)
 }
 
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
-void tile_shape(int family, int &tr, int &tc, bool wino = false)
+// `narrow`: the F(4,3) kernel's 32-pixel blocks.
+void tile_shape(int family, int &tr, int &tc, int wino = 0, bool narrow = false)
 {
-    if (family == F_CONV3 && wino) {  // lama_conv3x3w: 2 rows x 32 Winograd tiles
+    if ((family == F_CONV3 || family == F_CONV3G) && wino == 4 && narrow) {  // lama_conv3x3w4n
+        tr = 4;
+        tc = 32;
+    } else if ((family == F_CONV3 || family == F_CONV3G) && wino) {  // lama_conv3x3w / w4: 2 rows x 64 px
         tr = 2;
         tc = 64;
     } else if (family == F_CONV1 || family == F_CONV1R) {
@@ -198,6 +202,41 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
                         if (ci < C)
                             for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
                         d[((size_t)co * p.nchunk + ck) * 12 * KC + (u * 3 + ky) * KC + kc] = (float)v;
+                    }
+    return p;
+}
+
+// 3x3 weights for lama_conv3x3w4 / w4n: per output channel and chunk of
+// LAMA_WINO_KC input channels, [u][ky][ci] (u = 0..5) padded to LAMA_WINO4_WKP
+// floats, with U_u = sum over kx of G[u][kx] * w[ky][kx] and
+// G = (1/4, 0, 0; -1/6, -1/6, -1/6; -1/6, 1/6, -1/6; 1/24, 1/12, 1/6;
+// 1/24, -1/12, 1/6; 0, 0, 1) -- the Winograd F(4,3) weight transform for the
+// points 0, 1, -1, 2, -2, infinity, evaluated in f64 and rounded once to f32.
+Packed pack_wino4(Arena &A, int M, int C, const std::function<float(int, int, int)> &get)
+{
+    static const double G[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+                                   {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
+    constexpr int KC = LAMA_WINO_KC, WKP = LAMA_WINO4_WKP;
+    static_assert(WKP % KC == 0, "whole channel groups per padded row");
+    Packed p;
+    p.M = M;
+    p.C = C;
+    p.T = WKP / KC;  // the chunk stride is T * KC floats, as for the other layouts
+    p.KC = KC;
+    p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
+    p.wrow = p.nchunk * WKP;
+    p.off = A.add((size_t)M * p.wrow);
+    float *d = A.h.data() + p.off;
+    for (int co = 0; co < M; ++co)
+        for (int ck = 0; ck < p.nchunk; ++ck)
+            for (int u = 0; u < 6; ++u)
+                for (int ky = 0; ky < 3; ++ky)
+                    for (int kc = 0; kc < KC; ++kc) {
+                        const int ci = ck * KC + kc;
+                        double v = 0;
+                        if (ci < C)
+                            for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
+                        d[((size_t)co * p.nchunk + ck) * WKP + (u * 3 + ky) * KC + kc] = (float)v;
                     }
     return p;
 }
@@ -348,10 +387,19 @@ bool Engine::open(std::string &err)
             !check(hip_->hipModuleGetFunction(&fn_pw_v2_[f], module_, kPwV2Name[f]), kPwV2Name[f], err))
             return false;
     if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err) ||
-        !check(hip_->hipModuleGetFunction(&fn_tail_u8_, module_, "lama_tail_u8"), "lama_tail_u8", err))
+        !check(hip_->hipModuleGetFunction(&fn_wino4_[0], module_, "lama_conv3x3w4"), "lama_conv3x3w4", err) ||
+        !check(hip_->hipModuleGetFunction(&fn_wino4_[1], module_, "lama_conv3x3w4n"), "lama_conv3x3w4n", err) ||
+        !check(hip_->hipModuleGetFunction(&fn_tail_u8_, module_, "lama_tail_u8"), "lama_tail_u8", err) ||
+        !check(hip_->hipModuleGetFunction(&fn_finalize_ks_[0], module_, "lama_finalize10"), "lama_finalize10", err) ||
+        !check(hip_->hipModuleGetFunction(&fn_finalize_ks_[1], module_, "lama_finalize20"), "lama_finalize20", err))
         return false;
     fn_build_in_ = fn_[F_INPUT];
-    wino_ = !(getenv("LAMA_FFC_WINO") && atoi(getenv("LAMA_FFC_WINO")) == 0);
+    if (const char *wv = getenv("LAMA_FFC_WINO")) {
+        const int v = atoi(wv);
+        wino_ = v == 0 ? 0 : v == 4 ? 4 : 2;
+    }
+    if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
     for (int s = 0; s < 2; ++s)
         for (int f = 0; f < 2; ++f)
             if (!check(hip_->hipModuleGetFunction(&fn_fft_ct_[s][f], module_, kFftCtName[s][f]), kFftCtName[s][f], err))
@@ -436,8 +484,11 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
                 return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
             };
             auto l2gw = [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; };
-            F.local = wino_ ? pack_wino(A, 128, 512, local) : pack(A, 128, 512, 9, 8, local);
-            F.l2g = wino_ ? pack_wino(A, 384, 128, l2gw) : pack(A, 384, 128, 9, 8, l2gw);
+            F.local = wino_ == 4 ? pack_wino4(A, 128, 512, local)
+                      : wino_   ? pack_wino(A, 128, 512, local)
+                                : pack(A, 128, 512, 9, 8, local);
+            F.l2g = wino_ == 4 ? pack_wino4(A, 384, 128, l2gw) : wino_ ? pack_wino(A, 384, 128, l2gw)
+                                                                     : pack(A, 384, 128, 9, 8, l2gw);
             F.conv2 = pack(A, 384, 192, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
             F.conv1 = pack(A, 192, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
             F.fu = pack(A, 384, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
@@ -551,6 +602,7 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
 hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
 {
+    if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_narrow(probs[0].OW) ? 1 : 0];
     if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
     // the widest activation loads every plane of the launch allows
@@ -562,6 +614,36 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
         if (N % 2 != 0 || N < 4 || (uintptr_t)s.src % 8 != 0) vw = 1;
     }
     return vw == 4 ? fn_[family] : vw == 2 ? fn_pw_v2_[family == F_CONV1R] : fn_pw_any_[family == F_CONV1R];
+}
+
+// F(4,3) blocks: 32 pixels x 4 rows unless LAMA_W4_TILE=64 (read at open)
+// selects 64 x 2.  The 32-pixel blocks never waste more columns (75-wide
+// planes use 96 of 128 columns instead of 75 of 128) and stage a quarter
+// fewer input values per output (6 rows x 8 tiles instead of 4 x 16 for 128
+// outputs per channel); measured (passes/s, 32 vs 64): 512x512 252.1 vs
+// 231.3, 600x600 137.8 vs 122.6, 2048x2048 17.90 vs 17.86.
+bool Engine::w4_narrow(int OW) const
+{
+    (void)OW;
+    return w4_force_ != 64;
+}
+
+// The FFC GEMMs' K split: at small planes the F(4,3) launches have few
+// workgroups (16 per block of 4 rows x 32 pixels for A and B together, 128 at
+// 256 x 256), each walking the whole K, and most CUs idle; splitting K into s
+// slices (raw partials summed by finalize, and by conv2's epilogue for l2g)
+// gives s times the workgroups with 1/s of the K loop.  The largest s of
+// 1, 2, 4 that keeps A and B within two workgroups per CU.
+int Engine::ksplit_for(int h, int w) const
+{
+    if (wino_ != 4) return 1;
+    if (ksplit_force_ == 1 || ksplit_force_ == 2 || ksplit_force_ == 4) return ksplit_force_;
+    int tr, tc;
+    tile_shape(F_CONV3, tr, tc, 4, w4_narrow(w / 8));
+    const int tiles = ((w / 8 + tc - 1) / tc) * ((h / 8 + tr - 1) / tr);
+    int s = 1;
+    while (s < LAMA_KSPLIT_MAX && 16 * tiles * (2 * s) <= 2 * LAMA_CUS) s *= 2;
+    return s;
 }
 
 bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
@@ -697,7 +779,7 @@ bool Engine::upload_plan(const Plan &p, hipStream_t s, std::string &err)
 
 // Byte offsets of every buffer of the per-shape activation arena (each
 // 256-byte aligned) and its total size.
-size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, ArenaLayout &L)
+size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, ArenaLayout &L)
 {
     const size_t P = (size_t)H * W, P2 = (size_t)(H / 2) * (W / 2), P4 = (size_t)(H / 4) * (W / 4);
     const size_t P8 = (size_t)(H / 8) * (W / 8), PS = (size_t)(H / 8) * ((W / 8) / 2 + 1);
@@ -718,10 +800,12 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.s = take(384 * PS * 4);
     L.s2 = take(384 * PS * 4);
     L.out = take(3 * P * 4);
-    L.gc = take(2 * 384 * P8 * 4);  // the l2g partial, double-buffered by FFC parity
-    // the FFC local GEMM's K-range partials: l2l, then the g2l ranges twice (by
-    // FFC parity: B(k+1) may run while finalize(k) still reads B(k)'s)
-    L.lq = take((1 + 2 * LAMA_G2L_RANGES) * 128 * P8 * 4);
+    // the l2g partials (ksplit of them), double-buffered by FFC parity
+    L.gc = take(2 * (size_t)ksplit * 384 * P8 * 4);
+    // the FFC local GEMM's K-range partials: l2l (ksplit of them), then the g2l
+    // ranges twice (by FFC parity: B(k+1) may run while finalize(k) still
+    // reads B(k)'s)
+    L.lq = take((size_t)ksplit * (1 + 2 * LAMA_G2L_RANGES) * 128 * P8 * 4);
     L.tmp = take(fg.split ? fg.tmp_bytes : 0);
     L.twr = take(ntwr * 4);
     L.twc = take(ntwc * 4);
@@ -750,7 +834,7 @@ bool Engine::plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::s
     if (!fft_len(w / 8, fr, twr, err) || !fft_len(h / 8, fc, twc, err) || !fft_geom(192, h / 8, w / 8, fg, err))
         return false;
     ArenaLayout lay;
-    arena = arena_layout(h, w, fg, twr.size(), twc.size(), lay);
+    arena = arena_layout(h, w, fg, twr.size(), twc.size(), ksplit_for(h, w), lay);
     return true;
 }
 
@@ -772,7 +856,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     if (!fft_geom(192, H8, W8, fg, err)) return false;
 
     ArenaLayout lay;
-    p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), lay);
+    const int ks = ksplit_for(H, W);
+    p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), ks, lay);
     const size_t o_in = lay.in, o_a1 = lay.a1, o_a2 = lay.a2, o_a3 = lay.a3, o_x = lay.x, o_y = lay.y, o_f = lay.f,
                  o_g = lay.g, o_s = lay.s, o_s2 = lay.s2, o_out = lay.out, o_gc = lay.gc, o_lq = lay.lq, o_tmp = lay.tmp,
                  o_twr = lay.twr, o_twc = lay.twc, o_desc = lay.desc;
@@ -822,7 +907,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc, wino_);
+        tile_shape(family, tr, tc, wino_, w4_narrow(OW));
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
         q.mblocks = (M + 63) / 64;
@@ -849,7 +934,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         unsigned nb = 0;
         for (auto &q : probs) {
             nb += (unsigned)q.nblocks;
-            if (q.nblocks != q.tiles_x * q.tiles_y * q.mblocks)
+            if (q.nblocks != std::max(1, q.ksplit) * q.tiles_x * q.tiles_y * q.mblocks ||
+                (q.ksplit > 1 && (L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1])))
                 bad_problem = true;
         }
         // the head kernel walks its tiles: two resident workgroups per CU
@@ -910,15 +996,27 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     auto ffc_src = [&](int k) { return k % 2 == 0 ? X : Y; };
     auto ffc_dst = [&](int k) { return k % 2 == 0 ? Y : X; };
     auto ffc_res = [&](int k) -> const float * { return k % 2 == 0 ? nullptr : X; };
-    auto gc_buf = [&](int k) { return GC + (size_t)(k % 2) * 384 * P8; };
+    auto gc_buf = [&](int k) { return GC + (size_t)(k % 2) * ks * 384 * P8; };
     auto raw = [](ConvProblem q) {
         q.scale = q.shift = nullptr;
         q.relu = 0;
         return q;
     };
-    // LQ plane of local part q of FFC k: l2l at 0, g2l range q at q + (k%2)*ranges
+    // LQ plane of local partial q of FFC k: the ks l2l slices at 0 .. ks-1, then
+    // the 4 ks g2l slices of FFC parity k % 2
     auto lq_plane = [&](int k, int q) {
-        return LQ + (size_t)(q == 0 ? 0 : q + (k % 2) * LAMA_G2L_RANGES) * 128 * P8;
+        return LQ + (size_t)(q < ks ? q : q + (k % 2) * LAMA_G2L_RANGES * ks) * 128 * P8;
+    };
+    // a problem split into s K slices of the packed chunks (F(4,3) kernels)
+    auto kslices = [&](ConvProblem q, int s, long out_kstride) {
+        if (s > 1) {
+            q.ksplit = s;
+            q.kchunks = q.s0.nchunk / s;
+            q.out_kstride = out_kstride;
+            q.nblocks *= s;
+            if (q.kchunks * s != q.s0.nchunk || q.kchunks % 2) bad_problem = true;
+        }
+        return q;
     };
     // Local GEMM part q of FFC k, a raw partial into LQ plane q: part 0 is l2l
     // (input channels 0..127, 16 chunks of 8), parts 1-4 are g2l over input
@@ -938,8 +1036,10 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     auto launch_a = [&](int k) {
         const FfcW &Fw = ffc_[k];
         std::vector<ConvProblem> probs{
-            part(k, 0), raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8,
-                                    W8, nullptr))};
+            kslices(part(k, 0), ks, (long)128 * P8),
+            kslices(raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8, W8,
+                                nullptr)),
+                    ks, (long)384 * P8)};
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
                     k % 2 ? EV_A1 : EV_A0);
@@ -949,7 +1049,18 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     const bool b_stream = !(getenv("LAMA_B_STREAM") && atoi(getenv("LAMA_B_STREAM")) == 0);
     auto launch_b = [&](int k) {
         std::vector<ConvProblem> probs;
-        for (int q = 1; q <= LAMA_G2L_RANGES; ++q) probs.push_back(part(k, q));
+        if (ks > 1) {
+            // split: the g2l ranges as the K slices of one problem (F(4,3) kernels)
+            const FfcW &Fw = ffc_[k];
+            const Packed &pk = Fw.local;
+            ConvSeg sq = seg(ffc_src(k) + (size_t)128 * P8, pk, 384, H8, W8);
+            sq.wt = wp(pk.off) + (size_t)(128 / pk.KC) * pk.T * pk.KC;
+            sq.nchunk = 384 / pk.KC;
+            probs.push_back(kslices(raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, lq_plane(k, ks), P8, W8, nullptr)),
+                                    LAMA_G2L_RANGES * ks, (long)128 * P8));
+        } else {
+            for (int q = 1; q <= LAMA_G2L_RANGES; ++q) probs.push_back(part(k, q));
+        }
         // own stream: waits for x_g(k) (conv2(k-1), or model.4 for k = 0) and
         // records EV_B for finalize(k); else in the main stream's order
         const int xg = k == 0 ? EV_FORK : ((k - 1) % 2 ? EV_S1 : EV_S0);
@@ -960,8 +1071,9 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     auto launch_finalize = [&](int k) {
         const FfcW &Fw = ffc_[k];
         FinalizeArgs fa2{};
-        for (int q = 0; q < LAMA_FIN_PARTS; ++q) fa2.part[q] = lq_plane(k, q);
-        fa2.nparts = LAMA_FIN_PARTS;
+        const int np = LAMA_FIN_PARTS * ks;  // l2l slices, then the g2l slices, in K order
+        for (int q = 0; q < np; ++q) fa2.part[q] = lq_plane(k, q);
+        fa2.nparts = np;
         fa2.C = 128;
         fa2.plane = (long)P8;
         fa2.scale = wp(Fw.bn_l);
@@ -969,7 +1081,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         fa2.res = ffc_res(k);
         fa2.out = ffc_dst(k);
         Launch L{};
-        L.fn = fn_[F_FINAL];
+        L.fn = ks == 1 ? fn_[F_FINAL] : fn_finalize_ks_[ks == 2 ? 0 : 1];
         L.family = F_FINAL;
         L.stream = S_MAIN;
         L.wait_ev = b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1;
@@ -978,7 +1090,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         L.arg = put(&fa2, sizeof fa2);
         L.nparams = 1;
         L.step_end = -1;
-        L.bytes = f4 * 128 * P8 * (LAMA_FIN_PARTS + 1 + (fa2.res ? 1 : 0));
+        L.bytes = f4 * 128 * P8 * (np + 1 + (fa2.res ? 1 : 0));
         p.launches.push_back(L);
     };
     auto launch_spectral = [&](int k) {
@@ -1003,6 +1115,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
                                  ffc_dst(k) + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
         q2.addend = gc_buf(k);
+        q2.naddend = ks;  // the l2g K slices
+        q2.addend_kstride = (long)384 * P8;
         conv_launch(F_CONV1R, {q2}, k % 2 == 1 ? 5 + k / 2 : -1, 2.0 * 192 * 384 * P8,
                     f4 * (192 * P8 + 384 * P8 * (res ? 3 : 2) + 384 * 192), S_SIDE, k % 2 ? EV_A1 : EV_A0,
                     k % 2 ? EV_S1 : EV_S0);
@@ -1132,7 +1246,7 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t
     unsigned long long *stamp = nullptr;
     Pending pe{};
     pe.stamp_off = -1;
-    if (prof && is_conv_family(L.family) && !capturing_) {
+    if (((prof && is_conv_family(L.family)) || timeline_) && !capturing_) {
         const size_t need = 2 * (size_t)L.grid;
         if (!stamp_buf_) {
             stamp_cap_ = (size_t)4 << 20;  // 32 MiB of u64 entries
@@ -1146,8 +1260,10 @@ bool Engine::launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t
             stamp = stamp_buf_ + stamp_used_;
             pe.stamp_off = (long)stamp_used_;
             pe.grid = L.grid;
+            if (timeline_) tl_.push_back({L.family, L.stream, (long)stamp_used_, L.grid});
             stamp_used_ += need;
         }
+        if (!prof) pe.stamp_off = -1;
     }
     void *params[5] = {&arg, &ps.s[0], &ps.s[1], &ps.s[2], &stamp};
     if (prof) {
@@ -1803,10 +1919,53 @@ void Engine::collect_events()
                 prof_clock_ms_[pe.family] += (double)(t1 - t0) / clock_khz_;
             }
         }
-        hip_->hipMemset(stamp_buf_, 0, stamp_used_ * 8);
-        stamp_used_ = 0;
+        if (tl_.empty()) {  // the timeline reads the same array later
+            hip_->hipMemset(stamp_buf_, 0, stamp_used_ * 8);
+            stamp_used_ = 0;
+        }
     }
     pending_.clear();
+}
+
+bool Engine::set_timeline(bool on, std::string &err)
+{
+    collect_events();
+    tl_.clear();
+    if (stamp_buf_ && stamp_used_ &&
+        !check(hip_->hipMemset(stamp_buf_, 0, stamp_used_ * 8), "hipMemset(stamps)", err))
+        return false;
+    stamp_used_ = 0;
+    timeline_ = on;
+    return true;
+}
+
+int Engine::timeline_read(lama_launch_time *out, int max, std::string &err)
+{
+    if (!check(hip_->hipDeviceSynchronize(), "hipDeviceSynchronize", err)) return -1;
+    if (tl_.empty() || !stamp_used_ || clock_khz_ <= 0) return 0;
+    std::vector<unsigned long long> st(stamp_used_);
+    if (!check(hip_->hipMemcpy(st.data(), stamp_buf_, stamp_used_ * 8, hipMemcpyDeviceToHost), "hipMemcpy(stamps)", err))
+        return -1;
+    unsigned long long base = ~0ull;
+    std::vector<std::pair<unsigned long long, unsigned long long>> w(tl_.size(), {~0ull, 0ull});
+    for (size_t i = 0; i < tl_.size(); ++i) {
+        for (unsigned b = 0; b < tl_[i].grid; ++b) {
+            const unsigned long long a = st[tl_[i].stamp_off + 2 * b], e = st[tl_[i].stamp_off + 2 * b + 1];
+            if (!a) continue;
+            w[i].first = std::min(w[i].first, a);
+            w[i].second = std::max(w[i].second, e);
+        }
+        base = std::min(base, w[i].first);
+    }
+    int n = 0;
+    for (size_t i = 0; i < tl_.size() && n < max; ++i, ++n) {
+        out[n].family = tl_[i].family;
+        out[n].stream = tl_[i].stream;
+        const bool ok = w[i].second >= w[i].first && w[i].first != ~0ull;
+        out[n].start_us = ok ? (double)(w[i].first - base) * 1e3 / clock_khz_ : -1;
+        out[n].end_us = ok ? (double)(w[i].second - base) * 1e3 / clock_khz_ : -1;
+    }
+    return n;
 }
 
 bool Engine::profile_read_clock(int i, uint64_t &launches, double &ms)
@@ -1911,7 +2070,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     }
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
-    const bool wino = family == F_CONV3 && wino_;
+    const int wino = family == F_CONV3 ? wino_ : 0;
     const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : 8;
     if ((size_t)4 * KC * h * w >= ((size_t)1 << 32)) {  // 32-bit staging offsets within a K chunk
         err = "op_conv2d: plane too large";
@@ -1920,7 +2079,9 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     Arena A;
     const int T = k * k;
     auto getw = [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; };
-    Packed pk = wino ? pack_wino(A, cout, cin, getw) : pack(A, cout, cin, T, KC, getw);
+    Packed pk = wino == 4 ? pack_wino4(A, cout, cin, getw)
+                : wino    ? pack_wino(A, cout, cin, getw)
+                          : pack(A, cout, cin, T, KC, getw);
     size_t bn = A.add(2 * (size_t)cout);
     for (int i = 0; i < cout; ++i) {
         A.h[bn + i] = scale ? scale[i] : 1.f;
@@ -1944,7 +2105,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.OH = family == F_CONV1 ? 1 : oh;
     q.OW = family == F_CONV1 ? oh * ow : ow;
     int tr, tc;
-    tile_shape(family, tr, tc, wino);
+    tile_shape(family, tr, tc, wino, w4_narrow(q.OW));
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
     q.mblocks = (cout + 63) / 64;

@@ -9,6 +9,7 @@
 #include "hip_api.h"
 #include "kernels/common.h"
 #include "lama_host.h"
+#include "lama_hip.h"
 
 namespace lama {
 
@@ -146,6 +147,12 @@ public:
     // Family i's profiled conv launches timed by their kernel-clock stamps
     // (first workgroup start to last workgroup end; the conv families only).
     bool profile_read_clock(int i, uint64_t &launches, double &ms);
+    // Timeline: while on, every launch (any family) stores its workgroups'
+    // kernel-clock stamps, without events; timeline_read waits for the device
+    // and returns, per launch in issue order, its family, stream and
+    // first-start / last-end in microseconds from the first record's start.
+    bool set_timeline(bool on, std::string &err);
+    int timeline_read(lama_launch_time *out, int max, std::string &err);
     int launch_count(int h, int w);
     // Device bytes of one forward at h x w: the activation arena of that shape
     // (exact, from its layout) and the resident weights (0 before loading).
@@ -185,7 +192,7 @@ private:
     SpecPlan *spec_plan_for(int h, int w, std::string &err);
     bool step_hooks(Plan &p, const float *in, std::string &err);
     bool replay(Plan &p, hipStream_t s, std::string &err);
-    static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, ArenaLayout &L);
+    static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, ArenaLayout &L);
     bool use_graph() const;
     void free_plan(Plan &p);
     bool launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record = nullptr);
@@ -207,8 +214,17 @@ private:
     // FFC 3x3 convolutions as Winograd F(2,3) along x (lama_conv3x3w), or
     // with LAMA_FFC_WINO=0 as the direct implicit GEMM (lama_conv3x3); chosen
     // at open, since the weights are packed for one or the other
-    bool wino_ = true;
-    hipFunction_t fn_wino_ = nullptr;
+    // LAMA_FFC_WINO: 0 direct; 2 F(2,3) (lama_conv3x3w); 4 (default) F(4,3)
+    // in 32-pixel blocks (lama_conv3x3w4n), or 64-pixel ones (lama_conv3x3w4)
+    // with LAMA_W4_TILE=64
+    int wino_ = 4;
+    int w4_force_ = 0;  // LAMA_W4_TILE: 32 or 64 forces the F(4,3) block width
+    bool w4_narrow(int OW) const;
+    int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
+    // K split of the FFC GEMMs at input h x w (1 unless the F(4,3) kernels
+    // would leave CUs idle)
+    int ksplit_for(int h, int w) const;
+    hipFunction_t fn_wino_ = nullptr, fn_wino4_[2] = {};
     hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr, g2l_ = nullptr;
@@ -241,6 +257,7 @@ private:
     void release_scratch_owner();
     std::map<std::pair<int, int>, SpecPlan> spec_plans_;
     hipFunction_t fn_build_in_ = nullptr, fn_tail_u8_ = nullptr;
+    hipFunction_t fn_finalize_ks_[2] = {};  // lama_finalize10, lama_finalize20 (K split 2, 4)
 
     // profiling
     uint32_t prof_mask_ = 0;
@@ -257,6 +274,13 @@ private:
     size_t stamp_cap_ = 0, stamp_used_ = 0;
     double clock_khz_ = 0;  // device wall-clock rate
     uint64_t prof_clock_n_[F_COUNT] = {};
+    bool timeline_ = false;
+    struct TlRec {
+        int family, stream;
+        long stamp_off;
+        unsigned grid;
+    };
+    std::vector<TlRec> tl_;
     double prof_clock_ms_[F_COUNT] = {};
     std::vector<Pending> pending_;
     std::vector<hipEvent_t> event_pool_;

@@ -22,6 +22,11 @@ N_STEPS = 29
 _lib = None
 
 
+class LaunchTime(ctypes.Structure):
+    _fields_ = [("family", ctypes.c_int32), ("stream", ctypes.c_int32), ("start_us", ctypes.c_double),
+                ("end_us", ctypes.c_double)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -44,6 +49,8 @@ def lib():
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_print_stats.argtypes = [vp]
+        L.lama_hip_timeline.argtypes = [vp, ctypes.c_int]
+        L.lama_hip_timeline_read.argtypes = [vp, ctypes.POINTER(LaunchTime), ctypes.c_int]
         L.lama_hip_profile_read_clock.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
                                                   ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_launch_count.argtypes = [vp, ctypes.c_int, ctypes.c_int]
@@ -227,6 +234,18 @@ class Engine:
                                             clock_launches=cn.value, clock_ms=cms.value)
             i += 1
         return out
+
+    def timeline(self, on):
+        """Record every launch's kernel-clock window (lama_hip_timeline)."""
+        self._check(lib().lama_hip_timeline(self.ctx, int(bool(on))) and "lama_hip_timeline failed")
+
+    def timeline_read(self, max_launches=1 << 16):
+        """[(family name, stream, start_us, end_us)] in issue order."""
+        buf = (LaunchTime * max_launches)()
+        n = lib().lama_hip_timeline_read(self.ctx, buf, max_launches)
+        if n < 0:
+            raise HipError("lama_hip_timeline_read failed")
+        return [(FAMILIES[r.family], r.stream, r.start_us, r.end_us) for r in buf[:n]]
 
     def print_stats(self):
         lib().lama_hip_print_stats(self.ctx)

@@ -283,3 +283,96 @@ def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal, h,
     d = np.abs(u8g.astype(int) - u8r.astype(int))
     assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
     assert np.array_equal(u8g[mask == 0], img[mask == 0])
+
+
+@pytest.fixture(scope="module", params=[("2", ""), ("4", "64")], ids=["f23", "f43w64"])
+def w4_forward_engine(pkg, weights_dir, request):
+    """The forward with the non-default Winograd kernels: F(2,3)
+    (LAMA_FFC_WINO=2) and F(4,3) in 64-pixel blocks (LAMA_W4_TILE=64)."""
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_FFC_WINO", request.param[0])
+        mp.setenv("LAMA_W4_TILE", request.param[1])
+        eng = pkg.hip_engine.Engine()
+    eng.load_weights(pkg.host_api.Store(weights_dir["cal"]))
+    yield eng
+    eng.close()
+
+
+@pytest.mark.parametrize("h,w,kind", [(128, 96, "strokes"), (256, 256, "rect"), (600, 600, "rect")])
+def test_forward_winograd_f43_steps(pkg, w4_forward_engine, oracle_cal, h, w, kind):
+    """The forward with the FFC 3x3 convolutions as Winograd F(2,3) and as
+    F(4,3) in 64-pixel blocks (the default, F(4,3) in 32-pixel blocks, runs
+    every other forward test): every plan step within the per-layer bound of
+    the oracle, the composite within 1/255."""
+    img, mask = _case(pkg, h, w, kind)
+    x = pkg.host_api.build_input(img, mask)
+    print(f"case f43 {h}x{w} {kind}", flush=True)
+    got, got_steps = w4_forward_engine.forward_steps(x, list(range(29)))
+    ref, ref_steps = oracle_cal.forward(x, steps=True)
+    for s in range(29):
+        e = rel_err(got_steps[s], ref_steps[s])
+        assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+    assert np.array_equal(w4_forward_engine.forward(x), got)
+    u8g = pkg.host_api.composite(img, mask, got, 0, 0)
+    u8r = pkg.host_api.composite(img, mask, ref, 0, 0)
+    d = np.abs(u8g.astype(int) - u8r.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
+
+
+def test_forward_winograd_f43_matches_f23_512(pkg, w4_forward_engine, engine):
+    """At the bench shape, the default forward within float rounding of the
+    other Winograd variants'."""
+    img, mask = _case(pkg, 512, 512, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    a = w4_forward_engine.forward(x)
+    b = engine.forward(x)
+    assert rel_err(a, b) < 1e-4
+
+
+def test_timeline_records_every_launch(pkg, engine):
+    """lama_hip_timeline: one pass's 296 launches in issue order, each with a
+    kernel-clock window; launches on one stream never overlap, and the
+    timeline leaves the result unchanged."""
+    img, mask = _case(pkg, 128, 96, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    ref = engine.forward(x)
+    engine.timeline(True)
+    got = engine.forward(x)
+    tl = engine.timeline_read()
+    engine.timeline(False)
+    assert np.array_equal(got, ref)
+    assert len(tl) == 1 + 3 + 36 * 8 + 3 + 1
+    assert tl[0][0] == "conv7x7" and tl[-1][0] == "tail"
+    assert all(0 <= s <= e for _, _, s, e in tl)
+    for stream in (0, 1, 2):
+        own = [(s, e) for _, st, s, e in tl if st == stream]
+        assert own and all(b[0] >= a[1] - 0.05 for a, b in zip(own, own[1:])), stream
+    # FFC k's conv2 (stream 1) starts after its l2l + l2g launch (stream 0) ends
+    a_ends = [e for f, st, s, e in tl if f == "conv3x3"]
+    c2_starts = [s for f, st, s, e in tl if f == "conv1x1res"]
+    assert len(a_ends) == len(c2_starts) == 36
+    assert all(c >= a - 0.05 for a, c in zip(a_ends, c2_starts))
+
+
+@pytest.mark.parametrize("ks", ["1", "2"])
+def test_forward_ksplit_variants_256(pkg, engine, oracle_cal, monkeypatch, ks):
+    """The FFC GEMMs' K split (LAMA_KSPLIT, read at open): at 256 x 256 the
+    default splits K in 4 (its raw partials summed by finalize and by conv2's
+    epilogue); 1 and 2 slices give the same forward within float rounding,
+    and every plan step of the 2-slice forward is within the per-layer bound
+    of the oracle."""
+    img, mask = _case(pkg, 256, 256, "rect")
+    x = pkg.host_api.build_input(img, mask)
+    default = engine.forward(x)
+    monkeypatch.setenv("LAMA_KSPLIT", ks)
+    eng = pkg.hip_engine.Engine()
+    eng.load_weights(engine._cal_store)
+    print(f"case 256x256 ksplit {ks}", flush=True)
+    got, got_steps = eng.forward_steps(x, list(range(29)))
+    eng.close()
+    assert rel_err(got, default) < 1e-4
+    if ks == "2":
+        ref, ref_steps = oracle_cal.forward(x, steps=True)
+        for s in range(29):
+            e = rel_err(got_steps[s], ref_steps[s])
+            assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"

@@ -161,9 +161,10 @@ WINO_CASES = [
 
 @pytest.mark.parametrize("cin,cout,h,w", WINO_CASES)
 def test_conv3x3_winograd(engine, cin, cout, h, w):
-    """The FFC 3x3 convolution as Winograd F(2,3) along x (lama_conv3x3w, the
-    default) against the oracle's direct sum.  The transforms round
-    differently from the direct sum, within the same 1e-5 relative bound."""
+    """The FFC 3x3 convolution as the default engine runs it (Winograd F(4,3)
+    along x in 32-pixel blocks, lama_conv3x3w4n) against the oracle's direct
+    sum.  The transforms round differently from the direct sum, within the same
+    1e-5 relative bound."""
     rng = np.random.default_rng(cin * 100 + cout + w)
     x = rng.standard_normal((cin, h, w), np.float32)
     wt = (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
@@ -185,4 +186,41 @@ def test_conv3x3_direct(direct_engine, cin, cout, h, w):
     print(f"case direct {cin}x{h}x{w} -> {cout}", flush=True)
     got = direct_engine.op_conv2d(x, wt, None, 1, s, t, relu=True)
     ref = _oracle_bn_relu(O.conv2d(x, wt, None, pad=1, stride=1, reflect=True), s, t)
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32")], ids=["f23", "f43w64", "f43w32"])
+def w4_engine(pkg, request):
+    """Each Winograd kernel: F(2,3) (LAMA_FFC_WINO=2, lama_conv3x3w) and F(4,3)
+    (LAMA_FFC_WINO=4) with 64- or 32-pixel blocks (LAMA_W4_TILE); both are read
+    when the context opens."""
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_FFC_WINO", request.param[0])
+        mp.setenv("LAMA_W4_TILE", request.param[1])
+        eng = pkg.hip_engine.Engine()
+    yield eng
+    eng.close()
+
+
+W4_CASES = WINO_CASES + [
+    (8, 64, 5, 75),       # the 600x600 bottleneck width: 75 = 2 x 32 + 11 (or 64 + 11)
+    (16, 32, 9, 32),      # the 256x256 bottleneck width
+    (4, 70, 7, 3),        # narrower than one Winograd tile
+]
+
+
+@pytest.mark.parametrize("cin,cout,h,w", W4_CASES)
+def test_conv3x3_winograd_f43(w4_engine, cin, cout, h, w):
+    """The FFC 3x3 convolution as Winograd F(2,3) (lama_conv3x3w) and F(4,3)
+    along x (lama_conv3x3w4 / w4n) against the oracle's direct sum, the same
+    1e-5 relative bound: F(4,3)'s larger transform constants round a little
+    more than F(2,3)'s."""
+    rng = np.random.default_rng(cin * 100 + cout + w)
+    x = rng.standard_normal((cin, h, w), np.float32)
+    wt = (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
+    s, t = _bn(rng, cout)
+    print(f"case wino4 {cin}x{h}x{w} -> {cout}", flush=True)
+    got = w4_engine.op_conv2d(x, wt, None, 1, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv2d(x, wt, None, pad=1, stride=1, reflect=True), s, t)
+    assert got.shape == ref.shape
     assert rel_err(got, ref) < TOL
