@@ -89,18 +89,19 @@ def main():
     # both launches of each FFC: A = l2l + l2g (family conv3x3) and B = g2l
     # (family conv3x3g2l), one kernel
     dom_fams = ["conv3x3", "conv3x3g2l"]
-    # the FFC 3x3 convolutions run as Winograd F(4,3) along x in 32-pixel
-    # blocks (LAMA_FFC_WINO=2: F(2,3); 0: the direct implicit GEMM;
-    # LAMA_W4_TILE=64: F(4,3) in 64-pixel blocks); FLOPs are the convolution's
+    # the FFC 3x3 convolutions run as Winograd F(4,3) along x (LAMA_FFC_WINO=2:
+    # F(2,3); 0: the direct implicit GEMM); FLOPs are the convolution's
     # algorithmic count in every case, of which F(4,3) issues 1/2 and F(2,3)
     # 2/3 as MFMA work
     wv = os.environ.get("LAMA_FFC_WINO", "4")
     wino = 0 if wv == "0" else 2 if wv == "2" else 4
-    w4_wide = os.environ.get("LAMA_W4_TILE", "") == "64"
-    dom_kernel = {0: "lama_conv3x3", 2: "lama_conv3x3w", 4: "lama_conv3x3w4" if w4_wide else "lama_conv3x3w4n"}[wino]
+    # the plan's own kernel for the FFC GEMMs at this size (the F(4,3) block
+    # shape is chosen per plane: 2 x 64, 4 x 32 or 8 x 16 output pixels)
+    dom_kernel = eng.kernel_name(S, S, "conv3x3")
     issued = {0: 1.0, 2: 2.0 / 3.0, 4: 0.5}[wino]
-    geometry = {0: "512 workgroups of 64 channels x 64 px", 2: "256 workgroups of 64 channels x 2 rows x 64 px",
-                4: "256 workgroups of 64 channels x " + ("2 rows x 64 px" if w4_wide else "4 rows x 32 px")}[wino]
+    block = {"lama_conv3x3": "64 px", "lama_conv3x3w": "2 rows x 64 px", "lama_conv3x3w4": "2 rows x 64 px",
+             "lama_conv3x3w4n": "4 rows x 32 px", "lama_conv3x3w4q": "8 rows x 16 px"}[dom_kernel]
+    geometry = "workgroups of 64 channels x " + block
     method = {0: "direct implicit GEMM", 2: "Winograd F(2,3) along x", 4: "Winograd F(4,3) along x"}[wino]
     eng.profile_reset()
     eng.synchronize()

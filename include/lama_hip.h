@@ -185,6 +185,12 @@ int lama_hip_plan_bytes(lama_hip_ctx *ctx, int h, int w, uint64_t *arena_bytes, 
                         char *err, size_t errlen);
 /* Launches per forward at h x w (after a plan exists for that shape). */
 int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w);
+/* The kernel symbol of the first launch of family `family` (numbered as in
+ * lama_hip_profile) in the plan at h x w, e.g. which F(4,3) block shape the
+ * FFC GEMMs take at that plane size.  No reference counterpart: it names the
+ * kernel a trace of the pass shows.  0 on success; 1 without that plan or
+ * launch, or a name longer than namelen - 1. */
+int lama_hip_kernel_name(lama_hip_ctx *ctx, int h, int w, int family, char *name, size_t namelen);
 
 /* Device buffers for callers that keep their data resident (the role of
  * lightgpu's upload/download, cuda.rs:390-444). */

@@ -23,6 +23,8 @@
 // (its Bluestein path computes the opposite-sign DFT); `sign_fwd` carries it.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -580,36 +582,53 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const
     }
 }
 
-// ---- compile-time shapes: square power-of-two planes -------------------------
+// ---- compile-time shapes: square planes --------------------------------------
 //
-// The bottleneck planes of 256x256 and 512x512 inputs (32x32, 64x64) use the
-// single-block algorithm above with every length, count and stride a
-// compile-time constant, so no index arithmetic is left in the kernels but
-// shifts, masks and a multiply-high by the constant W/2+1.  This matters
+// The bottleneck planes of 256x256, 512x512 and 600x600 inputs (32x32, 64x64,
+// 75x75) use the single-block algorithm above with every length, count and
+// stride a compile-time constant, so no index arithmetic is left in the
+// kernels but shifts, masks and multiplies-high by constants.  This matters
 // beside the FFC GEMM: its FP32 MFMAs hold the SIMDs' math pipes, and every
 // VALU instruction of these kernels then waits its turn, so the runtime
 // integer divisions of the generic path (about half of its instructions)
-// cost more than the butterflies themselves.  The radix plan is 8 first,
-// then one 4 or 2 (64 = 8*8, 32 = 8*4); power-of-two lengths use the sign
-// -1 forward, +1 inverse.
+// cost more than the butterflies themselves.  The radix plan is the host's
+// (Engine::fft_len): 8s, then 4s, 2s, 3s and 5s (64 = 8*8, 32 = 8*4,
+// 75 = 3*5*5).  The exponent sign follows the same per-length rule as the
+// runtime-shaped kernels: -1 forward for powers of two, +1 otherwise.  Planes
+// whose side is a multiple of 4 move rows as float4 quads; others (75) load
+// and store the plane linearly, one float per lane.
 
 namespace {
 
-template <int N, int R, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
-__device__ __forceinline__ void ct_pass(const float2 *in, float2 *out, const float2 *tw)
+// the radix of the next pass, as Engine::fft_len orders them
+constexpr int ct_radix(int rem)
 {
-    constexpr int M = N / R, TWSTEP = N / (NS * R), TOTAL = COUNT * M;
-#pragma unroll
-    for (int it = 0; it < (TOTAL + LAMA_FFT_NT - 1) / LAMA_FFT_NT; ++it) {
-        const int idx = threadIdx.x + it * LAMA_FFT_NT;
-        if (TOTAL % LAMA_FFT_NT != 0 && idx >= TOTAL) break;
-        // rows: a transform's butterflies on neighbouring lanes; columns:
-        // neighbouring transforms on neighbouring lanes
+    return rem % 8 == 0 ? 8 : rem % 4 == 0 ? 4 : rem % 2 == 0 ? 2 : rem % 3 == 0 ? 3 : rem % 5 == 0 ? 5 : 0;
+}
+
+// Shape constants of a compile-time N x N plane.
+template <int N>
+struct CtPlane {
+    static constexpr int H = N, W = N, Wh = N / 2 + 1, HP = (N + 1) / 2, NB = lama_fft_nb(N, N), NT = LAMA_FFT_NT;
+    static constexpr int SF = (N & (N - 1)) == 0 ? -1 : 1;  // forward exponent sign
+    static constexpr bool VEC = N % 4 == 0;                  // rows as float4 quads
+    static constexpr int NE = H * W, RL = (NE + NT - 1) / NT;  // linear plane floats per thread
+};
+
+// Butterfly idx of a radix-R pass: its R inputs, twiddled and transformed
+// (ct_bfly_in), then stored (ct_bfly_out).  Rows: a transform's butterflies
+// on neighbouring lanes; columns: neighbouring transforms on neighbouring
+// lanes.
+template <int N, int R, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
+struct CtBfly {
+    static constexpr int M = N / R, TWSTEP = N / (NS * R), TOTAL = COUNT * M;
+    static constexpr int IT = (TOTAL + LAMA_FFT_NT - 1) / LAMA_FFT_NT;  // butterflies per thread
+    static __device__ __forceinline__ void in(int idx, const float2 *buf, const float2 *tw, float2 (&v)[R])
+    {
         const int b = ESTRIDE == 1 ? idx / M : idx % COUNT;
         const int j = ESTRIDE == 1 ? idx % M : idx / COUNT;
         const int k = j % NS;
-        const float2 *src = in + b * BSTRIDE;
-        float2 v[R];
+        const float2 *src = buf + b * BSTRIDE;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float2 x = src[(j + r * M) * ESTRIDE];
@@ -617,9 +636,15 @@ __device__ __forceinline__ void ct_pass(const float2 *in, float2 *out, const flo
             v[r] = x;
         }
         dft<R>(v, SIGN);
-        float2 *dst = out + b * BSTRIDE;
+    }
+    static __device__ __forceinline__ void out(int idx, float2 *buf, const float2 (&v)[R])
+    {
+        const int b = ESTRIDE == 1 ? idx / M : idx % COUNT;
+        const int j = ESTRIDE == 1 ? idx % M : idx / COUNT;
+        const int k = j % NS;
+        float2 *dst = buf + b * BSTRIDE;
         const int base = (j / NS) * NS * R + k;
-        if (NS == 1 && ESTRIDE == 1) {
+        if constexpr (NS == 1 && ESTRIDE == 1 && R % 2 == 0 && BSTRIDE % 2 == 0) {
 #pragma unroll
             for (int r = 0; r < R; r += 2)
                 *reinterpret_cast<float4 *>(dst + base + r) = make_float4(v[r].x, v[r].y, v[r + 1].x, v[r + 1].y);
@@ -628,19 +653,63 @@ __device__ __forceinline__ void ct_pass(const float2 *in, float2 *out, const flo
             for (int r = 0; r < R; ++r) dst[(base + r * NS) * ESTRIDE] = v[r];
         }
     }
+};
+
+template <int N, int R, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
+__device__ __forceinline__ void ct_pass(const float2 *in, float2 *out, const float2 *tw)
+{
+    using B = CtBfly<N, R, NS, COUNT, BSTRIDE, ESTRIDE, SIGN>;
+#pragma unroll
+    for (int it = 0; it < B::IT; ++it) {
+        const int idx = threadIdx.x + it * LAMA_FFT_NT;
+        if (B::TOTAL % LAMA_FFT_NT != 0 && idx >= B::TOTAL) break;
+        float2 v[R];
+        B::in(idx, in, tw, v);
+        B::out(idx, out, v);
+    }
 }
 
-// All passes of a length-N transform; returns the buffer holding the result.
-template <int N, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
+// The pass in place: the thread's butterflies are all read and transformed
+// before a barrier and stored after it, so one buffer serves as both.
+template <int N, int R, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN>
+__device__ __forceinline__ void ct_pass_ip(float2 *buf, const float2 *tw)
+{
+    using B = CtBfly<N, R, NS, COUNT, BSTRIDE, ESTRIDE, SIGN>;
+    float2 v[B::IT][R];
+#pragma unroll
+    for (int it = 0; it < B::IT; ++it) {
+        const int idx = threadIdx.x + it * LAMA_FFT_NT;
+        if (B::TOTAL % LAMA_FFT_NT != 0 && idx >= B::TOTAL) break;
+        B::in(idx, buf, tw, v[it]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < B::IT; ++it) {
+        const int idx = threadIdx.x + it * LAMA_FFT_NT;
+        if (B::TOTAL % LAMA_FFT_NT != 0 && idx >= B::TOTAL) break;
+        B::out(idx, buf, v[it]);
+    }
+}
+
+// All passes of a length-N transform; returns the buffer holding the result
+// (ping-ponging between a and b, or in a alone when IP).
+template <int N, int NS, int COUNT, int BSTRIDE, int ESTRIDE, int SIGN, bool IP = false>
 __device__ __forceinline__ float2 *ct_stockham(float2 *a, float2 *b, const float2 *tw)
 {
     if constexpr (NS >= N) {
         return a;
     } else {
-        constexpr int REM = N / NS, R = REM % 8 == 0 ? 8 : REM % 4 == 0 ? 4 : 2;
-        ct_pass<N, R, NS, COUNT, BSTRIDE, ESTRIDE, SIGN>(a, b, tw);
-        __syncthreads();
-        return ct_stockham<N, NS * R, COUNT, BSTRIDE, ESTRIDE, SIGN>(b, a, tw);
+        constexpr int R = ct_radix(N / NS);
+        static_assert(R != 0, "lengths of factors 2, 3 and 5 only");
+        if constexpr (IP) {
+            ct_pass_ip<N, R, NS, COUNT, BSTRIDE, ESTRIDE, SIGN>(a, tw);
+            __syncthreads();
+            return ct_stockham<N, NS * R, COUNT, BSTRIDE, ESTRIDE, SIGN, IP>(a, b, tw);
+        } else {
+            ct_pass<N, R, NS, COUNT, BSTRIDE, ESTRIDE, SIGN>(a, b, tw);
+            __syncthreads();
+            return ct_stockham<N, NS * R, COUNT, BSTRIDE, ESTRIDE, SIGN, IP>(b, a, tw);
+        }
     }
 }
 
@@ -661,48 +730,93 @@ __device__ __forceinline__ float2 ct_twiddle_fetch(const FftArgs &A)
     return *p;
 }
 
-template <int N>
+// IP: one plane buffer instead of two (passes and reorderings in place
+// through registers), for planes whose two buffers would keep a block from
+// sharing a CU with two FFC GEMM workgroups
+template <int N, bool IP>
 __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
 {
-    constexpr int H = N, W = N, Wh = N / 2 + 1, HP = N / 2, NB = lama_fft_nb(N, N), NT = LAMA_FFT_NT;
-    static_assert(2 * N <= NT && HP * W / 4 <= 2 * NT, "one twiddle and at most two quads per thread");
-    float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
+    using P = CtPlane<N>;
+    constexpr int H = P::H, W = P::W, Wh = P::Wh, HP = P::HP, NB = P::NB, NT = P::NT, SF = P::SF;
+    static_assert(2 * N <= NT, "one twiddle entry per thread");
+    float2 *b0 = sm, *b1 = IP ? sm : sm + NB, *twr = sm + (IP ? 1 : 2) * NB, *twc = twr + W;
     const int c = blockIdx.x;
     // prologue: every global load before the first LDS write
     float2 tv = ct_twiddle_fetch<N>(A);
     const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
-    constexpr int W4 = W / 4, NQ = HP * W4, RQ = (NQ + NT - 1) / NT;
-    float4 qa[RQ], qb[RQ];
+    if constexpr (P::VEC) {
+        constexpr int W4 = W / 4, NQ = HP * W4, RQ = (NQ + NT - 1) / NT;
+        static_assert(RQ <= 2, "at most two quads per thread");
+        float4 qa[RQ], qb[RQ];
 #pragma unroll
-    for (int k = 0; k < RQ; ++k) {
-        const int q = min((int)threadIdx.x + k * NT, NQ - 1), p = q / W4, x = (q % W4) * 4;
-        qa[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
-        qb[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
-    }
-    ct_twiddles<N>(A, twr, twc, tv);
+        for (int k = 0; k < RQ; ++k) {
+            const int q = min((int)threadIdx.x + k * NT, NQ - 1), p = q / W4, x = (q % W4) * 4;
+            qa[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
+            qb[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
+        }
+        ct_twiddles<N>(A, twr, twc, tv);
 #pragma unroll
-    for (int k = 0; k < RQ; ++k) {
-        const int q = threadIdx.x + k * NT;
-        if (NQ % NT != 0 && q >= NQ) break;
-        const int p = q / W4, x = (q % W4) * 4;
-        float2 *d = b0 + p * W + x;
-        d[0] = make_float2(qa[k].x, qb[k].x);
-        d[1] = make_float2(qa[k].y, qb[k].y);
-        d[2] = make_float2(qa[k].z, qb[k].z);
-        d[3] = make_float2(qa[k].w, qb[k].w);
+        for (int k = 0; k < RQ; ++k) {
+            const int q = threadIdx.x + k * NT;
+            if (NQ % NT != 0 && q >= NQ) break;
+            const int p = q / W4, x = (q % W4) * 4;
+            float2 *d = b0 + p * W + x;
+            d[0] = make_float2(qa[k].x, qb[k].x);
+            d[1] = make_float2(qa[k].y, qb[k].y);
+            d[2] = make_float2(qa[k].z, qb[k].z);
+            d[3] = make_float2(qa[k].w, qb[k].w);
+        }
+    } else {
+        // the plane in memory order; value (y, x) goes to part y & 1 of row
+        // pair y / 2, and an odd plane's last pair has a zero second row
+        constexpr int NE = P::NE, RL = P::RL;
+        static_assert(RL <= 12, "prologue register budget");
+        float xs[RL];
+#pragma unroll
+        for (int k = 0; k < RL; ++k) xs[k] = src[min((int)threadIdx.x + k * NT, NE - 1)];
+        ct_twiddles<N>(A, twr, twc, tv);
+        float *bf = reinterpret_cast<float *>(b0);
+#pragma unroll
+        for (int k = 0; k < RL; ++k) {
+            const int e = threadIdx.x + k * NT;
+            if (NE % NT != 0 && e >= NE) break;
+            const int y = e / W, x = e % W;
+            bf[2 * ((y >> 1) * W + x) + (y & 1)] = xs[k];
+        }
+        if constexpr (H & 1)
+            for (int x = threadIdx.x; x < W; x += NT) b0[(HP - 1) * W + x].y = 0.f;
     }
     __syncthreads();
-    float2 *r = ct_stockham<W, 1, HP, W, 1, -1>(b0, b1, twr);
+    float2 *r = ct_stockham<W, 1, HP, W, 1, SF, IP>(b0, b1, twr);
     float2 *o = r == b0 ? b1 : b0;
     // split each row pair into the two half spectra
-    for (int idx = threadIdx.x; idx < H * Wh; idx += NT) {
+    auto split = [&](int idx) {
         const int y = idx / Wh, k = idx % Wh, p = y >> 1;
-        const float2 z = r[p * W + k], zm = r[p * W + ((W - k) & (W - 1))];
-        o[idx] = (y & 1) ? make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x))
-                         : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+        const float2 z = r[p * W + k], zm = r[p * W + (k == 0 ? 0 : W - k)];
+        return (y & 1) ? make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x))
+                       : make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+    };
+    if constexpr (IP) {
+        constexpr int IO = (H * Wh + NT - 1) / NT;
+        float2 sv[IO];
+#pragma unroll
+        for (int it = 0; it < IO; ++it) {
+            const int idx = threadIdx.x + it * NT;
+            if ((H * Wh) % NT != 0 && idx >= H * Wh) break;
+            sv[it] = split(idx);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < IO; ++it) {
+            const int idx = threadIdx.x + it * NT;
+            if ((H * Wh) % NT != 0 && idx >= H * Wh) break;
+            o[idx] = sv[it];
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < H * Wh; idx += NT) o[idx] = split(idx);
     }
     __syncthreads();
-    float2 *q = ct_stockham<H, 1, Wh, 1, Wh, -1>(o, r, twc);
+    float2 *q = ct_stockham<H, 1, Wh, 1, Wh, SF, IP>(o, r, twc);
     LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh, *dim = dre + H * Wh;
     for (int idx = threadIdx.x; idx < H * Wh; idx += NT) {
         const float2 v = q[idx];
@@ -711,21 +825,31 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
     }
 }
 
-template <int N>
+template <int N, bool IP>
 __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
 {
-    constexpr int H = N, W = N, Wh = N / 2 + 1, HP = N / 2, NB = lama_fft_nb(N, N), NT = LAMA_FFT_NT;
-    constexpr int N4 = H * W / 4, FP = (N4 + NT - 1) / NT, NS = H * Wh, RS = (NS + NT - 1) / NT;
-    static_assert(2 * N <= NT && FP <= 2 && RS <= 8, "prologue register budget");
-    float2 *b0 = sm, *b1 = sm + NB, *twr = sm + 2 * NB, *twc = twr + W;
+    using P = CtPlane<N>;
+    constexpr int H = P::H, W = P::W, Wh = P::Wh, HP = P::HP, NB = P::NB, NT = P::NT, SF = P::SF;
+    constexpr int NS = H * Wh, RS = (NS + NT - 1) / NT;
+    constexpr int FP = P::VEC ? (H * W / 4 + NT - 1) / NT : P::RL;  // addend float4s or floats per thread
+    static_assert(2 * N <= NT && RS <= 8 && (P::VEC ? FP <= 2 : FP <= 12), "prologue register budget");
+    float2 *b0 = sm, *b1 = IP ? sm : sm + NB, *twr = sm + (IP ? 1 : 2) * NB, *twc = twr + W;
     const int c = blockIdx.x;
     // prologue: twiddles, this block's spectrum and the `f +` addend
     float2 tv = ct_twiddle_fetch<N>(A);
     const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + H * Wh;
-    const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.feat) + (long)c * H * W);
-    float4 fpre[FP];
+    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    using FT = typename std::conditional<P::VEC, float4, float>::type;
+    FT fpre[FP];
+    if constexpr (P::VEC) {
+        constexpr int N4 = H * W / 4;
+        const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(f);
 #pragma unroll
-    for (int k = 0; k < FP; ++k) fpre[k] = f4[min((int)threadIdx.x + k * NT, N4 - 1)];
+        for (int k = 0; k < FP; ++k) fpre[k] = f4[min((int)threadIdx.x + k * NT, N4 - 1)];
+    } else {
+#pragma unroll
+        for (int k = 0; k < FP; ++k) fpre[k] = f[min((int)threadIdx.x + k * NT, P::NE - 1)];
+    }
     float re[RS], im[RS];
 #pragma unroll
     for (int k = 0; k < RS; ++k) {
@@ -737,68 +861,106 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
 #pragma unroll
     for (int k = 0; k < RS; ++k) {
         const int idx = threadIdx.x + k * NT;
-        if (idx >= NS) break;
+        if (NS % NT != 0 && idx >= NS) break;
         b0[idx] = make_float2(re[k], im[k]);
     }
     __syncthreads();
-    float2 *r = ct_stockham<H, 1, Wh, 1, Wh, 1>(b0, b1, twc);
+    float2 *r = ct_stockham<H, 1, Wh, 1, Wh, -SF, IP>(b0, b1, twc);
     float2 *o = r == b0 ? b1 : b0;
-    // Hermitian rows, two per complex transform: z = Ga + i Gb
-    for (int idx = threadIdx.x; idx < HP * W; idx += NT) {
+    // Hermitian rows, two per complex transform: z = Ga + i Gb (an odd
+    // plane's last pair has no second row)
+    auto herm = [&](int idx) {
         const int p = idx / W, x = idx % W;
         float2 g[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int y = 2 * p + h;
-            float2 v;
-            if (x < Wh) {
-                v = r[y * Wh + x];
-                if (x == 0 || 2 * x == W) v.y = 0.f;
-            } else {
-                v = r[y * Wh + (W - x)];
-                v.y = -v.y;
+            float2 v = make_float2(0.f, 0.f);
+            if (!(H & 1) || y < H) {
+                if (x < Wh) {
+                    v = r[y * Wh + x];
+                    if (x == 0 || 2 * x == W) v.y = 0.f;
+                } else {
+                    v = r[y * Wh + (W - x)];
+                    v.y = -v.y;
+                }
             }
             g[h] = v;
         }
-        o[idx] = make_float2(g[0].x - g[1].y, g[0].y + g[1].x);
+        return make_float2(g[0].x - g[1].y, g[0].y + g[1].x);
+    };
+    if constexpr (IP) {
+        constexpr int IO = (HP * W + NT - 1) / NT;
+        float2 hv[IO];
+#pragma unroll
+        for (int it = 0; it < IO; ++it) {
+            const int idx = threadIdx.x + it * NT;
+            if ((HP * W) % NT != 0 && idx >= HP * W) break;
+            hv[it] = herm(idx);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < IO; ++it) {
+            const int idx = threadIdx.x + it * NT;
+            if ((HP * W) % NT != 0 && idx >= HP * W) break;
+            o[idx] = hv[it];
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < HP * W; idx += NT) o[idx] = herm(idx);
     }
     __syncthreads();
-    float2 *q = ct_stockham<W, 1, HP, W, 1, 1>(o, r, twr);
-    LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + (long)c * H * W);
+    float2 *q = ct_stockham<W, 1, HP, W, 1, -SF, IP>(o, r, twr);
+    if constexpr (P::VEC) {
+        constexpr int N4 = H * W / 4;
+        LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + (long)c * H * W);
 #pragma unroll
-    for (int k = 0; k < FP; ++k) {
-        const int i4 = threadIdx.x + k * NT;
-        if (N4 % NT != 0 && i4 >= N4) break;
-        const int idx = i4 * 4, y = idx / W, x = idx % W;
-        const float2 *v = q + (y >> 1) * W + x;
-        float4 o4 = (y & 1) ? make_float4(v[0].y, v[1].y, v[2].y, v[3].y) : make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
-        o4.x = o4.x * A.scale + fpre[k].x;
-        o4.y = o4.y * A.scale + fpre[k].y;
-        o4.z = o4.z * A.scale + fpre[k].z;
-        o4.w = o4.w * A.scale + fpre[k].w;
-        d4[i4] = o4;
+        for (int k = 0; k < FP; ++k) {
+            const int i4 = threadIdx.x + k * NT;
+            if (N4 % NT != 0 && i4 >= N4) break;
+            const int idx = i4 * 4, y = idx / W, x = idx % W;
+            const float2 *v = q + (y >> 1) * W + x;
+            float4 o4 = (y & 1) ? make_float4(v[0].y, v[1].y, v[2].y, v[3].y) : make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
+            o4.x = o4.x * A.scale + fpre[k].x;
+            o4.y = o4.y * A.scale + fpre[k].y;
+            o4.z = o4.z * A.scale + fpre[k].z;
+            o4.w = o4.w * A.scale + fpre[k].w;
+            d4[i4] = o4;
+        }
+    } else {
+        LAMA_GLOBAL float *d = gp(A.out) + (long)c * H * W;
+        const float *qf = reinterpret_cast<const float *>(q);
+#pragma unroll
+        for (int k = 0; k < FP; ++k) {
+            const int e = threadIdx.x + k * NT;
+            if (P::NE % NT != 0 && e >= P::NE) break;
+            const int y = e / W, x = e % W;
+            d[e] = qf[2 * ((y >> 1) * W + x) + (y & 1)] * A.scale + fpre[k];
+        }
     }
 }
 
 }  // namespace
 
-#define LAMA_FFT_CT(N)                                                                                          \
+// IP (in place) must match the host's LDS size for the kernel
+// (Engine::fft_geom: kFftCtInPlace)
+#define LAMA_FFT_CT(N, IP)                                                                                      \
     extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
     {                                                                                                           \
         side_priority();                                                                                        \
         LAMA_STAMP_SCOPE;                                                                                       \
         extern __shared__ float2 sm[];                                                                          \
-        rfft2_ct<N>(*args, sm);                                                                                 \
+        rfft2_ct<N, IP>(*args, sm);                                                                             \
     }                                                                                                           \
     extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
     {                                                                                                           \
         side_priority();                                                                                        \
         LAMA_STAMP_SCOPE;                                                                                       \
         extern __shared__ float2 sm[];                                                                          \
-        irfft2_ct<N>(*args, sm);                                                                                \
+        irfft2_ct<N, IP>(*args, sm);                                                                            \
     }
-LAMA_FFT_CT(64)
-LAMA_FFT_CT(32)
+LAMA_FFT_CT(64, false)
+LAMA_FFT_CT(32, false)
+LAMA_FFT_CT(75, true)
 #undef LAMA_FFT_CT
 
 // ---- split mode with compile-time shapes: square power-of-two planes -------

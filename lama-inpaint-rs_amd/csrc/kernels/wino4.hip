@@ -332,4 +332,5 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
     }
 LAMA_W4_KERNEL(lama_conv3x3w4, 16)
 LAMA_W4_KERNEL(lama_conv3x3w4n, 8)
+LAMA_W4_KERNEL(lama_conv3x3w4q, 4)
 #undef LAMA_W4_KERNEL

@@ -199,6 +199,14 @@ extern "C" int lama_hip_plan_bytes(lama_hip_ctx *ctx, int h, int w, uint64_t *ar
 
 extern "C" int lama_hip_launch_count(lama_hip_ctx *ctx, int h, int w) { return ctx ? ctx->eng.launch_count(h, w) : -1; }
 
+extern "C" int lama_hip_kernel_name(lama_hip_ctx *ctx, int h, int w, int family, char *name, size_t namelen)
+{
+    const char *n = ctx ? ctx->eng.kernel_name(h, w, family) : nullptr;
+    if (!n || !name || std::strlen(n) + 1 > namelen) return 1;
+    std::memcpy(name, n, std::strlen(n) + 1);
+    return 0;
+}
+
 extern "C" int lama_hip_malloc(lama_hip_ctx *ctx, size_t bytes, void **ptr, char *err, size_t errlen)
 {
     GUARD(ctx->eng.check(ctx->eng.hip()->hipMalloc(ptr, bytes), "hipMalloc", e_));

@@ -80,7 +80,11 @@ const char *const kPwAnyName[2] = {"lama_conv1x1_s", "lama_conv1x1_res_s"};
 const char *const kPwV2Name[2] = {"lama_conv1x1_v2", "lama_conv1x1_res_v2"};
 
 // Single-block FFT kernels with the plane shape fixed at compile time.
-const char *const kFftCtName[2][2] = {{"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}};
+const int kFftCtSide[3] = {64, 32, 75};
+// the kernel keeps one plane buffer in LDS, not two (LAMA_FFT_CT's IP)
+const bool kFftCtInPlace[3] = {false, false, true};
+const char *const kFftCtName[3][2] = {
+    {"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}, {"lama_rfft2_75", "lama_irfft2_75"}};
 
 // The first workgroup of each problem after the first, for a grouped launch.
 ProbStarts prob_starts(const ConvProblem *q, size_t n)
@@ -93,12 +97,12 @@ ProbStarts prob_starts(const ConvProblem *q, size_t n)
 
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 // `narrow`: the F(4,3) kernel's 32-pixel blocks.
-void tile_shape(int family, int &tr, int &tc, int wino = 0, bool narrow = false)
+void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
 {
-    if ((family == F_CONV3 || family == F_CONV3G) && wino == 4 && narrow) {  // lama_conv3x3w4n
-        tr = 4;
-        tc = 32;
-    } else if ((family == F_CONV3 || family == F_CONV3G) && wino) {  // lama_conv3x3w / w4: 2 rows x 64 px
+    if ((family == F_CONV3 || family == F_CONV3G) && wino == 4) {  // lama_conv3x3w4 / w4n / w4q
+        tr = 2 << w4v;                                              // 2 x 64, 4 x 32 or 8 x 16
+        tc = 128 / tr;
+    } else if ((family == F_CONV3 || family == F_CONV3G) && wino) {  // lama_conv3x3w: 2 rows x 64 px
         tr = 2;
         tc = 64;
     } else if (family == F_CONV1 || family == F_CONV1R) {
@@ -374,24 +378,24 @@ bool Engine::open(std::string &err)
         scratch_ = d.ptr;
     }
     for (int f = 0; f < F_COUNT; ++f)
-        if (!check(hip_->hipModuleGetFunction(&fn_[f], module_, kKernelName[f]), kKernelName[f], err)) return false;
+        if (!get_fn(fn_[f], kKernelName[f], err)) return false;
     for (int f = 0; f < 4; ++f)
-        if (!check(hip_->hipModuleGetFunction(&fn_split_[f], module_, kSplitName[f]), kSplitName[f], err)) return false;
+        if (!get_fn(fn_split_[f], kSplitName[f], err)) return false;
     for (int s = 0; s < 2; ++s)
         for (int f = 0; f < 4; ++f)
-            if (!check(hip_->hipModuleGetFunction(&fn_split_ct_[s][f], module_, kSplitCtName[s][f]), kSplitCtName[s][f],
-                       err))
+            if (!get_fn(fn_split_ct_[s][f], kSplitCtName[s][f], err))
                 return false;
     for (int f = 0; f < 2; ++f)
-        if (!check(hip_->hipModuleGetFunction(&fn_pw_any_[f], module_, kPwAnyName[f]), kPwAnyName[f], err) ||
-            !check(hip_->hipModuleGetFunction(&fn_pw_v2_[f], module_, kPwV2Name[f]), kPwV2Name[f], err))
+        if (!get_fn(fn_pw_any_[f], kPwAnyName[f], err) ||
+            !get_fn(fn_pw_v2_[f], kPwV2Name[f], err))
             return false;
-    if (!check(hip_->hipModuleGetFunction(&fn_wino_, module_, "lama_conv3x3w"), "lama_conv3x3w", err) ||
-        !check(hip_->hipModuleGetFunction(&fn_wino4_[0], module_, "lama_conv3x3w4"), "lama_conv3x3w4", err) ||
-        !check(hip_->hipModuleGetFunction(&fn_wino4_[1], module_, "lama_conv3x3w4n"), "lama_conv3x3w4n", err) ||
-        !check(hip_->hipModuleGetFunction(&fn_tail_u8_, module_, "lama_tail_u8"), "lama_tail_u8", err) ||
-        !check(hip_->hipModuleGetFunction(&fn_finalize_ks_[0], module_, "lama_finalize10"), "lama_finalize10", err) ||
-        !check(hip_->hipModuleGetFunction(&fn_finalize_ks_[1], module_, "lama_finalize20"), "lama_finalize20", err))
+    if (!get_fn(fn_wino_, "lama_conv3x3w", err) ||
+        !get_fn(fn_wino4_[0], "lama_conv3x3w4", err) ||
+        !get_fn(fn_wino4_[1], "lama_conv3x3w4n", err) ||
+        !get_fn(fn_wino4_[2], "lama_conv3x3w4q", err) ||
+        !get_fn(fn_tail_u8_, "lama_tail_u8", err) ||
+        !get_fn(fn_finalize_ks_[0], "lama_finalize10", err) ||
+        !get_fn(fn_finalize_ks_[1], "lama_finalize20", err))
         return false;
     fn_build_in_ = fn_[F_INPUT];
     if (const char *wv = getenv("LAMA_FFC_WINO")) {
@@ -400,9 +404,9 @@ bool Engine::open(std::string &err)
     }
     if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
-            if (!check(hip_->hipModuleGetFunction(&fn_fft_ct_[s][f], module_, kFftCtName[s][f]), kFftCtName[s][f], err))
+            if (!get_fn(fn_fft_ct_[s][f], kFftCtName[s][f], err))
                 return false;
     {
         int lds = 0;
@@ -602,7 +606,7 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
 hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
 {
-    if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_narrow(probs[0].OW) ? 1 : 0];
+    if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_variant(probs[0].OH, probs[0].OW)];
     if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
     // the widest activation loads every plane of the launch allows
@@ -616,16 +620,26 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
     return vw == 4 ? fn_[family] : vw == 2 ? fn_pw_v2_[family == F_CONV1R] : fn_pw_any_[family == F_CONV1R];
 }
 
-// F(4,3) blocks: 32 pixels x 4 rows unless LAMA_W4_TILE=64 (read at open)
-// selects 64 x 2.  The 32-pixel blocks never waste more columns (75-wide
-// planes use 96 of 128 columns instead of 75 of 128) and stage a quarter
-// fewer input values per output (6 rows x 8 tiles instead of 4 x 16 for 128
-// outputs per channel); measured (passes/s, 32 vs 64): 512x512 252.1 vs
-// 231.3, 600x600 137.8 vs 122.6, 2048x2048 17.90 vs 17.86.
-bool Engine::w4_narrow(int OW) const
+// F(4,3) blocks of 32 Winograd tiles: 2 rows x 64 pixels (lama_conv3x3w4),
+// 4 x 32 (w4n) or 8 x 16 (w4q).  The shape that covers the plane with the
+// fewest blocks, 4 x 32 on a tie; LAMA_W4_TILE=64, 32 or 16 (read at open)
+// forces one.  Measured (passes/s, 32 / 16 / 64-pixel blocks): 512x512
+// 253.6 / 248.6 / 228.7 (32 blocks each for 32 and 16), 600x600 142.7 /
+// 151.1 / 124.9 (75-wide planes: 57 / 50 / 76 blocks), 1024x1024 71.4 /
+// 69.0 / 68.4, 256x256 381.1 / 376.5 / 383.0.
+int Engine::w4_variant(int OH, int OW) const
 {
-    (void)OW;
-    return w4_force_ != 64;
+    if (w4_force_ == 64) return 0;
+    if (w4_force_ == 32) return 1;
+    if (w4_force_ == 16) return 2;
+    auto blocks = [&](int v) {
+        const int tr = 2 << v, tc = 128 / tr;
+        return (long)((OW + tc - 1) / tc) * ((OH + tr - 1) / tr);
+    };
+    int best = 1;
+    for (int v : {2, 0})
+        if (blocks(v) < blocks(best)) best = v;
+    return best;
 }
 
 // The FFC GEMMs' K split: at small planes the F(4,3) launches have few
@@ -639,7 +653,7 @@ int Engine::ksplit_for(int h, int w) const
     if (wino_ != 4) return 1;
     if (ksplit_force_ == 1 || ksplit_force_ == 2 || ksplit_force_ == 4) return ksplit_force_;
     int tr, tc;
-    tile_shape(F_CONV3, tr, tc, 4, w4_narrow(w / 8));
+    tile_shape(F_CONV3, tr, tc, 4, w4_variant(h / 8, w / 8));
     const int tiles = ((w / 8 + tc - 1) / tc) * ((h / 8 + tr - 1) / tr);
     int s = 1;
     while (s < LAMA_KSPLIT_MAX && 16 * tiles * (2 * s) <= 2 * LAMA_CUS) s *= 2;
@@ -658,10 +672,15 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
     const bool fits = std::max((size_t)HP * W, (size_t)H * Wh) <= 8 * (size_t)LAMA_FFT_NT;
     if (!force && fits && g.lds <= std::min<size_t>(max_lds_, 64 * 1024)) {
         g.grid_rows = g.grid_cols = (unsigned)C;  // one block per plane
-        // square 64 or 32 planes have kernels with the shape compiled in
+        // square 64, 32 or 75 planes have kernels with the shape compiled in
         // (LAMA_FFT_GENERIC=1 keeps the runtime-shaped ones, for tests)
         const char *gen = getenv("LAMA_FFT_GENERIC");
-        if (H == W && (H == 64 || H == 32) && !(gen && atoi(gen) == 1)) g.ct = H;
+        if (H == W && !(gen && atoi(gen) == 1))
+            for (int s = 0; s < 3; ++s)
+                if (H == kFftCtSide[s]) {
+                    g.ct = s + 1;
+                    if (kFftCtInPlace[s]) g.lds = ((size_t)lama_fft_nb(H, W) + H + W) * f2;
+                }
         return true;
     }
     // complex values the two ping-pong buffers may hold next to the twiddles
@@ -706,7 +725,7 @@ void Engine::push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int st
     L.nparams = 1;
     L.step_end = -1;
     if (!g.split) {
-        L.fn = g.ct ? fn_fft_ct_[g.ct == 64 ? 0 : 1][inverse ? 1 : 0] : fn_[L.family];
+        L.fn = g.ct ? fn_fft_ct_[g.ct - 1][inverse ? 1 : 0] : fn_[L.family];
         L.grid = g.grid_rows;
         L.shmem = (unsigned)g.lds;
         L.bytes = bytes_a + bytes_b;
@@ -907,7 +926,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc, wino_, w4_narrow(OW));
+        tile_shape(family, tr, tc, wino_, w4_variant(OH, OW));
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
         q.mblocks = (M + 63) / 64;
@@ -935,7 +954,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         for (auto &q : probs) {
             nb += (unsigned)q.nblocks;
             if (q.nblocks != std::max(1, q.ksplit) * q.tiles_x * q.tiles_y * q.mblocks ||
-                (q.ksplit > 1 && (L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1])))
+                (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2]))
                 bad_problem = true;
         }
         // the head kernel walks its tiles: two resident workgroups per CU
@@ -1888,6 +1907,25 @@ int Engine::launch_count(int h, int w)
     return it == plans_.end() ? -1 : (int)it->second.launches.size();
 }
 
+bool Engine::get_fn(hipFunction_t &fn, const char *name, std::string &err)
+{
+    if (!check(hip_->hipModuleGetFunction(&fn, module_, name), name, err)) return false;
+    fn_names_[fn] = name;
+    return true;
+}
+
+const char *Engine::kernel_name(int h, int w, int family) const
+{
+    auto it = plans_.find({h, w});
+    if (it == plans_.end()) return nullptr;
+    for (const Launch &L : it->second.launches)
+        if (L.family == family) {
+            auto n = fn_names_.find(L.fn);
+            return n == fn_names_.end() ? nullptr : n->second;
+        }
+    return nullptr;
+}
+
 void Engine::collect_events()
 {
     for (auto &pe : pending_) {
@@ -2105,7 +2143,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.OH = family == F_CONV1 ? 1 : oh;
     q.OW = family == F_CONV1 ? oh * ow : ow;
     int tr, tc;
-    tile_shape(family, tr, tc, wino, w4_narrow(q.OW));
+    tile_shape(family, tr, tc, wino, w4_variant(q.OH, q.OW));
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
     q.mblocks = (cout + 63) / 64;

@@ -67,7 +67,7 @@ struct FftGeom {
     size_t lds_rows = 0, lds_cols = 0;
     unsigned grid_rows = 0, grid_cols = 0;
     size_t tmp_bytes = 0;           // interleaved complex [C][H][W/2+1]
-    int ct = 0;                     // single-block square plane with compile-time kernels (32 or 64), else 0
+    int ct = 0;                     // single-block square plane with compile-time kernels: 1 + index in kFftCtSide, else 0
     int ct_split = 0;               // split square plane with compile-time kernels (128 or 256), else 0
 };
 
@@ -154,6 +154,9 @@ public:
     bool set_timeline(bool on, std::string &err);
     int timeline_read(lama_launch_time *out, int max, std::string &err);
     int launch_count(int h, int w);
+    // The kernel of the first launch of `family` in the plan at h x w (null
+    // without that plan or launch).
+    const char *kernel_name(int h, int w, int family) const;
     // Device bytes of one forward at h x w: the activation arena of that shape
     // (exact, from its layout) and the resident weights (0 before loading).
     bool plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::string &err);
@@ -170,6 +173,7 @@ public:
     const HipApi *hip() const { return hip_; }
     hipStream_t stream() const { return stream_; }
     bool check(hipError_t e, const char *what, std::string &err);
+    bool get_fn(hipFunction_t &fn, const char *name, std::string &err);  // and records its name
 
 private:
     struct FfcW {
@@ -204,27 +208,28 @@ private:
     const HipApi *hip_ = nullptr;
     int device_ = 0;
     hipModule_t module_ = nullptr;
+    std::map<hipFunction_t, const char *> fn_names_;  // every loaded kernel's name
     hipFunction_t fn_[F_COUNT] = {};
     // split-mode FFT kernels: rfft2 rows, rfft2 cols, irfft2 cols, irfft2 rows
     hipFunction_t fn_split_[4] = {};
     hipFunction_t fn_pw_any_[2] = {};  // 1x1 kernels for planes that are not float4-aligned
     hipFunction_t fn_pw_v2_[2] = {};   // 1x1 kernels for float2-aligned planes of even length
-    hipFunction_t fn_fft_ct_[2][2] = {};  // [64x64, 32x32][rfft2, irfft2]
+    hipFunction_t fn_fft_ct_[3][2] = {};  // [64x64, 32x32, 75x75][rfft2, irfft2]
     hipFunction_t fn_split_ct_[2][4] = {};  // [256x256, 128x128][as fn_split_]
     // FFC 3x3 convolutions as Winograd F(2,3) along x (lama_conv3x3w), or
     // with LAMA_FFC_WINO=0 as the direct implicit GEMM (lama_conv3x3); chosen
     // at open, since the weights are packed for one or the other
     // LAMA_FFC_WINO: 0 direct; 2 F(2,3) (lama_conv3x3w); 4 (default) F(4,3)
-    // in 32-pixel blocks (lama_conv3x3w4n), or 64-pixel ones (lama_conv3x3w4)
-    // with LAMA_W4_TILE=64
+    // in blocks of 2 x 64, 4 x 32 or 8 x 16 output pixels (lama_conv3x3w4,
+    // w4n, w4q), chosen per plane shape
     int wino_ = 4;
-    int w4_force_ = 0;  // LAMA_W4_TILE: 32 or 64 forces the F(4,3) block width
-    bool w4_narrow(int OW) const;
+    int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
+    int w4_variant(int OH, int OW) const;  // index into fn_wino4_
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
     // K split of the FFC GEMMs at input h x w (1 unless the F(4,3) kernels
     // would leave CUs idle)
     int ksplit_for(int h, int w) const;
-    hipFunction_t fn_wino_ = nullptr, fn_wino4_[2] = {};
+    hipFunction_t fn_wino_ = nullptr, fn_wino4_[3] = {};
     hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr, g2l_ = nullptr;

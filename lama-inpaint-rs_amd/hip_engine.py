@@ -54,6 +54,8 @@ def lib():
         L.lama_hip_profile_read_clock.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
                                                   ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_launch_count.argtypes = [vp, ctypes.c_int, ctypes.c_int]
+        L.lama_hip_kernel_name.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_char_p,
+                                           ctypes.c_size_t]
         L.lama_hip_plan_bytes.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
                                           ctypes.POINTER(ctypes.c_uint64), cp, sz]
         L.lama_hip_malloc.argtypes = [vp, sz, ctypes.POINTER(vp), cp, sz]
@@ -252,6 +254,14 @@ class Engine:
 
     def launch_count(self, h, w):
         return lib().lama_hip_launch_count(self.ctx, h, w)
+
+    def kernel_name(self, h, w, family):
+        """The kernel symbol of the first `family` launch of the plan at h x w,
+        or None (no such plan or launch)."""
+        buf = ctypes.create_string_buffer(128)
+        if lib().lama_hip_kernel_name(self.ctx, h, w, FAMILIES.index(family), buf, 128) != 0:
+            return None
+        return buf.value.decode()
 
     def plan_bytes(self, h, w):
         """(activation arena bytes at h x w, resident weight bytes)."""

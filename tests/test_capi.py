@@ -108,6 +108,9 @@ def test_null_context_is_an_error_not_a_crash():
     assert L.lama_hip_synchronize(None, err, 256) == 1 and b"null context" in err.value
     L.lama_hip_launch_count.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
     assert L.lama_hip_launch_count(None, 8, 8) == -1
+    L.lama_hip_kernel_name.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_char_p,
+                                       ctypes.c_size_t]
+    assert L.lama_hip_kernel_name(None, 8, 8, 2, err, 256) == 1
     L.lama_hip_open.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
     assert L.lama_hip_open(None, err, 256) == 1 and b"null output" in err.value
     L.lama_hip_close.argtypes = [ctypes.c_void_p]

@@ -190,10 +190,10 @@ def test_forward_split_forced_matches_single(pkg, engine, monkeypatch):
     assert rel_err(b, a) < 1e-5
 
 
-@pytest.mark.parametrize("size", [256, 512, 1024, 2048])
+@pytest.mark.parametrize("size", [256, 512, 600, 1024, 2048])
 def test_compiled_shape_fft_equals_generic(pkg, engine, monkeypatch, size):
-    """The 32x32 / 64x64 bottleneck planes (256 and 512 inputs) use single-block
-    FFT kernels with the shape compiled in, the 128x128 / 256x256 planes (1024
+    """The 32x32 / 64x64 / 75x75 bottleneck planes (256, 512 and 600 inputs) use
+    single-block FFT kernels with the shape compiled in, the 128x128 / 256x256 planes (1024
     and 2048 inputs) split row/column kernels with the shape compiled in; they
     run the same radix plan as the runtime-shaped kernels (LAMA_FFT_GENERIC=1),
     so the whole forward agrees to float rounding (the compiler contracts a few
@@ -285,10 +285,11 @@ def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal, h,
     assert np.array_equal(u8g[mask == 0], img[mask == 0])
 
 
-@pytest.fixture(scope="module", params=[("2", ""), ("4", "64")], ids=["f23", "f43w64"])
+@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16")],
+                ids=["f23", "f43w64", "f43w32", "f43w16"])
 def w4_forward_engine(pkg, weights_dir, request):
-    """The forward with the non-default Winograd kernels: F(2,3)
-    (LAMA_FFC_WINO=2) and F(4,3) in 64-pixel blocks (LAMA_W4_TILE=64)."""
+    """The forward with each Winograd kernel forced: F(2,3) (LAMA_FFC_WINO=2)
+    and F(4,3) in 64-, 32- or 16-pixel blocks (LAMA_W4_TILE)."""
     with pytest.MonkeyPatch.context() as mp:
         mp.setenv("LAMA_FFC_WINO", request.param[0])
         mp.setenv("LAMA_W4_TILE", request.param[1])
@@ -376,3 +377,22 @@ def test_forward_ksplit_variants_256(pkg, engine, oracle_cal, monkeypatch, ks):
         for s in range(29):
             e = rel_err(got_steps[s], ref_steps[s])
             assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+
+
+@pytest.mark.parametrize("h,w,kernel,fft", [(512, 512, "lama_conv3x3w4n", "lama_rfft2_64"),
+                                            (600, 600, "lama_conv3x3w4q", "lama_rfft2_75"),
+                                            (600, 592, "lama_conv3x3w4q", "lama_rfft2"),
+                                            (256, 256, "lama_conv3x3w4n", "lama_rfft2_32"),
+                                            (16, 1024, "lama_conv3x3w4", "lama_rfft2")])
+def test_ffc_block_shape_per_plane(pkg, engine, h, w, kernel, fft):
+    """The FFC GEMMs take the F(4,3) block shape that covers the bottleneck
+    plane with the fewest blocks of 32 tiles (4 x 32 px on a tie): 75-rows
+    planes 10 x 5 blocks of 8 x 16 instead of 19 x 3 of 4 x 32; a plane of 2
+    rows and 128 columns 2 blocks of 2 x 64 instead of 4 of 4 x 32.  Square
+    32, 64 and 75 planes take the FFT kernels with the shape compiled in."""
+    print(f"case block shape {h}x{w}", flush=True)
+    x = np.zeros((4, h, w), np.float32)
+    engine.forward(x)
+    assert engine.kernel_name(h, w, "conv3x3") == kernel
+    assert engine.kernel_name(h, w, "conv3x3g2l") == kernel
+    assert engine.kernel_name(h, w, "rfft2") == fft

@@ -90,8 +90,8 @@ LARGE = [(256, 256), (128, 128), (200, 130), (150, 90)]
 def fft_mode(request, monkeypatch):
     """'split' forces the row/column launches (LAMA_FFT_SPLIT=1) at every size;
     'generic' keeps the runtime-shaped kernels where a kernel with the plane
-    shape compiled in exists (single-block 32x32 and 64x64, split 128x128 and
-    256x256; LAMA_FFT_GENERIC=1)."""
+    shape compiled in exists (single-block 32x32, 64x64 and 75x75, split
+    128x128 and 256x256; LAMA_FFT_GENERIC=1)."""
     monkeypatch.delenv("LAMA_FFT_SPLIT", raising=False)
     monkeypatch.delenv("LAMA_FFT_GENERIC", raising=False)
     if request.param == "split":
@@ -189,11 +189,12 @@ def test_conv3x3_direct(direct_engine, cin, cout, h, w):
     assert rel_err(got, ref) < TOL
 
 
-@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32")], ids=["f23", "f43w64", "f43w32"])
+@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16")],
+                ids=["f23", "f43w64", "f43w32", "f43w16"])
 def w4_engine(pkg, request):
     """Each Winograd kernel: F(2,3) (LAMA_FFC_WINO=2, lama_conv3x3w) and F(4,3)
-    (LAMA_FFC_WINO=4) with 64- or 32-pixel blocks (LAMA_W4_TILE); both are read
-    when the context opens."""
+    (LAMA_FFC_WINO=4) with 64-, 32- or 16-pixel blocks (LAMA_W4_TILE); both are
+    read when the context opens."""
     with pytest.MonkeyPatch.context() as mp:
         mp.setenv("LAMA_FFC_WINO", request.param[0])
         mp.setenv("LAMA_W4_TILE", request.param[1])
@@ -212,7 +213,7 @@ W4_CASES = WINO_CASES + [
 @pytest.mark.parametrize("cin,cout,h,w", W4_CASES)
 def test_conv3x3_winograd_f43(w4_engine, cin, cout, h, w):
     """The FFC 3x3 convolution as Winograd F(2,3) (lama_conv3x3w) and F(4,3)
-    along x (lama_conv3x3w4 / w4n) against the oracle's direct sum, the same
+    along x (lama_conv3x3w4 / w4n / w4q) against the oracle's direct sum, the same
     1e-5 relative bound: F(4,3)'s larger transform constants round a little
     more than F(2,3)'s."""
     rng = np.random.default_rng(cin * 100 + cout + w)
