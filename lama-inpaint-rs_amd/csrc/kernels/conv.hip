@@ -621,11 +621,14 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
     // (XCD = blockIdx.x mod 8, here b, the launch's only problem), and each
     // XCD has an L2 of its own; giving all M blocks of pixel strip t to XCD
     // t mod 8 makes each strip travel from HBM into one L2 once, instead of
-    // once per M block
-    if (P.tiles_x % 8 == 0) {
+    // once per M block.  The host opts in by sizing the grid for the strips
+    // rounded up to a multiple of 8; blocks of the padding strips return
+    // (the whole workgroup, before any barrier).
+    if (P.nblocks == (P.tiles_x + 7) / 8 * 8 * P.mblocks) {
         const int j = b >> 3;
         mb = j % P.mblocks;
         t = (j / P.mblocks) * 8 + (b & 7);
+        if (t >= P.tiles_x) return;
     }
 #endif
     const int m0 = mb * 64, ox0 = t * C::NPX;

@@ -158,7 +158,8 @@ __device__ __forceinline__ void w4_store(const W4Stage<C> &st, const W4Slots<C> 
 // MFMAs of one chunk for wave (wm, wu): for each (ky, u) of the wave's three
 // positions, lane half g reads its two channels of the weights and of the
 // input (one 8-byte read each) and feeds one to each of two MFMAs as the
-// MFMA's K slot g; the reads of the next (ky, u) are issued first.
+// MFMA's K slot g; the reads of the next (ky, u) are issued first (reading
+// 2, 3 or all 9 steps ahead measured the same).
 template <class C>
 __device__ __forceinline__ void w4_compute(f32x16 (&acc)[C::NUW], const float *lds)
 {
@@ -196,7 +197,13 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
         ks = b / per;
         b -= ks * per;
     }
+#if LAMA_W4_XCD
+    // M-block-major: with the XCD-contiguous launch order, an XCD's blocks
+    // cover few M blocks (each of whose weights its L2 then holds once)
+    const int ntile = P.tiles_x * P.tiles_y, mb = b / ntile, tt = b - mb * ntile;
+#else
     const int mb = b % P.mblocks, tt = b / P.mblocks;
+#endif
     const int tx = tt % P.tiles_x, ty = tt / P.tiles_x;
     const int m0 = mb * 64, oy0 = ty * C::TR, ox0 = tx * C::TC;
     const float ep = epi_param_load(P, m0);
@@ -309,6 +316,31 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
 // accumulators in VGPRs and fits the kernel in 170 registers (220 without
 // the bound), so a third wave -- a SpectralTransform kernel's -- fits on a
 // SIMD beside two of these: 252.2 vs 250.9 passes/s at 512x512.
+// XCD-contiguous launch order: the dispatcher deals workgroups to the eight
+// XCDs round-robin (workgroup i to XCD i mod 8), each XCD with its own L2.
+// Workgroup i takes block x * q + min(x, r) + i / 8 of the launch's natural
+// order (x = i mod 8; the n blocks split as q = n / 8 per XCD, the first
+// r = n mod 8 XCDs one more), so that each XCD works through one contiguous
+// range: with M-block-major problems that is one or two M blocks' weights
+// (0.6 MB each) and one problem's input channels per L2, instead of every
+// M block's weights (A: 4.7 MB against a 4 MB L2) or all 384 global input
+// planes (B: 6.3 MB) in every L2.  LAMA_W4_XCD=0 keeps the natural order.
+#ifndef LAMA_W4_XCD
+#define LAMA_W4_XCD 1
+#endif
+namespace {
+__device__ __forceinline__ int w4_xcd_order(int i, int n)
+{
+#if LAMA_W4_XCD
+    const int x = i & 7, q = n >> 3, r = n & 7;
+    return x * q + min(x, r) + (i >> 3);
+#else
+    (void)n;
+    return i;
+#endif
+}
+}  // namespace
+
 #ifndef LAMA_W4_NUM_VGPR
 #define LAMA_W4_NUM_VGPR 120
 #endif
@@ -325,7 +357,7 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
         using C = W4Cfg<NTR>;                                                              \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                     \
         __shared__ float epl[192];                                                         \
-        int b = blockIdx.x;                                                                \
+        int b = w4_xcd_order(blockIdx.x, gridDim.x);                                       \
         int pi = find_problem(ps, b);                                                      \
         w4_tile<C>(probs[pi], b, lds, epl);                                                \
         LAMA_STAMP_END;                                                                    \

@@ -114,6 +114,17 @@ void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
     }
 }
 
+// Pointwise launches of one problem (one row of pixel strips): the grid holds
+// the strips rounded up to a multiple of 8, so that the kernel's XCD-aware
+// order (all M blocks of strip t on XCD t mod 8) holds for any strip count;
+// the blocks of the padding strips exit at once.
+long pw_xcd_blocks(const ConvProblem &q) { return (long)(q.tiles_x + 7) / 8 * 8 * q.mblocks; }
+void pw_xcd_pad(int family, ConvProblem &q)
+{
+    if (LAMA_PW_XCD && (family == F_CONV1 || family == F_CONV1R) && q.tiles_y == 1 && q.ksplit <= 1)
+        q.nblocks = (int)pw_xcd_blocks(q);
+}
+
 struct WeightSrc {
     const uint8_t *blob;
     size_t len;
@@ -393,6 +404,7 @@ bool Engine::open(std::string &err)
         !get_fn(fn_wino4_[0], "lama_conv3x3w4", err) ||
         !get_fn(fn_wino4_[1], "lama_conv3x3w4n", err) ||
         !get_fn(fn_wino4_[2], "lama_conv3x3w4q", err) ||
+
         !get_fn(fn_tail_u8_, "lama_tail_u8", err) ||
         !get_fn(fn_finalize_ks_[0], "lama_finalize10", err) ||
         !get_fn(fn_finalize_ks_[1], "lama_finalize20", err))
@@ -404,6 +416,7 @@ bool Engine::open(std::string &err)
     }
     if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
+
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
             if (!get_fn(fn_fft_ct_[s][f], kFftCtName[s][f], err))
@@ -945,6 +958,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     auto conv_launch = [&](int family, std::vector<ConvProblem> probs, int step, double flops, double bytes,
                            int stream = S_MAIN, int wait_ev = -1, int record_ev = -1) {
         Launch L{};
+        if (probs.size() == 1) pw_xcd_pad(family, probs[0]);
         L.fn = conv_fn(family, probs.data(), probs.size());
         L.family = family;
         L.stream = stream;
@@ -953,7 +967,9 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         unsigned nb = 0;
         for (auto &q : probs) {
             nb += (unsigned)q.nblocks;
-            if (q.nblocks != std::max(1, q.ksplit) * q.tiles_x * q.tiles_y * q.mblocks ||
+            const bool pw = family == F_CONV1 || family == F_CONV1R;
+            const int tx = pw && q.nblocks == pw_xcd_blocks(q) ? (q.tiles_x + 7) / 8 * 8 : q.tiles_x;
+            if (q.nblocks != std::max(1, q.ksplit) * tx * q.tiles_y * q.mblocks ||
                 (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2]))
                 bad_problem = true;
         }
@@ -1816,8 +1832,9 @@ SpecPlan *Engine::spec_plan_for(int h, int w, std::string &err)
         q.oy_mul = q.ox_mul = 1;
         return q;
     };
-    auto conv = [&](std::vector<Launch> &out, const ConvProblem &q, double flops, double bytes) {
+    auto conv = [&](std::vector<Launch> &out, ConvProblem q, double flops, double bytes) {
         Launch L{};
+        pw_xcd_pad(F_CONV1, q);
         L.fn = conv_fn(F_CONV1, &q, 1);
         L.family = F_CONV1;
         L.stream = S_MAIN;
@@ -2156,6 +2173,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.out_cstride = (long)oh * ow;
     q.outW = q.OW;
     q.oy_mul = q.ox_mul = 1;
+    pw_xcd_pad(family, q);
     UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
     if (!check(hip_->hipMemcpy(dq, &q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
     Launch L{};
