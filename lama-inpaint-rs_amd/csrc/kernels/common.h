@@ -215,8 +215,21 @@ struct FftArgs {
     int rows_per_block;
     float *tmp;
     int cols_per_block;
+    // K-split producers (single-block kernels only): the transform's input
+    // (rfft: the SpectralTransform conv1's output; irfft: the FourierUnit
+    // conv's) and irfft's `feat` (conv1's output) arrive as `np` raw partial
+    // sums `pstride` floats apart; a value is then the in-order sum of its
+    // partials through BN and ReLU, max(sum * scale[ch] + shift[ch], 0), with
+    // ch the plane's output channel of the producer.  np <= 1: plain values.
+    int in_np;    // <= LAMA_PW_KSPLIT_MAX
+    int feat_np;
     int pad_;
+    long in_pstride, feat_pstride;
+    const float *in_scale, *in_shift, *feat_scale, *feat_shift;
 };
+
+// Most K slices of the pointwise convolutions that feed a transform.
+#define LAMA_PW_KSPLIT_MAX 4
 
 // Sum of K-partials + BN + ReLU (+ residual) over [C][plane].
 #ifndef LAMA_G2L_RANGES

@@ -539,7 +539,7 @@ __device__ __forceinline__ float epi_param_load(const ConvProblem &P, int m0)
 
 template <int TR, int TC, bool PREFETCH>
 __device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, const ConvProblem &P, const float *epl,
-                                         int m0, int oy0, int ox0)
+                                         int m0, int oy0, int ox0, long obase = 0)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
@@ -566,7 +566,7 @@ __device__ __forceinline__ void epilogue(const f32x16 &acc, const EpiPre &e, con
             x += gp(P.res)[o];
         v[r] = x;
     }
-    LAMA_GLOBAL float *out = gp(P.out);
+    LAMA_GLOBAL float *out = gp(P.out) + obase;
     const int cbase = m0 + wm * 32 + 4 * g;
     if (m0 + 64 <= P.M) {
 #pragma unroll
@@ -612,9 +612,21 @@ __device__ __forceinline__ void conv_tile(const ConvProblem &P, int b, float *ld
 // One 64 x NPX tile of a pointwise problem (a flat plane: OH == 1).  The
 // epilogue runs once per 32-pixel accumulator; shifting its tile origin by
 // wn*(NPX/2 - 32) + h*32 places accumulator h of wave column wn.
+//
+// K split (P.ksplit > 1, from the host for small planes whose tiles leave
+// most CUs idle): the blocks of slice ks follow those of ks - 1; slice ks
+// walks input channels [ks * kchunks * KC, + kchunks * KC) and stores its raw
+// partial at out + ks * out_kstride (the host clears bias, BN, ReLU, addends
+// and residual; the consumer sums the partials and applies them).
 template <class C, bool PREFETCH, int D>
 __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds, float *epl)
 {
+    int ks = 0;
+    if (P.ksplit > 1) {
+        const int per = P.mblocks * P.tiles_x;
+        ks = b / per;
+        b -= ks * per;
+    }
     int mb = b % P.mblocks, t = b / P.mblocks;
 #if LAMA_PW_XCD
     // XCD-aware order: workgroups are dealt to the eight XCDs round-robin
@@ -624,7 +636,7 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
     // once per M block.  The host opts in by sizing the grid for the strips
     // rounded up to a multiple of 8; blocks of the padding strips return
     // (the whole workgroup, before any barrier).
-    if (P.nblocks == (P.tiles_x + 7) / 8 * 8 * P.mblocks) {
+    if (P.ksplit <= 1 && P.nblocks == (P.tiles_x + 7) / 8 * 8 * P.mblocks) {
         const int j = b >> 3;
         mb = j % P.mblocks;
         t = (j / P.mblocks) * 8 + (b & 7);
@@ -649,12 +661,21 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
     for (int h = 0; h < C::NACC; ++h)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[h][r] = 0.f;
-    run_segment_pw<C, D>(acc, P.s0, m0, P.M, ox0, lds);
+    ConvSeg sg = P.s0;
+    if (P.ksplit > 1) {
+        const int c0 = ks * P.kchunks * C::KC;
+        sg.src += (long)c0 * sg.IH * sg.IW;
+        sg.wt += c0;  // 1x1 rows: chunk k at k * KC floats
+        sg.C -= c0;
+        sg.nchunk = P.kchunks;
+    }
+    run_segment_pw<C, D>(acc, sg, m0, P.M, ox0, lds);
     if (threadIdx.x < 192) epl[threadIdx.x] = ep;
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < C::NACC; ++h)
-        epilogue<1, 64, PREFETCH>(acc[h], pre[h], P, epl, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
+        epilogue<1, 64, PREFETCH>(acc[h], pre[h], P, epl, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32,
+                                  (long)ks * P.out_kstride);
 }
 
 // Problem index of workgroup b, and b made relative to that problem's first

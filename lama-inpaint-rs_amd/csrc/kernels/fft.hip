@@ -48,6 +48,58 @@ __device__ __forceinline__ float2 twd(const float2 *tw, int idx, int sign)
     return w;
 }
 
+// One value of a K-split producer's output plane (FftArgs: np partials
+// pstride apart, in-order sum, BN, ReLU); np <= 1 reads the plain value.
+struct KsIn {
+    int np;
+    long ps;
+    float sc, sh;
+};
+__device__ __forceinline__ KsIn ks_in(int np, long ps, const float *scale, const float *shift, int ch)
+{
+    KsIn k{np, ps, 1.f, 0.f};
+    if (np > 1) {
+        k.sc = gp(scale)[ch];
+        k.sh = gp(shift)[ch];
+    }
+    return k;
+}
+// (up to LAMA_PW_KSPLIT_MAX partials: every load is issued before the sum)
+__device__ __forceinline__ float ks_ld(const LAMA_GLOBAL float *p, long i, const KsIn &k)
+{
+    if (k.np <= 1) return p[i];
+    float u[LAMA_PW_KSPLIT_MAX];
+    u[0] = p[i];
+#pragma unroll
+    for (int j = 1; j < LAMA_PW_KSPLIT_MAX; ++j) u[j] = j < k.np ? p[i + j * k.ps] : 0.f;
+    float v = u[0];
+#pragma unroll
+    for (int j = 1; j < LAMA_PW_KSPLIT_MAX; ++j)
+        if (j < k.np) v += u[j];
+    return fmaxf(v * k.sc + k.sh, 0.f);
+}
+__device__ __forceinline__ float4 ks_ld4(const LAMA_GLOBAL float *p, long i, const KsIn &k)
+{
+    if (k.np <= 1) return *reinterpret_cast<const LAMA_GLOBAL float4 *>(p + i);
+    float4 u[LAMA_PW_KSPLIT_MAX];
+    u[0] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(p + i);
+#pragma unroll
+    for (int j = 1; j < LAMA_PW_KSPLIT_MAX; ++j)
+        u[j] = j < k.np ? float4(*reinterpret_cast<const LAMA_GLOBAL float4 *>(p + i + j * k.ps))
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v = u[0];
+#pragma unroll
+    for (int j = 1; j < LAMA_PW_KSPLIT_MAX; ++j)
+        if (j < k.np) {
+            v.x += u[j].x;
+            v.y += u[j].y;
+            v.z += u[j].z;
+            v.w += u[j].w;
+        }
+    return make_float4(fmaxf(v.x * k.sc + k.sh, 0.f), fmaxf(v.y * k.sc + k.sh, 0.f), fmaxf(v.z * k.sc + k.sh, 0.f),
+                       fmaxf(v.w * k.sc + k.sh, 0.f));
+}
+
 template <int R>
 __device__ __forceinline__ void dft(float2 (&v)[R], int sign);
 
@@ -268,6 +320,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
     TwFetch tw;
     tw.issue(A, threadIdx.x);
     const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
+    const KsIn kin = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, c);
     const int NT = LAMA_FFT_NT;
     if ((W & 3) == 0 && (H & 1) == 0) {  // row pairs as float4 quads
         const int W4 = W >> 2, nq = HP * W4;
@@ -276,8 +329,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
 #pragma unroll
         for (int k = 0; k < RQ; ++k) {
             const int q = min((int)threadIdx.x + k * NT, nq - 1), p = q / W4, x = (q - p * W4) * 4;
-            qa[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
-            qb[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
+            qa[k] = ks_ld4(src, (2 * p) * W + x, kin);
+            qb[k] = ks_ld4(src, (2 * p + 1) * W + x, kin);
         }
         put_twiddles(A, tw, twr, twc);
 #pragma unroll
@@ -298,8 +351,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
 #pragma unroll
         for (int k = 0; k < RS; ++k) {
             const int idx = min((int)threadIdx.x + k * NT, ne - 1), p = idx / W, x = idx - p * W;
-            sa[k] = src[(2 * p) * W + x];
-            sb[k] = src[min(2 * p + 1, H - 1) * W + x];
+            sa[k] = ks_ld(src, (2 * p) * W + x, kin);
+            sb[k] = ks_ld(src, min(2 * p + 1, H - 1) * W + x, kin);
         }
         put_twiddles(A, tw, twr, twc);
 #pragma unroll
@@ -350,20 +403,23 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     tw.issue(A, threadIdx.x);
     const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
     const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    const KsIn kre = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c);
+    const KsIn kim = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c + 1);
+    const KsIn kf = ks_in(A.feat_np, A.feat_pstride, A.feat_scale, A.feat_shift, c);
     const bool vec = (W & 3) == 0;
     const int n4 = (H * W) >> 2, ns = H * Wh;
     constexpr int FP = 2, RS = 8;
     float4 fpre[FP];
     // unaligned planes (W % 4 != 0) fetch a harmless aligned dummy instead
-    const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(vec ? f : gp(A.feat));
+    const LAMA_GLOBAL float *fv = vec ? f : gp(A.feat);
 #pragma unroll
-    for (int k = 0; k < FP; ++k) fpre[k] = f4[vec ? min((int)threadIdx.x + k * NT, max(n4 - 1, 0)) : 0];
+    for (int k = 0; k < FP; ++k) fpre[k] = ks_ld4(fv, 4L * (vec ? min((int)threadIdx.x + k * NT, max(n4 - 1, 0)) : 0), kf);
     float re[RS], im[RS];
 #pragma unroll
     for (int k = 0; k < RS; ++k) {
         const int idx = min((int)threadIdx.x + k * NT, ns - 1);
-        re[k] = sre[idx];
-        im[k] = sim[idx];
+        re[k] = ks_ld(sre, idx, kre);
+        im[k] = ks_ld(sim, idx, kim);
     }
     put_twiddles(A, tw, twr, twc);
 #pragma unroll
@@ -419,13 +475,12 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
             const int i4 = threadIdx.x + k * blockDim.x;
             if (i4 < n4) emit(i4, fpre[k]);
         }
-        for (int i4 = threadIdx.x + FP * blockDim.x; i4 < n4; i4 += blockDim.x)
-            emit(i4, reinterpret_cast<const LAMA_GLOBAL float4 *>(f)[i4]);
+        for (int i4 = threadIdx.x + FP * blockDim.x; i4 < n4; i4 += blockDim.x) emit(i4, ks_ld4(f, 4L * i4, kf));
     } else {
         for (int idx = threadIdx.x; idx < H * W; idx += blockDim.x) {
             const int y = idx / W, x = idx - y * W;
             const float2 v = q[(y >> 1) * W + x];
-            d[idx] = ((y & 1) ? v.y : v.x) * A.scale + f[idx];
+            d[idx] = ((y & 1) ? v.y : v.x) * A.scale + ks_ld(f, idx, kf);
         }
     }
 }
@@ -744,6 +799,7 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
     // prologue: every global load before the first LDS write
     float2 tv = ct_twiddle_fetch<N>(A);
     const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
+    const KsIn kin = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, c);
     if constexpr (P::VEC) {
         constexpr int W4 = W / 4, NQ = HP * W4, RQ = (NQ + NT - 1) / NT;
         static_assert(RQ <= 2, "at most two quads per thread");
@@ -751,8 +807,8 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
 #pragma unroll
         for (int k = 0; k < RQ; ++k) {
             const int q = min((int)threadIdx.x + k * NT, NQ - 1), p = q / W4, x = (q % W4) * 4;
-            qa[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p) * W + x);
-            qb[k] = *reinterpret_cast<const LAMA_GLOBAL float4 *>(src + (2 * p + 1) * W + x);
+            qa[k] = ks_ld4(src, (2 * p) * W + x, kin);
+            qb[k] = ks_ld4(src, (2 * p + 1) * W + x, kin);
         }
         ct_twiddles<N>(A, twr, twc, tv);
 #pragma unroll
@@ -773,7 +829,7 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
         static_assert(RL <= 12, "prologue register budget");
         float xs[RL];
 #pragma unroll
-        for (int k = 0; k < RL; ++k) xs[k] = src[min((int)threadIdx.x + k * NT, NE - 1)];
+        for (int k = 0; k < RL; ++k) xs[k] = ks_ld(src, min((int)threadIdx.x + k * NT, NE - 1), kin);
         ct_twiddles<N>(A, twr, twc, tv);
         float *bf = reinterpret_cast<float *>(b0);
 #pragma unroll
@@ -839,23 +895,25 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
     float2 tv = ct_twiddle_fetch<N>(A);
     const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + H * Wh;
     const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    const KsIn kre = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c);
+    const KsIn kim = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c + 1);
+    const KsIn kf = ks_in(A.feat_np, A.feat_pstride, A.feat_scale, A.feat_shift, c);
     using FT = typename std::conditional<P::VEC, float4, float>::type;
     FT fpre[FP];
     if constexpr (P::VEC) {
         constexpr int N4 = H * W / 4;
-        const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(f);
 #pragma unroll
-        for (int k = 0; k < FP; ++k) fpre[k] = f4[min((int)threadIdx.x + k * NT, N4 - 1)];
+        for (int k = 0; k < FP; ++k) fpre[k] = ks_ld4(f, 4L * min((int)threadIdx.x + k * NT, N4 - 1), kf);
     } else {
 #pragma unroll
-        for (int k = 0; k < FP; ++k) fpre[k] = f[min((int)threadIdx.x + k * NT, P::NE - 1)];
+        for (int k = 0; k < FP; ++k) fpre[k] = ks_ld(f, min((int)threadIdx.x + k * NT, P::NE - 1), kf);
     }
     float re[RS], im[RS];
 #pragma unroll
     for (int k = 0; k < RS; ++k) {
         const int idx = min((int)threadIdx.x + k * NT, NS - 1);
-        re[k] = sre[idx];
-        im[k] = sim[idx];
+        re[k] = ks_ld(sre, idx, kre);
+        im[k] = ks_ld(sim, idx, kim);
     }
     ct_twiddles<N>(A, twr, twc, tv);
 #pragma unroll

@@ -416,6 +416,7 @@ bool Engine::open(std::string &err)
     }
     if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
 
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
@@ -673,6 +674,34 @@ int Engine::ksplit_for(int h, int w) const
     return s;
 }
 
+// The K split of the SpectralTransform's two pointwise convolutions that
+// feed a transform (conv1: 384 -> 192 over the x_g planes; the FourierUnit
+// conv: 384 -> 384 over the spectrum): at small planes their 64 x 64 tiles
+// leave most CUs idle while each wave walks K = 384, so the launch is split
+// into s K slices of raw partials that the single-block transform sums (with
+// the BN + ReLU) while loading them.  The largest s of 1, 2, 4 that keeps the
+// launch within LAMA_PW_KSPLIT_WG workgroups, one per CU; 1 with split-mode
+// transforms.  Measured (passes/s, split / unsplit): 256x256 (s = 4) 411.2 /
+// 384.7; 512x512 with s = 2 (two workgroups per CU) 241.8 / 253.1, so 512x512
+// stays unsplit.  LAMA_PW_KSPLIT=1, 2 or 4 (read at open) forces s.
+#ifndef LAMA_PW_KSPLIT_WG
+#define LAMA_PW_KSPLIT_WG LAMA_CUS
+#endif
+void Engine::pw_ksplit_for(int h, int w, const FftGeom &fg, int &k1, int &ku) const
+{
+    k1 = ku = 1;
+    if (fg.split) return;
+    const long p8 = (long)(h / 8) * (w / 8), ps = (long)(h / 8) * ((w / 8) / 2 + 1);
+    auto pick = [&](long nb) {
+        if (pw_ksplit_force_ == 1 || pw_ksplit_force_ == 2 || pw_ksplit_force_ == 4) return pw_ksplit_force_;
+        int s = 1;
+        while (s < LAMA_PW_KSPLIT_MAX && nb * 2 * s <= LAMA_PW_KSPLIT_WG) s *= 2;
+        return s;
+    };
+    k1 = pick((p8 + 63) / 64 * 3);
+    ku = pick((ps + 63) / 64 * 6);
+}
+
 bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
 {
     const int Wh = W / 2 + 1, HP = (H + 1) / 2;
@@ -811,7 +840,8 @@ bool Engine::upload_plan(const Plan &p, hipStream_t s, std::string &err)
 
 // Byte offsets of every buffer of the per-shape activation arena (each
 // 256-byte aligned) and its total size.
-size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, ArenaLayout &L)
+size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, int pk1, int pku,
+                            ArenaLayout &L)
 {
     const size_t P = (size_t)H * W, P2 = (size_t)(H / 2) * (W / 2), P4 = (size_t)(H / 4) * (W / 4);
     const size_t P8 = (size_t)(H / 8) * (W / 8), PS = (size_t)(H / 8) * ((W / 8) / 2 + 1);
@@ -827,10 +857,10 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.a3 = take(256 * P4 * 4);
     L.x = take(512 * P8 * 4);
     L.y = take(512 * P8 * 4);
-    L.f = take(192 * P8 * 4);
+    L.f = take((size_t)pk1 * 192 * P8 * 4);  // conv1's output (its K partials when split)
     L.g = take(192 * P8 * 4);
     L.s = take(384 * PS * 4);
-    L.s2 = take(384 * PS * 4);
+    L.s2 = take((size_t)pku * 384 * PS * 4);  // the FourierUnit conv's output (partials when split)
     L.out = take(3 * P * 4);
     // the l2g partials (ksplit of them), double-buffered by FFC parity
     L.gc = take(2 * (size_t)ksplit * 384 * P8 * 4);
@@ -845,8 +875,9 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
     L.mask8 = take(P);
     L.out8 = take(3 * P);
     const size_t n_conv = 4 + 36 * 9 + 4 * 3;      // problems
-    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 4;  // descriptor uploads, each 256-byte aligned
-    L.desc = take(n_conv * sizeof(ConvProblem) + 2 * sizeof(FftArgs) + 2 * sizeof(TailArgs) + sizeof(InputArgs) +
+    const size_t n_fft = 2 + 2 * 36;                      // FFT descriptors (per FFC with a pointwise K split)
+    const size_t n_puts = 4 + 36 * 6 + 3 + 3 + 4 + n_fft;  // descriptor uploads, each 256-byte aligned
+    L.desc = take(n_conv * sizeof(ConvProblem) + n_fft * sizeof(FftArgs) + 2 * sizeof(TailArgs) + sizeof(InputArgs) +
                   n_puts * 256 + 4096);
     return off;
 }
@@ -866,7 +897,9 @@ bool Engine::plan_bytes(int h, int w, uint64_t &arena, uint64_t &weights, std::s
     if (!fft_len(w / 8, fr, twr, err) || !fft_len(h / 8, fc, twc, err) || !fft_geom(192, h / 8, w / 8, fg, err))
         return false;
     ArenaLayout lay;
-    arena = arena_layout(h, w, fg, twr.size(), twc.size(), ksplit_for(h, w), lay);
+    int pk1, pku;
+    pw_ksplit_for(h, w, fg, pk1, pku);
+    arena = arena_layout(h, w, fg, twr.size(), twc.size(), ksplit_for(h, w), pk1, pku, lay);
     return true;
 }
 
@@ -889,7 +922,9 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
 
     ArenaLayout lay;
     const int ks = ksplit_for(H, W);
-    p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), ks, lay);
+    int pk1, pku;  // K split of the SpectralTransform conv1 and of the FourierUnit conv
+    pw_ksplit_for(H, W, fg, pk1, pku);
+    p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), ks, pk1, pku, lay);
     const size_t o_in = lay.in, o_a1 = lay.a1, o_a2 = lay.a2, o_a3 = lay.a3, o_x = lay.x, o_y = lay.y, o_f = lay.f,
                  o_g = lay.g, o_s = lay.s, o_s2 = lay.s2, o_out = lay.out, o_gc = lay.gc, o_lq = lay.lq, o_tmp = lay.tmp,
                  o_twr = lay.twr, o_twc = lay.twc, o_desc = lay.desc;
@@ -968,9 +1003,10 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         for (auto &q : probs) {
             nb += (unsigned)q.nblocks;
             const bool pw = family == F_CONV1 || family == F_CONV1R;
-            const int tx = pw && q.nblocks == pw_xcd_blocks(q) ? (q.tiles_x + 7) / 8 * 8 : q.tiles_x;
+            const int tx = pw && q.ksplit <= 1 && q.nblocks == pw_xcd_blocks(q) ? (q.tiles_x + 7) / 8 * 8 : q.tiles_x;
             if (q.nblocks != std::max(1, q.ksplit) * tx * q.tiles_y * q.mblocks ||
-                (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2]))
+                (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2] &&
+                 family != F_CONV1))
                 bad_problem = true;
         }
         // the head kernel walks its tiles: two resident workgroups per CU
@@ -1012,11 +1048,41 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     fa.tmp = fg.split ? (float *)(base + o_tmp) : nullptr;
     fa.in = Fb;
     fa.out = Sb;
+    fa.in_np = fa.feat_np = 1;
     void *d_rfft = put(&fa, sizeof fa);
     fa.in = S2;
     fa.out = G;
     fa.feat = Fb;
     void *d_irfft = put(&fa, sizeof fa);
+    // with a pointwise K split the transforms reduce the partials and apply
+    // the producer's BN + ReLU: one descriptor pair per FFC (its BN)
+    std::vector<void *> d_rfft_k(36, d_rfft), d_irfft_k(36, d_irfft);
+    if (pk1 > 1 || pku > 1)
+        for (int k = 0; k < 36; ++k) {
+            const FfcW &Fw = ffc_[k];
+            FftArgs fk = fa;
+            fk.in = Fb;
+            fk.out = Sb;
+            fk.feat = nullptr;
+            fk.in_np = pk1;
+            fk.in_pstride = (long)192 * P8;
+            fk.in_scale = wp(Fw.bn1);
+            fk.in_shift = wp(Fw.bn1 + 192);
+            fk.feat_np = 1;
+            d_rfft_k[k] = put(&fk, sizeof fk);
+            fk.in = S2;
+            fk.out = G;
+            fk.in_np = pku;
+            fk.in_pstride = (long)384 * PS;
+            fk.in_scale = wp(Fw.fu_bn);
+            fk.in_shift = wp(Fw.fu_bn + 384);
+            fk.feat = Fb;
+            fk.feat_np = pk1;
+            fk.feat_pstride = (long)192 * P8;
+            fk.feat_scale = wp(Fw.bn1);
+            fk.feat_shift = wp(Fw.bn1 + 192);
+            d_irfft_k[k] = put(&fk, sizeof fk);
+        }
 
     // steps 5-22: 18 resblocks = 36 FFCs, ping-ponging X -> Y -> X (+ residual).
     // FFC k's 3x3 convolutions run on the main stream as two grouped launches:
@@ -1128,20 +1194,36 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         L.bytes = f4 * 128 * P8 * (np + 1 + (fa2.res ? 1 : 0));
         p.launches.push_back(L);
     };
+    // a pointwise problem split into s K slices of its chunks: raw partials
+    // s planes apart, reduced (with BN + ReLU) by the consuming transform
+    auto pw_kslices = [&](ConvProblem q, int s, long out_kstride) {
+        if (s > 1) {
+            q = raw(q);
+            q.ksplit = s;
+            q.kchunks = q.s0.nchunk / s;
+            q.out_kstride = out_kstride;
+            q.nblocks *= s;
+            if (q.kchunks * s != q.s0.nchunk) bad_problem = true;
+        }
+        return q;
+    };
     auto launch_spectral = [&](int k) {
         const FfcW &Fw = ffc_[k];
         // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
         conv_launch(F_CONV1,
-                    {problem(F_CONV1, seg(ffc_src(k) + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8, Fw.bn1,
-                             192, Fb, P8, (int)P8, nullptr)},
-                    -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + 192 * P8 + 192 * 384), S_SIDE, k == 0 ? EV_FORK : -1);
-        push_fft(p, false, fg, d_rfft, S_SIDE, f4 * 192 * P8, 8.0 * 192 * PS);
+                    {pw_kslices(problem(F_CONV1, seg(ffc_src(k) + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8,
+                                        Fw.bn1, 192, Fb, P8, (int)P8, nullptr),
+                                pk1, (long)192 * P8)},
+                    -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + pk1 * 192 * P8 + 192 * 384), S_SIDE,
+                    k == 0 ? EV_FORK : -1);
+        push_fft(p, false, fg, d_rfft_k[k], S_SIDE, f4 * pk1 * 192 * P8, 8.0 * 192 * PS);
         // FourierUnit conv over the stacked spectrum + BN + ReLU
         conv_launch(F_CONV1,
-                    {problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS, (int)PS,
-                             nullptr)},
-                    -1, 2.0 * 384 * 384 * PS, f4 * (2 * 384 * PS + 384 * 384), S_SIDE);
-        push_fft(p, true, fg, d_irfft, S_SIDE, 8.0 * 192 * PS, 2 * f4 * 192 * P8);  // + the fused feat read
+                    {pw_kslices(problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS,
+                                        (int)PS, nullptr),
+                                pku, (long)384 * PS)},
+                    -1, 2.0 * 384 * 384 * PS, f4 * ((1 + pku) * 384 * PS + 384 * 384), S_SIDE);
+        push_fft(p, true, fg, d_irfft_k[k], S_SIDE, 8.0 * pku * 192 * PS, (1 + pk1) * f4 * 192 * P8);  // + the fused feat read
     };
     auto launch_conv2 = [&](int k) {
         const FfcW &Fw = ffc_[k];

@@ -196,7 +196,8 @@ private:
     SpecPlan *spec_plan_for(int h, int w, std::string &err);
     bool step_hooks(Plan &p, const float *in, std::string &err);
     bool replay(Plan &p, hipStream_t s, std::string &err);
-    static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, ArenaLayout &L);
+    static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, int pk1, int pku,
+                               ArenaLayout &L);
     bool use_graph() const;
     void free_plan(Plan &p);
     bool launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record = nullptr);
@@ -226,6 +227,9 @@ private:
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
+    int pw_ksplit_force_ = 0;  // LAMA_PW_KSPLIT: 1, 2 or 4 forces the K split of conv1 and the FourierUnit conv
+    // K split of the SpectralTransform conv1 (k1) and FourierUnit conv (ku)
+    void pw_ksplit_for(int h, int w, const FftGeom &fg, int &k1, int &ku) const;
     // K split of the FFC GEMMs at input h x w (1 unless the F(4,3) kernels
     // would leave CUs idle)
     int ksplit_for(int h, int w) const;
