@@ -14,6 +14,7 @@ host's cores on one bounded pass).
 """
 import argparse
 import json
+import subprocess
 import os
 import sys
 import tempfile
@@ -233,8 +234,20 @@ def main():
                         break
         except OSError:
             pass
+        # lscpu's identification lines, where the box has the tool
+        lscpu = {}
+        try:
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+            for ln in out.splitlines():
+                k, _, v = ln.partition(":")
+                if k.strip() in ("Model name", "Vendor ID", "CPU family", "Model", "Stepping", "CPU(s)",
+                                 "Thread(s) per core", "Core(s) per socket", "Socket(s)", "CPU max MHz",
+                                 "L3 cache", "Hypervisor vendor", "Virtualization type"):
+                    lscpu[k.strip()] = v.strip()
+        except (OSError, subprocess.SubprocessError):
+            pass
         cpu = {"value": round(scale / cpu_s, 5), "unit": "passes/s", "cores": O.lib().or_num_threads(),
-               "cpu_model": cpu_model, "kind": "port",
+               "cpu_model": cpu_model, "lscpu": lscpu, "kind": "port",
                "sample": f"one {cs}x{cs} whole-image pass of the C restatement of cpu.rs "
                          f"(-O3 -ffp-contract=off, OpenMP), {cpu_s:.2f} s"
                          + ("" if cs == S else f", scaled by pixel count to {S}x{S}")}

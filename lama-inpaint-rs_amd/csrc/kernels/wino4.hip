@@ -36,6 +36,14 @@
 
 namespace {
 
+// LDS padding: floats after each weight row (a multiple of 4: the rows are
+// stored as float4s) and after each staged input row (even: read as float2s)
+#ifndef LAMA_W4_WPAD
+#define LAMA_W4_WPAD 4
+#endif
+#ifndef LAMA_W4_VPAD
+#define LAMA_W4_VPAD 0
+#endif
 template <int NTR_>
 struct W4Cfg {
     static constexpr int KC = LAMA_WINO_KC;      // input channels per chunk
@@ -47,13 +55,14 @@ struct W4Cfg {
     static constexpr int IR = TR + 2;            // input rows per block
     static constexpr int WK = NU * KY * KC;      // weights per output channel and chunk (72)
     static constexpr int WKP = LAMA_WINO4_WKP;   // packed (padded) weights per channel and chunk
-    static constexpr int WSTR = WKP + 4;         // LDS row stride (= 4 mod 8)
+    static constexpr int WSTR = WKP + LAMA_W4_WPAD;  // LDS row stride of the weights
     static constexpr int H = KC / 2;             // channels per lane half and MFMA K slot
     static constexpr int KCP = KC + 2;           // LDS floats per (row, u, tile)
     static constexpr int W_LDS = 64 * WSTR;
     static constexpr int NITEM = KC * IR * NTR;  // (ci, row, tile) input items per chunk
     static constexpr int VITER = (NITEM + LAMA_NT - 1) / LAMA_NT;
-    static constexpr int V_LDS = IR * NU * NTR * KCP + NU * 64;  // + a dummy tail for items past NITEM
+    static constexpr int VRS = NU * NTR * KCP + LAMA_W4_VPAD;  // LDS stride of an input row
+    static constexpr int V_LDS = IR * VRS + NU * 64;  // + a dummy tail for items past NITEM
     static constexpr int LDS = W_LDS + V_LDS;    // floats per stage
     static constexpr int WITER = 64 * WKP / 4 / LAMA_NT;  // weight float4s per thread
     // epilogue exchange: per channel half, two pixels x 16 registers x 64 lanes from each position half
@@ -101,8 +110,7 @@ __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int 
             const int ix = reflect1(ox0 + 4 * t - 1 + c, sg.IW);
             sl.po[it][c] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + ix));
         }
-        sl.vl[it] = idx < C::NITEM ? (r * C::NU * C::NTR + t) * C::KCP + ci
-                                   : C::IR * C::NU * C::NTR * C::KCP + (idx - C::NITEM) % 64;
+        sl.vl[it] = idx < C::NITEM ? r * C::VRS + t * C::KCP + ci : C::IR * C::VRS + (idx - C::NITEM) % 64;
     }
 }
 
@@ -145,7 +153,7 @@ __device__ __forceinline__ void w4_store(const W4Stage<C> &st, const W4Slots<C> 
                     d5 = st.d[it][5];
         const int o = sl.vl[it];
         // dummy items (o in the tail) write six words within the tail's 6 * 64
-        const int st_ = o >= C::IR * C::NU * C::NTR * C::KCP ? 64 : S;
+        const int st_ = o >= C::IR * C::VRS ? 64 : S;
         vl[o] = 4.f * d0 - 5.f * d2 + d4;
         vl[o + st_] = d3 + d4 - 4.f * (d1 + d2);
         vl[o + 2 * st_] = 4.f * (d1 - d2) - d3 + d4;
@@ -172,7 +180,7 @@ __device__ __forceinline__ void w4_compute(f32x16 (&acc)[C::NUW], const float *l
     auto rd = [&](int s, int buf) {
         const int ky = s / C::NUW, u = C::NUW * wu + s % C::NUW;
         lds_vec<C::H>(a[buf], wrow + (u * C::KY + ky) * C::KC);
-        lds_vec<C::H>(b[buf], vrow + ((r + ky) * C::NU + u) * C::NTR * C::KCP);
+        lds_vec<C::H>(b[buf], vrow + (r + ky) * C::VRS + u * C::NTR * C::KCP);
     };
     rd(0, 0);
 #pragma unroll

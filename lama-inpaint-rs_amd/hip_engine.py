@@ -54,6 +54,8 @@ def lib():
         L.lama_hip_profile_read_clock.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
                                                   ctypes.POINTER(ctypes.c_double)]
         L.lama_hip_launch_count.argtypes = [vp, ctypes.c_int, ctypes.c_int]
+        L.lama_hip_plan_signature.argtypes = []
+        L.lama_hip_plan_signature.restype = cp
         L.lama_hip_kernel_name.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_char_p,
                                            ctypes.c_size_t]
         L.lama_hip_plan_bytes.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64),
@@ -333,10 +335,20 @@ def vram():
 _ENGINE = None
 
 
+def plan_signature():
+    """model::describe (model.rs:260-274) of the plan the backend hard-codes."""
+    return lib().lama_hip_plan_signature().decode()
+
+
 def run(store, model, input, h, w):
     """cuda::run: one forward over [4][h][w] -> [3][h][w] with a
-    process-wide engine whose weights stay resident (cuda.rs:222-231)."""
+    process-wide engine whose weights stay resident (cuda.rs:222-231).
+    `model` is None or the model's describe() line; a line other than the
+    backend's plan signature is refused before any device work, as a plan
+    mismatch rather than a later tensor-shape error."""
     global _ENGINE
+    if model is not None and str(model) != plan_signature():
+        raise HipError(f"hip backend: plan mismatch (model: {model}; backend: {plan_signature()})")
     if _ENGINE is None or getattr(_ENGINE, "_store", None) is not store:
         if _ENGINE is None:
             _ENGINE = Engine()

@@ -7,6 +7,7 @@ import re
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -125,3 +126,15 @@ def test_plan_signature_is_the_reference_describe_of_big_lama():
     L.lama_hip_plan_signature.restype = ctypes.c_char_p
     steps = 1 + 4 + 18 + 1 + 3 + 1 + 1
     assert L.lama_hip_plan_signature().decode() == f"{steps} steps, {4 + 2 * 18} FFC_BN_ACT calls, 18 resblocks"
+
+
+def test_run_refuses_another_network_before_any_device_work(pkg):
+    """hip_engine.run mirrors the Rust binding's plan check: a model whose
+    describe() line differs from the backend's plan signature is refused as a
+    plan mismatch, before a context is opened (no GPU needed to see it)."""
+    E = pkg.hip_engine
+    sig = E.plan_signature()
+    assert sig.startswith("29 steps, 40 FFC_BN_ACT calls")
+    other = "29 steps, 38 FFC_BN_ACT calls, 17 resblocks"
+    with pytest.raises(E.HipError, match="plan mismatch"):
+        E.run(None, other, np.zeros((4, 8, 8), np.float32), 8, 8)
