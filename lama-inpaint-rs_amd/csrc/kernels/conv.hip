@@ -799,6 +799,31 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(LAMA_CONV_PAR
     LAMA_STAMP_END;
 }
 
+// XCD-contiguous order within each problem of the stride-2 and transposed
+// convolutions: the dispatcher deals workgroups to the eight XCDs
+// round-robin (workgroup i to XCD i mod 8), each XCD with its own L2.  Block j
+// of a problem of n blocks (which starts at a multiple of 8) is replaced by
+// block x * q + min(x, r) + j / 8 (x = j mod 8, q = n / 8, r = n mod 8), so
+// each XCD works through a contiguous range of tiles with all their M blocks
+// (M blocks vary fastest): an input tile is fetched into one L2 instead of
+// into every XCD that holds one of its M blocks (model.4's 8 M blocks fell on
+// the 8 XCDs, and each XCD read the whole input).  Per problem, so that the
+// four transposed-convolution phases (1, 2, 2 and 4 taps) are spread evenly
+// over the XCDs, and an XCD's share of each phase covers the same input rows.
+#ifndef LAMA_CONV_XCD
+#define LAMA_CONV_XCD 1
+#endif
+__device__ __forceinline__ int conv_xcd_order(int i, int n)
+{
+#if LAMA_CONV_XCD
+    const int x = i & 7, q = n >> 3, r = n & 7;
+    return x * q + min(x, r) + (i >> 3);
+#else
+    (void)n;
+    return i;
+#endif
+}
+
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
 extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_PARAMS)
 {
@@ -808,6 +833,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_P
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
+    b = conv_xcd_order(b, probs[pi].nblocks);
     conv_tile<CfgDown, false>(probs[pi], b, lds, epl);
     LAMA_STAMP_END;
 }
@@ -869,6 +895,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(LAMA_CONV_PARAM
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
+    b = conv_xcd_order(b, probs[pi].nblocks);
     switch (pi) {
     case 0: conv_tile<CfgT00, false>(probs[0], b, lds, epl); break;
     case 1: conv_tile<CfgT01, false>(probs[1], b, lds, epl); break;
