@@ -18,6 +18,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CLI = os.path.join(ROOT, "lama-inpaint-rs_amd", "bin", "lama-inpaint")
 
 
+# The reference's own inputs (testdata/in.png and testdata/mask.png), kept as fixtures:
+# a 512 x 512 photograph with a 38,000-pixel hole inside the box x 150-469, y 60-329.
+TD_IMG = os.path.join(ROOT, "tests", "golden", "testdata_in.png")
+TD_MASK = os.path.join(ROOT, "tests", "golden", "testdata_mask.png")
+
+
 def run_cli(*args, stdin=None, timeout=300):
     return subprocess.run([CLI, *args], capture_output=True, timeout=timeout, input=stdin)
 
@@ -98,6 +104,39 @@ def test_empty_mask_tile_and_sections_copy_the_input(H, tmp_path, weights_dir):
         assert r.returncode == 0, r.stderr
         assert b"mask is empty" in r.stderr
         assert np.array_equal(H.png_read_rgb(out), img)
+
+
+def test_reference_testdata_geometry(H):
+    """The --tile and --sections geometry on the reference's own inputs.
+    --tile wants a window twice the 320-pixel box, which the 512-pixel image
+    caps, so the window is the whole image (main.rs:740-790).  --sections cuts
+    the box into 256-pixel cells from its top-left corner, clipped to the box,
+    keeps those holding hole pixels and orders them by the shallowest hole
+    pixel's 4-connected distance to the rim, then y0, x0 (main.rs:597-659).
+    The distance is the taxicab distance transform of the zero-padded mask
+    less one: the nearest unmasked pixel in L1 is reached by a monotone path
+    through masked pixels, so the breadth-first depth equals it."""
+    from scipy.ndimage import distance_transform_cdt
+    img, mask = H.png_read_rgb(TD_IMG), H.png_read_gray(TD_MASK)
+    assert img.shape == (512, 512, 3) and mask.shape == (512, 512)
+    ys, xs = np.nonzero(mask)
+    assert len(xs) == 38000 and (xs.min(), xs.max(), ys.min(), ys.max()) == (150, 469, 60, 329)
+    t = H.tile_rect(mask)
+    assert (t.x0, t.y0, t.side) == (0, 0, 512)
+
+    hole = mask > 0
+    depth = distance_transform_cdt(np.pad(hole, 1), metric="taxicab")[1:-1, 1:-1] - 1
+    assert np.array_equal(H.mask_depth(mask)[hole], depth[hole])
+    cells = [(x0, y0, min(x0 + 256, 470), min(y0 + 256, 330)) for y0 in (60, 316) for x0 in (150, 406)]
+    cells = [c for c in cells if hole[c[1]:c[3], c[0]:c[2]].any()]
+    secs = H.section_rects(mask)
+    assert len(secs) == 3 and sorted(secs) == sorted(cells)
+    cover = np.zeros(mask.shape, int)
+    for x0, y0, x1, y1 in secs:
+        cover[y0:y1, x0:x1] += 1
+    assert np.all(cover[hole] == 1)
+    keys = [(int(depth[y0:y1, x0:x1][hole[y0:y1, x0:x1]].min()), y0, x0) for x0, y0, x1, y1 in secs]
+    assert keys == sorted(keys)
 
 
 # ------------------------------------------------------------------ GPU
@@ -186,6 +225,35 @@ def test_cli_sections_equal_the_restated_pass_loop(H, engine, tmp_path, weights_
     assert np.array_equal(got, _sections_by_hand(H, engine, img, mask))
     assert np.array_equal(got[mask == 0], img[mask == 0])
     assert len(list(dump.iterdir())) == 9
+
+
+@pytest.mark.gpu
+def test_cli_reference_testdata_whole_tile_sections(H, engine, tmp_path, weights_dir):
+    """The reference's own image and mask through the whole-image, --tile and
+    --sections flows.  Unmasked pixels come back bit-exact in all three; the
+    --tile window is the whole image, so its output equals the whole-image
+    pass; --sections equals the restated pass loop; the whole-image pass is
+    within 1/255 (max) and 0.1 (mean) of the CPU oracle's."""
+    import oracle_api as O
+    img, mask = H.png_read_rgb(TD_IMG), H.png_read_gray(TD_MASK)
+    outs = {}
+    for flag in ("", "--tile", "--sections"):
+        print(f"case testdata 512x512 {flag or 'whole image'}", flush=True)
+        out = str(tmp_path / f"o{flag}.png")
+        r = run_cli("--image", TD_IMG, "--mask", TD_MASK, "--output", out, "--weights", weights_dir["cal"], "--gpu",
+                    *([flag] if flag else []))
+        assert r.returncode == 0, r.stderr
+        got = H.png_read_rgb(out)
+        assert np.array_equal(got[mask == 0], img[mask == 0])
+        outs[flag] = (got, r.stderr)
+    assert b"tile: 512x512 window" in outs["--tile"][1]
+    assert np.array_equal(outs["--tile"][0], outs[""][0])
+    assert b"sections: 3 passes, 512x512 window each" in outs["--sections"][1]
+    assert np.array_equal(outs["--sections"][0], _sections_by_hand(H, engine, img, mask))
+    x = O.build_input(img, mask, 0, 0)
+    ref = O.composite(img, mask, O.OracleNet(O.read_safetensors(weights_dir["cal"])).forward(x), 0, 0)
+    d = np.abs(outs[""][0].astype(int) - ref.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1
 
 
 @pytest.mark.gpu
