@@ -230,10 +230,11 @@ def test_cli_sections_equal_the_restated_pass_loop(H, engine, tmp_path, weights_
 @pytest.mark.gpu
 def test_cli_reference_testdata_whole_tile_sections(H, engine, tmp_path, weights_dir):
     """The reference's own image and mask through the whole-image, --tile and
-    --sections flows.  Unmasked pixels come back bit-exact in all three; the
+    --sections flows.  Unmasked pixels come back bit-exact in all three.  The
     --tile window is the whole image, so its output equals the whole-image
-    pass; --sections equals the restated pass loop; the whole-image pass is
-    within 1/255 (max) and 0.1 (mean) of the CPU oracle's."""
+    pass; --sections on an image whose short side is at most 512 runs the
+    whole image (main.rs:244-251).  The whole-image pass is within 1/255 (max)
+    and 0.1 (mean) of the CPU oracle's."""
     import oracle_api as O
     img, mask = H.png_read_rgb(TD_IMG), H.png_read_gray(TD_MASK)
     outs = {}
@@ -246,14 +247,38 @@ def test_cli_reference_testdata_whole_tile_sections(H, engine, tmp_path, weights
         got = H.png_read_rgb(out)
         assert np.array_equal(got[mask == 0], img[mask == 0])
         outs[flag] = (got, r.stderr)
-    assert b"tile: 512x512 window" in outs["--tile"][1]
+    assert b"tile: 512x512 window at (0,0) covering a 320x270 mask" in outs["--tile"][1]
     assert np.array_equal(outs["--tile"][0], outs[""][0])
-    assert b"sections: 3 passes, 512x512 window each" in outs["--sections"][1]
-    assert np.array_equal(outs["--sections"][0], _sections_by_hand(H, engine, img, mask))
+    assert b"at or below 512px on its short side; running the whole image" in outs["--sections"][1]
+    assert np.array_equal(outs["--sections"][0], outs[""][0])
     x = O.build_input(img, mask, 0, 0)
     ref = O.composite(img, mask, O.OracleNet(O.read_safetensors(weights_dir["cal"])).forward(x), 0, 0)
     d = np.abs(outs[""][0].astype(int) - ref.astype(int))
     assert d.max() <= 1 and d.mean() <= 0.1
+
+
+@pytest.mark.gpu
+def test_cli_reference_testdata_in_a_larger_frame(H, engine, tmp_path, weights_dir):
+    """The reference's image and mask set into a 700 x 660 frame (so that
+    --sections cuts the real hole into its 3 sections): --sections equals the
+    restated pass loop and --tile the crop-run-paste, bit for bit, with the
+    frame's pixels and the unmasked image pixels untouched."""
+    img, mask = H.png_read_rgb(TD_IMG), H.png_read_gray(TD_MASK)
+    big = H.synth_image(700, 660, 9)
+    bmask = np.zeros((700, 660), np.uint8)
+    big[100:612, 80:592], bmask[100:612, 80:592] = img, mask
+    ip, mp = write_case(H, str(tmp_path), big, bmask)
+    for flag, want in (("--sections", lambda: _sections_by_hand(H, engine, big, bmask)),
+                       ("--tile", lambda: _tile_by_hand(H, engine, big, bmask))):
+        print(f"case testdata in 700x660 {flag}", flush=True)
+        out = str(tmp_path / f"o{flag}.png")
+        r = run_cli("--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["cal"], flag)
+        assert r.returncode == 0, r.stderr
+        got = H.png_read_rgb(out)
+        assert np.array_equal(got[bmask == 0], big[bmask == 0])
+        assert np.array_equal(got, want())
+        if flag == "--sections":
+            assert b"sections: 3 passes, 512x512 window each" in r.stderr
 
 
 @pytest.mark.gpu
