@@ -8,67 +8,83 @@
 
 #include "common.h"
 
-// NP partials, a compile-time count: every load is issued before any
-// arithmetic, and the partials are summed in order
-template <int NP>
+// One block per (channel, G * 1024-element segment of its plane): the channel
+// and its BN scale and shift are block-uniform (no per-element division).
+// Each thread takes G groups of 4 consecutive elements, 1024 apart, with
+// 16-byte accesses that need only 4-byte alignment (a plane need not be a
+// multiple of 4).  A group that runs past the plane reads the plane's last 4
+// elements instead (a clamped window, so every load is issued before any
+// arithmetic, without branches) and stores only its own elements.  The NP
+// partials are summed in order.
+typedef float f4a4 __attribute__((ext_vector_type(4), aligned(4)));
+template <int NP, int G>
 __device__ __forceinline__ void finalize_body(const FinalizeArgs &A)
 {
-    const long n = (long)A.C * A.plane;
-    const long i = ((long)blockIdx.x * LAMA_NT + threadIdx.x) * 4;
-    if (i >= n) return;
-    long idx[4];
-    int ch[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        idx[e] = min(i + e, n - 1);
-        ch[e] = (int)(idx[e] / A.plane);
+    constexpr int SEG = 4 * LAMA_NT * G;
+    const int plane = (int)A.plane;
+    const int segs = (plane + SEG - 1) / SEG;
+    const int c = blockIdx.x / segs, j0 = (blockIdx.x - c * segs) * SEG + 4 * threadIdx.x;
+    if (c >= A.C || j0 >= plane) return;
+    const float sc = gp(A.scale)[c], sh = gp(A.shift)[c];
+    const long cb = (long)c * plane;
+    if (plane < 4) {  // planes of 1 to 3 pixels: one element at a time
+        for (int j = j0; j < min(j0 + 4, plane); ++j) {
+            float v = 0.f;
+            for (int q = 0; q < NP; ++q) v += gp(A.part[q])[cb + j];
+            float x = fmaxf(v * sc + sh, 0.f);
+            if (A.res) x += gp(A.res)[cb + j];
+            gp(A.out)[cb + j] = x;
+        }
+        return;
     }
-    float part[NP][4], sc[4], sh[4], rs[4];
+    int jw[G];
+    f4a4 part[G][NP], rs[G];
 #pragma unroll
-    for (int q = 0; q < NP; ++q) {
-        const LAMA_GLOBAL float *pq = gp(A.part[q]);
+    for (int g = 0; g < G; ++g) {
+        jw[g] = min(j0 + 4 * LAMA_NT * g, plane - 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) part[q][e] = pq[idx[e]];
+        for (int q = 0; q < NP; ++q) part[g][q] = *(const LAMA_GLOBAL f4a4 *)(gp(A.part[q]) + cb + jw[g]);
+        if (A.res) rs[g] = *(const LAMA_GLOBAL f4a4 *)(gp(A.res) + cb + jw[g]);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        sc[e] = gp(A.scale)[ch[e]];
-        sh[e] = gp(A.shift)[ch[e]];
-    }
-    if (A.res) {
+    for (int g = 0; g < G; ++g) {
+        f4a4 out;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) rs[e] = gp(A.res)[idx[e]];
-    }
-    float out[4];
+        for (int e = 0; e < 4; ++e) {
+            float v = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float v = 0.f;
+            for (int q = 0; q < NP; ++q) v += part[g][q][e];
+            float x = fmaxf(v * sc + sh, 0.f);
+            if (A.res) x += rs[g][e];
+            out[e] = x;
+        }
+        const int j = j0 + 4 * LAMA_NT * g;
+        LAMA_GLOBAL float *o = gp(A.out) + cb + jw[g];
+        if (j + 4 <= plane) {
+            *(LAMA_GLOBAL f4a4 *)o = out;
+        } else if (j < plane) {  // the window's elements from j on
 #pragma unroll
-        for (int q = 0; q < NP; ++q) v += part[q][e];
-        float x = fmaxf(v * sc[e] + sh[e], 0.f);
-        if (A.res) x += rs[e];
-        out[e] = x;
-    }
-    LAMA_GLOBAL float *o = gp(A.out);
-    if (i + 4 <= n) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[i + e] = out[e];
-    } else {
-        for (int e = 0; e < (int)(n - i); ++e) o[i + e] = out[e];
+            for (int e = 0; e < 4; ++e)
+                if (jw[g] + e >= j) o[e] = out[e];
+        }
     }
 }
 
 // The FFC local branch's finish over 5, 10 or 20 partials (K split 1, 2, 4),
-// one kernel each so that each holds only its own partials in registers.
-#define LAMA_FINALIZE(NAME, NP)                                                                                   \
+// one kernel each so that each holds only its own partials in registers; the
+// _g2 kernels take two groups per thread (half the blocks).
+#define LAMA_FINALIZE(NAME, NP, G)                                                                                \
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(const FinalizeArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
     {                                                                                                            \
         LAMA_STAMP_SCOPE;                                                                                        \
-        finalize_body<NP>(*args);                                                                                \
+        finalize_body<NP, G>(*args);                                                                             \
     }
-LAMA_FINALIZE(lama_finalize, LAMA_FIN_PARTS)
-LAMA_FINALIZE(lama_finalize10, 2 * LAMA_FIN_PARTS)
-LAMA_FINALIZE(lama_finalize20, 4 * LAMA_FIN_PARTS)
+LAMA_FINALIZE(lama_finalize, LAMA_FIN_PARTS, 1)
+LAMA_FINALIZE(lama_finalize10, 2 * LAMA_FIN_PARTS, 1)
+LAMA_FINALIZE(lama_finalize20, 4 * LAMA_FIN_PARTS, 1)
+LAMA_FINALIZE(lama_finalize_g2, LAMA_FIN_PARTS, 2)
+LAMA_FINALIZE(lama_finalize10_g2, 2 * LAMA_FIN_PARTS, 2)
+LAMA_FINALIZE(lama_finalize20_g2, 4 * LAMA_FIN_PARTS, 2)
 #undef LAMA_FINALIZE
 
 // build_input (main.rs:175-196) on the device: the 8-bit h x w image (HWC

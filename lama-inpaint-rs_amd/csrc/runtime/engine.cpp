@@ -407,7 +407,10 @@ bool Engine::open(std::string &err)
 
         !get_fn(fn_tail_u8_, "lama_tail_u8", err) ||
         !get_fn(fn_finalize_ks_[0], "lama_finalize10", err) ||
-        !get_fn(fn_finalize_ks_[1], "lama_finalize20", err))
+        !get_fn(fn_finalize_ks_[1], "lama_finalize20", err) ||
+        !get_fn(fn_finalize_g2_[0], "lama_finalize_g2", err) ||
+        !get_fn(fn_finalize_g2_[1], "lama_finalize10_g2", err) ||
+        !get_fn(fn_finalize_g2_[2], "lama_finalize20_g2", err))
         return false;
     fn_build_in_ = fn_[F_INPUT];
     if (const char *wv = getenv("LAMA_FFC_WINO")) {
@@ -417,6 +420,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_FIN_GROUPS")) fin_groups_force_ = atoi(t);
 
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
@@ -672,6 +676,19 @@ int Engine::ksplit_for(int h, int w) const
     int s = 1;
     while (s < LAMA_KSPLIT_MAX && 16 * tiles * (2 * s) <= 2 * LAMA_CUS) s *= 2;
     return s;
+}
+
+// Groups of 4 elements per finalize thread (1 or 2): two where one group per
+// thread would give between 2.5 and 4 blocks per CU.  Measured: at 75 x 75
+// 768 blocks ran slower beside the concurrent kernels than 384 (157.4 vs
+// 158.9 passes/s); at 64 x 64 512 blocks ran faster than 256 (260.2 vs
+// 258.5); at 128 x 128 and 256 x 256 planes (8 and 32 blocks per CU) one
+// group was as fast or 0.3% faster.
+int Engine::fin_groups(size_t plane) const
+{
+    if (fin_groups_force_ == 1 || fin_groups_force_ == 2) return fin_groups_force_;
+    const size_t blocks = 128 * ((plane + 4 * LAMA_NT - 1) / (4 * LAMA_NT));
+    return 2 * blocks > 5 * (size_t)LAMA_CUS && blocks <= 4 * (size_t)LAMA_CUS ? 2 : 1;
 }
 
 // The K split of the SpectralTransform's two pointwise convolutions that
@@ -1182,12 +1199,14 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         fa2.res = ffc_res(k);
         fa2.out = ffc_dst(k);
         Launch L{};
-        L.fn = ks == 1 ? fn_[F_FINAL] : fn_finalize_ks_[ks == 2 ? 0 : 1];
+        const int g = fin_groups(P8);
+        const int ki = ks == 1 ? 0 : ks == 2 ? 1 : 2;
+        L.fn = g == 2 ? fn_finalize_g2_[ki] : ki == 0 ? fn_[F_FINAL] : fn_finalize_ks_[ki - 1];
         L.family = F_FINAL;
         L.stream = S_MAIN;
         L.wait_ev = b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1;
         L.record_ev = -1;
-        L.grid = (unsigned)(((128 * P8 + 3) / 4 + LAMA_NT - 1) / LAMA_NT);
+        L.grid = (unsigned)(128 * ((P8 + 4 * LAMA_NT * g - 1) / (4 * LAMA_NT * g)));
         L.arg = put(&fa2, sizeof fa2);
         L.nparams = 1;
         L.step_end = -1;

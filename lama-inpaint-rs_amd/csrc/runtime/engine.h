@@ -227,8 +227,10 @@ private:
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
+    int fin_groups_force_ = 0;  // LAMA_FIN_GROUPS: 1 or 2 forces the finalize kernel's groups per thread
     int pw_ksplit_force_ = 0;  // LAMA_PW_KSPLIT: 1, 2 or 4 forces the K split of conv1 and the FourierUnit conv
     // K split of the SpectralTransform conv1 (k1) and FourierUnit conv (ku)
+    int fin_groups(size_t plane) const;
     void pw_ksplit_for(int h, int w, const FftGeom &fg, int &k1, int &ku) const;
     // K split of the FFC GEMMs at input h x w (1 unless the F(4,3) kernels
     // would leave CUs idle)
@@ -267,6 +269,7 @@ private:
     std::map<std::pair<int, int>, SpecPlan> spec_plans_;
     hipFunction_t fn_build_in_ = nullptr, fn_tail_u8_ = nullptr;
     hipFunction_t fn_finalize_ks_[2] = {};  // lama_finalize10, lama_finalize20 (K split 2, 4)
+    hipFunction_t fn_finalize_g2_[3] = {};  // the same three with two element groups per thread
 
     // profiling
     uint32_t prof_mask_ = 0;

@@ -144,6 +144,16 @@ hipError_t hipModuleGetGlobal(hipDeviceptr_t *p, size_t *bytes, hipModule_t, con
     *bytes = n;
     return hipSuccess;
 }
+// FAKEHIP_TRACE=<file>: one line per launch, "<kernel> <grid x>", appended
+static void trace(hipFunction_t f, unsigned gx)
+{
+    static const char *path = getenv("FAKEHIP_TRACE");
+    if (!path) return;
+    if (FILE *fp = fopen(path, "a")) {
+        fprintf(fp, "%s %u\n", ((Fn *)f)->name.c_str(), gx);
+        fclose(fp);
+    }
+}
 static void launched(hipFunction_t f, void **params)
 {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -152,15 +162,17 @@ static void launched(hipFunction_t f, void **params)
     // pointer as the first argument
     if (params && params[0]) check_ptr(*(void **)params[0], ((Fn *)f)->name.c_str());
 }
-hipError_t hipModuleLaunchKernel(hipFunction_t f, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned,
+hipError_t hipModuleLaunchKernel(hipFunction_t f, unsigned gx, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned,
                                  hipStream_t, void **params, void **)
 {
+    trace(f, gx);
     launched(f, params);
     return hipSuccess;
 }
-hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, size_t,
+hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t gx, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, size_t,
                                     hipStream_t, void **params, void **, hipEvent_t, hipEvent_t, uint32_t)
 {
+    trace(f, gx);
     launched(f, params);
     return hipSuccess;
 }

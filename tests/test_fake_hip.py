@@ -66,6 +66,9 @@ def test_every_shape_plans_and_issues_its_launches(fake_lib, weights_file):
     # finalize sums 5 partials unsplit, 20 with the 256x256 K split (s = 4)
     assert p["512x512"]["finalize"] == "lama_finalize"
     assert p["256x256"]["finalize"] == "lama_finalize20"
+    # two element groups per thread where one would give 2.5-4 blocks per CU
+    assert p["600x600"]["finalize"] == "lama_finalize_g2"
+    assert p["1024x1024"]["finalize"] == "lama_finalize"
     # 1x1 activation loads by plane alignment: 4096 (float4), 5625 (scalar)
     assert p["512x512"]["conv1x1"] == "lama_conv1x1"
     assert p["600x600"]["conv1x1"] == "lama_conv1x1_s"

@@ -285,6 +285,23 @@ def test_forward_600_tile_window_non_pow2_bottleneck(pkg, engine, oracle_cal, h,
     assert np.array_equal(u8g[mask == 0], img[mask == 0])
 
 
+@pytest.mark.parametrize("h,w", [(8, 8), (8, 24), (16, 24), (24, 56)])
+def test_forward_tiny_bottleneck_planes(pkg, engine, oracle_cal, h, w):
+    """Bottleneck planes of 1, 3, 6 and 21 pixels against the oracle, every
+    step: the local branch's finish (sum of the K-range partials, BN, ReLU,
+    residual) takes its one-element path below 4 pixels and its clamped
+    4-element window at the plane's end otherwise."""
+    img, mask = _case(pkg, h, w, "rect")
+    x = pkg.host_api.build_input(img, mask)
+    print(f"case {h}x{w} rect", flush=True)
+    got, got_steps = engine.forward_steps(x, list(range(29)))
+    ref, ref_steps = oracle_cal.forward(x, steps=True)
+    for s in range(29):
+        e = rel_err(got_steps[s], ref_steps[s])
+        assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+    assert rel_err(got, ref) < STEP_TOL
+
+
 @pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16")],
                 ids=["f23", "f43w64", "f43w32", "f43w16"])
 def w4_forward_engine(pkg, weights_dir, request):
