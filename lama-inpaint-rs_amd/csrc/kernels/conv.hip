@@ -716,13 +716,21 @@ __device__ __forceinline__ int find_problem(const ProbStarts &ps, int &b)
     } while (0)
 
 using CfgHead = Cfg<7, 7, 1, true, 4, 2, 32>;
-using CfgDown = Cfg<3, 3, 2, true, 8, 2, 32>;
 using CfgFfc = Cfg<3, 3, 1, true, 8, 2, 32>;
 using CfgFfc1 = Cfg<1, 1, 1, false, 8, 2, 32>;
-using CfgT00 = Cfg<1, 1, 1, false, LAMA_CONVT_KC0, 2, 32>;
-using CfgT01 = Cfg<1, 2, 1, false, LAMA_CONVT_KC1, 2, 32>;
-using CfgT10 = Cfg<2, 1, 1, false, LAMA_CONVT_KC2, 2, 32>;
-using CfgT11 = Cfg<2, 2, 1, false, LAMA_CONVT_KC3, 2, 32>;
+// The stride-2 and transposed convolutions also come in 4 x 16-pixel tiles
+// (the _q kernels), for planes whose width leaves much of a 32-pixel tile
+// row empty (75 wide: 3 x 32 columns hold 78% of the tile, 5 x 16 hold 94%).
+template <int TR, int TC>
+using CfgDownT = Cfg<3, 3, 2, true, 8, TR, TC>;
+template <int TR, int TC>
+struct CfgT {
+    using P00 = Cfg<1, 1, 1, false, LAMA_CONVT_KC0, TR, TC>;
+    using P01 = Cfg<1, 2, 1, false, LAMA_CONVT_KC1, TR, TC>;
+    using P10 = Cfg<2, 1, 1, false, LAMA_CONVT_KC2, TR, TC>;
+    using P11 = Cfg<2, 2, 1, false, LAMA_CONVT_KC3, TR, TC>;
+    static constexpr int LDS = cmax(cmax(P00::LDS, P01::LDS), cmax(P10::LDS, P11::LDS));
+};
 
 }  // namespace
 
@@ -825,16 +833,29 @@ __device__ __forceinline__ int conv_xcd_order(int i, int n)
 }
 
 // model.2/3/4: 3x3 stride 2, reflect pad 1, BN + ReLU.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_PARAMS)
+template <int TR, int TC>
+__device__ __forceinline__ void conv3x3s2_body(const ConvProblem *__restrict__ probs, const ProbStarts &ps)
 {
-    LAMA_CONV_STARTS;
-    LAMA_STAMP_BEGIN;
-    __shared__ __attribute__((aligned(16))) float lds[2 * CfgDown::LDS];
+    using C = CfgDownT<TR, TC>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     b = conv_xcd_order(b, probs[pi].nblocks);
-    conv_tile<CfgDown, false>(probs[pi], b, lds, epl);
+    conv_tile<C, false>(probs[pi], b, lds, epl);
+}
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2(LAMA_CONV_PARAMS)
+{
+    LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
+    conv3x3s2_body<2, 32>(probs, ps);
+    LAMA_STAMP_END;
+}
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3s2_q(LAMA_CONV_PARAMS)
+{
+    LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
+    conv3x3s2_body<4, 16>(probs, ps);
     LAMA_STAMP_END;
 }
 
@@ -887,20 +908,33 @@ LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, 1, 64, true, LAMA_PW_DEPTH_RES)
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions
 // (problems 0..3 = phases (py,px) = (0,0), (0,1), (1,0), (1,1)), each a valid
 // (1+py) x (1+px) convolution with zero fill at the bottom/right edge.
-extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(LAMA_CONV_PARAMS)
+template <int TR, int TC>
+__device__ __forceinline__ void convt_body(const ConvProblem *__restrict__ probs, const ProbStarts &ps)
 {
-    LAMA_CONV_STARTS;
-    LAMA_STAMP_BEGIN;
-    __shared__ __attribute__((aligned(16))) float lds[2 * cmax(cmax(CfgT00::LDS, CfgT01::LDS), cmax(CfgT10::LDS, CfgT11::LDS))];
+    using C = CfgT<TR, TC>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];
     __shared__ float epl[192];
     int b = blockIdx.x;
     int pi = find_problem(ps, b);
     b = conv_xcd_order(b, probs[pi].nblocks);
     switch (pi) {
-    case 0: conv_tile<CfgT00, false>(probs[0], b, lds, epl); break;
-    case 1: conv_tile<CfgT01, false>(probs[1], b, lds, epl); break;
-    case 2: conv_tile<CfgT10, false>(probs[2], b, lds, epl); break;
-    default: conv_tile<CfgT11, false>(probs[3], b, lds, epl); break;
+    case 0: conv_tile<typename C::P00, false>(probs[0], b, lds, epl); break;
+    case 1: conv_tile<typename C::P01, false>(probs[1], b, lds, epl); break;
+    case 2: conv_tile<typename C::P10, false>(probs[2], b, lds, epl); break;
+    default: conv_tile<typename C::P11, false>(probs[3], b, lds, epl); break;
     }
+}
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt(LAMA_CONV_PARAMS)
+{
+    LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
+    convt_body<2, 32>(probs, ps);
+    LAMA_STAMP_END;
+}
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt_q(LAMA_CONV_PARAMS)
+{
+    LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
+    convt_body<4, 16>(probs, ps);
     LAMA_STAMP_END;
 }

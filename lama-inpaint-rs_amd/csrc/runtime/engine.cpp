@@ -97,6 +97,9 @@ ProbStarts prob_starts(const ConvProblem *q, size_t n)
 
 // Tile geometry of each conv family (kernels/conv.hip): rows x columns.
 // `narrow`: the F(4,3) kernel's 32-pixel blocks.
+// Pixel tile (rows x columns) of a conv family; `w4v` is the tile variant
+// (Engine::tile_variant): the F(4,3) block shape, or for the stride-2 and
+// transposed convolutions 0 = 2 x 32, 1 = 4 x 16.
 void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
 {
     if ((family == F_CONV3 || family == F_CONV3G) && wino == 4) {  // lama_conv3x3w4 / w4n / w4q
@@ -108,6 +111,9 @@ void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
     } else if (family == F_CONV1 || family == F_CONV1R) {
         tr = 1;
         tc = 64;
+    } else if ((family == F_CONV3S2 || family == F_CONVT) && w4v == 1) {  // the _q kernels
+        tr = 4;
+        tc = 16;
     } else {
         tr = 2;
         tc = 32;
@@ -410,7 +416,9 @@ bool Engine::open(std::string &err)
         !get_fn(fn_finalize_ks_[1], "lama_finalize20", err) ||
         !get_fn(fn_finalize_g2_[0], "lama_finalize_g2", err) ||
         !get_fn(fn_finalize_g2_[1], "lama_finalize10_g2", err) ||
-        !get_fn(fn_finalize_g2_[2], "lama_finalize20_g2", err))
+        !get_fn(fn_finalize_g2_[2], "lama_finalize20_g2", err) ||
+        !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
+        !get_fn(fn_edge_q_[1], "lama_convt_q", err))
         return false;
     fn_build_in_ = fn_[F_INPUT];
     if (const char *wv = getenv("LAMA_FFC_WINO")) {
@@ -421,6 +429,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_FIN_GROUPS")) fin_groups_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_EDGE_TILE")) edge_force_ = atoi(t);
 
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
@@ -626,6 +635,8 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
 {
     if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_variant(probs[0].OH, probs[0].OW)];
     if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
+    if ((family == F_CONV3S2 || family == F_CONVT) && tile_variant(family, probs[0].OH, probs[0].OW) == 1)
+        return fn_edge_q_[family == F_CONVT];
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
     // the widest activation loads every plane of the launch allows
     int vw = 4;
@@ -658,6 +669,22 @@ int Engine::w4_variant(int OH, int OW) const
     for (int v : {2, 0})
         if (blocks(v) < blocks(best)) best = v;
     return best;
+}
+
+// Tile variant of a conv family at an OH x OW output (for the transposed
+// convolution, the phase grid): the F(4,3) block shape, or for the
+// stride-2 and transposed convolutions 4 x 16 tiles (1) where they cover the
+// plane with fewer tiles than 2 x 32 (0), which is where the width leaves
+// much of a 32-pixel row empty (75: 3 x 32 columns for 75, 5 x 16 for 80).
+// LAMA_EDGE_TILE=32 or 16 (read at open) forces one.
+int Engine::tile_variant(int family, int OH, int OW) const
+{
+    if (family == F_CONV3 || family == F_CONV3G) return w4_variant(OH, OW);
+    if (family != F_CONV3S2 && family != F_CONVT) return 0;
+    if (edge_force_ == 32) return 0;
+    if (edge_force_ == 16) return 1;
+    const long t32 = (long)((OW + 31) / 32) * ((OH + 1) / 2), t16 = (long)((OW + 15) / 16) * ((OH + 3) / 4);
+    return t16 < t32 ? 1 : 0;
 }
 
 // The FFC GEMMs' K split: at small planes the F(4,3) launches have few
@@ -991,7 +1018,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc, wino_, w4_variant(OH, OW));
+        tile_shape(family, tr, tc, wino_, tile_variant(family, OH, OW));
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
         q.mblocks = (M + 63) / 64;
@@ -2261,7 +2288,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.OH = family == F_CONV1 ? 1 : oh;
     q.OW = family == F_CONV1 ? oh * ow : ow;
     int tr, tc;
-    tile_shape(family, tr, tc, wino, w4_variant(q.OH, q.OW));
+    tile_shape(family, tr, tc, wino, tile_variant(family, q.OH, q.OW));
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
     q.mblocks = (cout + 63) / 64;
@@ -2311,7 +2338,7 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
     UPLOAD(dx, x, (size_t)cin * h * w);
     UPLOAD(dw, A.h.data(), A.h.size());
     UPLOAD(dout, nullptr, (size_t)cout * 4 * h * w);
-    ConvProblem q[4];
+    ConvProblem q[4]{};
     unsigned nb = 0;
     for (int k = 0; k < 4; ++k) {
         ConvProblem &c = q[k];
@@ -2326,8 +2353,10 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
         c.M = cout;
         c.OH = h;
         c.OW = w;
-        c.tiles_x = (w + 31) / 32;
-        c.tiles_y = (h + 1) / 2;
+        int tr, tc;
+        tile_shape(F_CONVT, tr, tc, 0, tile_variant(F_CONVT, h, w));
+        c.tiles_x = (w + tc - 1) / tc;
+        c.tiles_y = (h + tr - 1) / tr;
         c.mblocks = (cout + 63) / 64;
         c.nblocks = c.tiles_x * c.tiles_y * c.mblocks;
         nb += c.nblocks;
@@ -2345,7 +2374,7 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
     UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
     if (!check(hip_->hipMemcpy(dq, q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
     Launch L{};
-    L.fn = fn_[F_CONVT];
+    L.fn = conv_fn(F_CONVT, q, 4);
     L.family = F_CONVT;
     L.grid = nb;
     L.arg = dq;

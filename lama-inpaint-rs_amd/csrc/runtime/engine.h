@@ -226,7 +226,9 @@ private:
     int wino_ = 4;
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
+    int tile_variant(int family, int OH, int OW) const;
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
+    int edge_force_ = 0;  // LAMA_EDGE_TILE: 32 or 16 forces the stride-2 / transposed conv tile width
     int fin_groups_force_ = 0;  // LAMA_FIN_GROUPS: 1 or 2 forces the finalize kernel's groups per thread
     int pw_ksplit_force_ = 0;  // LAMA_PW_KSPLIT: 1, 2 or 4 forces the K split of conv1 and the FourierUnit conv
     // K split of the SpectralTransform conv1 (k1) and FourierUnit conv (ku)
@@ -270,6 +272,7 @@ private:
     hipFunction_t fn_build_in_ = nullptr, fn_tail_u8_ = nullptr;
     hipFunction_t fn_finalize_ks_[2] = {};  // lama_finalize10, lama_finalize20 (K split 2, 4)
     hipFunction_t fn_finalize_g2_[3] = {};  // the same three with two element groups per thread
+    hipFunction_t fn_edge_q_[2] = {};       // lama_conv3x3s2_q, lama_convt_q (4 x 16 tiles)
 
     // profiling
     uint32_t prof_mask_ = 0;

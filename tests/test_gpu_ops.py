@@ -76,6 +76,44 @@ def test_conv_transpose(engine, cin, cout, h, w):
     assert rel_err(got, ref) < TOL
 
 
+@pytest.fixture(scope="module", params=["32", "16"], ids=["tile2x32", "tile4x16"])
+def edge_engine(pkg, request):
+    """An engine with the stride-2 and transposed convolutions' tile forced:
+    2 x 32 pixels (lama_conv3x3s2, lama_convt) or 4 x 16 (the _q kernels)."""
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_EDGE_TILE", request.param)
+        eng = pkg.hip_engine.Engine()
+    yield eng
+    eng.close()
+
+
+@pytest.mark.parametrize("cin,cout,h,w", [(16, 64, 150, 150), (16, 24, 9, 70), (64, 128, 32, 32), (8, 72, 13, 37)])
+def test_conv3x3s2_tile_shapes(edge_engine, cin, cout, h, w):
+    """Stride 2 in both tile shapes, against the oracle: a 75 x 75 output
+    (the 600 x 600 model.4 plane), odd heights, partial tiles, M % 64 != 0."""
+    rng = np.random.default_rng(cin * 7 + cout + h)
+    x = rng.standard_normal((cin, h, w), np.float32)
+    wt = (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
+    s, t = _bn(rng, cout)
+    got = edge_engine.op_conv2d(x, wt, None, 2, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv2d(x, wt, None, pad=1, stride=2, reflect=True), s, t)
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("cin,cout,h,w", [(64, 32, 75, 75), (32, 16, 5, 7), (40, 72, 9, 19)])
+def test_conv_transpose_tile_shapes(edge_engine, cin, cout, h, w):
+    """The transposed convolution in both tile shapes, against the oracle: a
+    75 x 75 input (the 600 x 600 model.24 plane) and ragged shapes."""
+    rng = np.random.default_rng(cin + 3 * cout + h)
+    x = np.maximum(rng.standard_normal((cin, h, w)), 0).astype(np.float32)
+    wt = (rng.standard_normal((cin, cout, 3, 3)) * np.sqrt(2.0 / (cout * 9))).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.05).astype(np.float32)
+    s, t = _bn(rng, cout)
+    got = edge_engine.op_conv_transpose(x, wt, b, s, t, relu=True)
+    ref = _oracle_bn_relu(O.conv_transpose(x, wt, b), s, t)
+    assert rel_err(got, ref) < TOL
+
+
 # (64, 64), (32, 32), (33, 96), (31, 32): padded row-pair stride, odd row counts
 SIZES = [(8, 8), (64, 64), (32, 32), (75, 75), (6, 10), (5, 7), (1, 1), (2, 3), (64, 33), (16, 12), (38, 19),
          (33, 96), (31, 32)]
