@@ -59,10 +59,7 @@ static inline constexpr int lama_convt_kc(int phase)
 #ifndef LAMA_WINO_KC
 #define LAMA_WINO_KC 4
 #endif
-// Floats per output channel and K chunk of the F(4,3) Winograd weights: the
-// 6 positions x 3 kernel rows x 4 channels, padded to whole float4 slots of
-// one workgroup's staging round
-#define LAMA_WINO4_WKP 80
+
 // output tile of the 7x7 tail kernel (rows x columns) and the adjacent
 // pixels each of its threads computes
 #ifndef LAMA_TAIL_ROWS

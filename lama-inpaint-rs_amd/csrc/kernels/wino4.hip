@@ -19,84 +19,65 @@
 // direct sum: half the direct convolution's MFMA work, 3/4 of F(2,3)'s.
 //
 // A workgroup computes 64 output channels x RW rows x 4*NTR pixels (32
-// Winograd tiles: RW rows of NTR tiles, NTR = 16 or 8, so 64- or 32-pixel
-// wide blocks).  Wave (wm, wu) owns channels wm*32 .. +32 and the positions
-// u = 3*wu .. 3*wu+2 as three 32 x 32 accumulators of v_mfma_f32_32x32x2f32:
-// GEMM rows are output channels, GEMM columns the block's 32 tiles, K =
-// (ci, ky).  K is walked in chunks of LAMA_WINO_KC = 4 input channels; per
-// chunk the block stages in LDS the transformed weights [64 co][u][ky][4]
-// (rows padded to 80 floats) and the transformed input [rows][u][tiles][4
-// (+2 pad)], with the two-stage pipeline of the F(2,3) kernel and an even
-// chunk count.  In the epilogue the two position halves of each channel half
-// swap partial sums of the output transform through LDS, so that each wave
-// finishes two of the four pixels of every tile.
+// Winograd tiles: RW rows of NTR tiles, NTR = 16, 8 or 4, so 64-, 32- or
+// 16-pixel wide blocks).  Wave (wm, wu) owns channels wm*32 .. +32 and the
+// positions u = 3*wu .. 3*wu+2 as three 32 x 32 accumulators of
+// v_mfma_f32_32x32x2f32: GEMM rows are output channels, GEMM columns the
+// block's 32 tiles, K = (ci, ky).  K is walked in chunks of LAMA_WINO_KC = 4
+// input channels.  Each weight is an MFMA operand of exactly one wave, so the
+// waves load their transformed weights straight from global memory into
+// registers (the host packs them in operand order), one chunk ahead; only the
+// transformed input, which the two channel halves share, is staged in LDS
+// ([rows][u][tiles][4 (+2 pad)]), two stages with one barrier per chunk and
+// an even chunk count.  In the epilogue the two position halves of each
+// channel half swap partial sums of the output transform through LDS, so
+// that each wave finishes two of the four pixels of every tile.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
 
 namespace {
 
-// LDS padding: floats after each weight row (a multiple of 4: the rows are
-// stored as float4s) and after each staged input row (even: read as float2s)
-#ifndef LAMA_W4_WPAD
-#define LAMA_W4_WPAD 4
-#endif
-#ifndef LAMA_W4_VPAD
-#define LAMA_W4_VPAD 0
-#endif
 template <int NTR_>
 struct W4Cfg {
     static constexpr int KC = LAMA_WINO_KC;      // input channels per chunk
     static constexpr int NU = 6, KY = 3;         // Winograd positions, kernel rows
     static constexpr int NUW = NU / 2;           // positions per wave
+    static constexpr int NS = KY * NUW;          // MFMA steps of two K slots per wave and chunk
     static constexpr int NTR = NTR_;             // tiles per output row
     static constexpr int RW = 32 / NTR;          // output rows per block
     static constexpr int TR = RW, TC = 4 * NTR;  // output rows x pixels per block
     static constexpr int IR = TR + 2;            // input rows per block
     static constexpr int WK = NU * KY * KC;      // weights per output channel and chunk (72)
-    static constexpr int WKP = LAMA_WINO4_WKP;   // packed (padded) weights per channel and chunk
-    static constexpr int WSTR = WKP + LAMA_W4_WPAD;  // LDS row stride of the weights
+    static constexpr int WCH = 64 * WK;          // packed weights per 64-channel block and chunk
     static constexpr int H = KC / 2;             // channels per lane half and MFMA K slot
     static constexpr int KCP = KC + 2;           // LDS floats per (row, u, tile)
-    static constexpr int W_LDS = 64 * WSTR;
     static constexpr int NITEM = KC * IR * NTR;  // (ci, row, tile) input items per chunk
     static constexpr int VITER = (NITEM + LAMA_NT - 1) / LAMA_NT;
-    static constexpr int VRS = NU * NTR * KCP + LAMA_W4_VPAD;  // LDS stride of an input row
-    static constexpr int V_LDS = IR * VRS + NU * 64;  // + a dummy tail for items past NITEM
-    static constexpr int LDS = W_LDS + V_LDS;    // floats per stage
-    static constexpr int WITER = 64 * WKP / 4 / LAMA_NT;  // weight float4s per thread
+    static constexpr int VRS = NU * NTR * KCP;   // LDS stride of an input row
+    static constexpr int V_LDS = IR * VRS + NU * 64;  // per stage, + a dummy tail for items past NITEM
     // epilogue exchange: per channel half, two pixels x 16 registers x 64 lanes from each position half
     static constexpr int X_LDS = 2 * 2 * 2 * 16 * 64;
-    static_assert(WITER * LAMA_NT * 4 == 64 * WKP, "whole weight float4s");
-    static_assert(WKP >= WK && WKP % 16 == 0, "padded weight rows");
+    static constexpr int LDS = 2 * V_LDS > X_LDS ? 2 * V_LDS : X_LDS;  // floats
     static_assert(NTR * RW == 32, "32 tiles per block");
-    static_assert(X_LDS <= 2 * LDS, "the exchange fits in the staging buffers");
     static_assert(KC == 4, "two channels per lane half");
 };
 
 template <class C>
 struct W4Slots {
-    int wg[C::WITER], wl[C::WITER];  // weights: float offset in the row, LDS offset
-    unsigned po[C::VITER][6];        // input: byte offsets of d0..d5 from the chunk's first plane
-    int vl[C::VITER];                // input: LDS offset of V_0 (V_u at + u * NTR * KCP)
+    unsigned po[C::VITER][6];  // byte offsets of d0..d5 from the chunk's first plane
+    int vl[C::VITER];          // LDS offset of V_0 (V_u at + u * NTR * KCP)
 };
 
 template <class C>
 struct W4Stage {
-    float w[4 * C::WITER];
     float d[C::VITER][6];
 };
 
 template <class C>
-__device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int m0, int M, int oy0, int ox0)
+__device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int oy0, int ox0)
 {
     const int tid = threadIdx.x;
-#pragma unroll
-    for (int it = 0; it < C::WITER; ++it) {
-        const int idx = tid + it * LAMA_NT, row = idx / (C::WKP / 4), c4 = idx % (C::WKP / 4);
-        sl.wl[it] = row * C::WSTR + c4 * 4;
-        sl.wg[it] = min(m0 + row, M - 1) * sg.wrow + c4 * 4;
-    }
     const unsigned plane = (unsigned)(sg.IH * sg.IW);
 #pragma unroll
     for (int it = 0; it < C::VITER; ++it) {
@@ -114,18 +95,26 @@ __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int 
     }
 }
 
+// A wave's MFMA A operands of one chunk: for steps s = ky * 3 + q (position
+// u = 3 wu + q) lane (g, j) holds the transformed weights of output channel
+// wm * 32 + j and input channels 2g, 2g + 1 of the chunk, 64 lanes x 8
+// contiguous bytes per step (`wb` is the wave's lane's first float).
 template <class C>
-__device__ __forceinline__ void w4_load(W4Stage<C> &st, const W4Slots<C> &sl, const ConvSeg &sg, int ck)
+__device__ __forceinline__ void w4_load_w(float (&w)[2 * C::NS], const LAMA_GLOBAL float *wb, int ck)
 {
-    const LAMA_GLOBAL float *wt = gp(sg.wt) + (long)ck * C::WKP;
+    const LAMA_GLOBAL float *p = wb + (long)ck * C::WCH;
 #pragma unroll
-    for (int it = 0; it < C::WITER; ++it) {
-        const float4 v = *at_byte<float4>(wt, 4u * (unsigned)sl.wg[it]);
-        st.w[4 * it] = v.x;
-        st.w[4 * it + 1] = v.y;
-        st.w[4 * it + 2] = v.z;
-        st.w[4 * it + 3] = v.w;
+    for (int s = 0; s < C::NS; ++s) {
+        const float2 v = *reinterpret_cast<const LAMA_GLOBAL float2 *>(p + s * 128);
+        w[2 * s] = v.x;
+        w[2 * s + 1] = v.y;
     }
+}
+
+// The input rows d0..d5 of each of the thread's items of chunk `ck`.
+template <class C>
+__device__ __forceinline__ void w4_load_d(W4Stage<C> &st, const W4Slots<C> &sl, const ConvSeg &sg, int ck)
+{
     // channels past C (zero weights) read the last float of the source; the
     // zero chunk that pads the count to even reads within channel C - 1
     const unsigned plane = (unsigned)(sg.IH * sg.IW);
@@ -138,14 +127,10 @@ __device__ __forceinline__ void w4_load(W4Stage<C> &st, const W4Slots<C> &sl, co
         for (int c = 0; c < 6; ++c) st.d[it][c] = *at_byte<float>(src, min(sl.po[it][c], last));
 }
 
+// V = B^T d of each item into the LDS stage `vl`.
 template <class C>
-__device__ __forceinline__ void w4_store(const W4Stage<C> &st, const W4Slots<C> &sl, float *lds)
+__device__ __forceinline__ void w4_store_v(const W4Stage<C> &st, const W4Slots<C> &sl, float *vl)
 {
-#pragma unroll
-    for (int it = 0; it < C::WITER; ++it)
-        *reinterpret_cast<float4 *>(lds + sl.wl[it]) =
-            make_float4(st.w[4 * it], st.w[4 * it + 1], st.w[4 * it + 2], st.w[4 * it + 3]);
-    float *vl = lds + C::W_LDS;
     constexpr int S = C::NTR * C::KCP;  // LDS distance between positions
 #pragma unroll
     for (int it = 0; it < C::VITER; ++it) {
@@ -164,33 +149,30 @@ __device__ __forceinline__ void w4_store(const W4Stage<C> &st, const W4Slots<C> 
 }
 
 // MFMAs of one chunk for wave (wm, wu): for each (ky, u) of the wave's three
-// positions, lane half g reads its two channels of the weights and of the
-// input (one 8-byte read each) and feeds one to each of two MFMAs as the
-// MFMA's K slot g; the reads of the next (ky, u) are issued first (reading
-// 2, 3 or all 9 steps ahead measured the same).
+// positions, lane half g reads its two channels of the input (one 8-byte
+// read, issued a step ahead) and feeds one to each of two MFMAs as the MFMA's
+// K slot g, beside the weights of that step from registers.
 template <class C>
-__device__ __forceinline__ void w4_compute(f32x16 (&acc)[C::NUW], const float *lds)
+__device__ __forceinline__ void w4_compute(f32x16 (&acc)[C::NUW], const float (&w)[2 * C::NS], const float *vl)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wu = wave & 1, g = lane >> 5, j = lane & 31;
+    const int wu = wave & 1, g = lane >> 5, j = lane & 31;
     const int r = j / C::NTR, t = j % C::NTR;  // the MFMA column's output row and tile within the block
-    const float *wrow = lds + (wm * 32 + j) * C::WSTR + C::H * g;
-    const float *vrow = lds + C::W_LDS + t * C::KCP + C::H * g;
-    float a[2][C::H], b[2][C::H];
+    const float *vrow = vl + t * C::KCP + C::H * g;
+    float b[2][C::H];
     auto rd = [&](int s, int buf) {
         const int ky = s / C::NUW, u = C::NUW * wu + s % C::NUW;
-        lds_vec<C::H>(a[buf], wrow + (u * C::KY + ky) * C::KC);
         lds_vec<C::H>(b[buf], vrow + (r + ky) * C::VRS + u * C::NTR * C::KCP);
     };
     rd(0, 0);
 #pragma unroll
-    for (int s = 0; s < C::KY * C::NUW; ++s) {
+    for (int s = 0; s < C::NS; ++s) {
         const int cur = s & 1;
-        if (s + 1 < C::KY * C::NUW) rd(s + 1, cur ^ 1);
+        if (s + 1 < C::NS) rd(s + 1, cur ^ 1);
         const int q = s % C::NUW;
 #pragma unroll
         for (int c = 0; c < C::H; ++c)
-            acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][c], b[cur][c], acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[2 * s + c], b[cur][c], acc[q], 0, 0, 0);
     }
 }
 
@@ -224,30 +206,42 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
     if (P.ksplit > 1) {
         const int c0 = ks * P.kchunks * C::KC;
         sg.src += (long)c0 * sg.IH * sg.IW;
-        sg.wt += (long)ks * P.kchunks * C::WKP;
+        sg.wt += (long)ks * P.kchunks * C::WCH;
         sg.C -= c0;
         sg.nchunk = P.kchunks;
     }
     const int n = sg.nchunk, last = n - 1;
-    W4Slots<C> sl;
-    w4_slots<C>(sl, sg, m0, P.M, oy0, ox0);
-    float *l0 = lds, *l1 = lds + C::LDS;
-    W4Stage<C> r0, r1;
-    w4_load<C>(r0, sl, sg, 0);
-    w4_load<C>(r1, sl, sg, min(1, last));
-    w4_store<C>(r0, sl, l0);
-    w4_load<C>(r0, sl, sg, min(2, last));
-    __syncthreads();
-    // n is even (the weights are packed in pairs of chunks): one loop exit
-    for (int ck = 0; ck < n; ck += 2) {
-        w4_compute<C>(acc, l0);
-        w4_store<C>(r1, sl, l1);
-        w4_load<C>(r1, sl, sg, min(ck + 3, last));
+    {
+        W4Slots<C> sl;
+        w4_slots<C>(sl, sg, oy0, ox0);
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        // the M block's weights (64 rows of wrow floats), then this wave's and lane's operands
+        const LAMA_GLOBAL float *wb = gp(sg.wt) + (long)mb * 64 * sg.wrow + wave * (C::NS * 128) + lane * 2;
+        float *l0 = lds, *l1 = lds + C::V_LDS;
+        float w0[2 * C::NS], w1[2 * C::NS];
+        W4Stage<C> r0, r1;
+        // weights one chunk ahead, inputs two; the prefetches past the last
+        // chunk re-read it (uniform control flow)
+        w4_load_w<C>(w0, wb, 0);
+        w4_load_d<C>(r0, sl, sg, 0);
+        w4_load_w<C>(w1, wb, min(1, last));
+        w4_load_d<C>(r1, sl, sg, min(1, last));
+        w4_store_v<C>(r0, sl, l0);
+        w4_load_d<C>(r0, sl, sg, min(2, last));
         __syncthreads();
-        w4_compute<C>(acc, l1);
-        w4_store<C>(r0, sl, l0);
-        w4_load<C>(r0, sl, sg, min(ck + 4, last));
-        __syncthreads();
+        // n is even (the weights are packed in pairs of chunks): one loop exit
+        for (int ck = 0; ck < n; ck += 2) {
+            w4_compute<C>(acc, w0, l0);
+            w4_load_w<C>(w0, wb, min(ck + 2, last));
+            w4_store_v<C>(r1, sl, l1);
+            w4_load_d<C>(r1, sl, sg, min(ck + 3, last));
+            __syncthreads();
+            w4_compute<C>(acc, w1, l1);
+            w4_load_w<C>(w1, wb, min(ck + 3, last));
+            w4_store_v<C>(r0, sl, l0);
+            w4_load_d<C>(r0, sl, sg, min(ck + 4, last));
+            __syncthreads();
+        }
     }
     // output transform: wave wu = 0 holds m0..m2, wu = 1 holds m3..m5.
     // Partials  p = (m0 + m1 + m2, m1 - m2, m1 + m2, m1 - m2)   (wu = 0)
@@ -321,9 +315,12 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
 // along x, in 64-pixel (lama_conv3x3w4) or 32-pixel (lama_conv3x3w4n) wide
 // blocks; problems of a grouped launch are found as in the direct kernels.
 // Register budget of the F(4,3) kernels: at 120 the compiler keeps the
-// accumulators in VGPRs and fits the kernel in 170 registers (220 without
-// the bound), so a third wave -- a SpectralTransform kernel's -- fits on a
-// SIMD beside two of these: 252.2 vs 250.9 passes/s at 512x512.
+// accumulators in VGPRs and fits the kernel in 130 registers (216 with
+// accumulation registers, without the bound), so three of these fit on a
+// SIMD, or two beside a SpectralTransform kernel's wave.  With 33.5 KB of
+// LDS three workgroups also fit on a CU; the host adds dynamic LDS to hold
+// the GEMMs at two per CU where that leaves the SpectralTransform's kernels
+// room.
 // XCD-contiguous launch order: the dispatcher deals workgroups to the eight
 // XCDs round-robin (workgroup i to XCD i mod 8), each XCD with its own L2.
 // Workgroup i takes block x * q + min(x, r) + i / 8 of the launch's natural
@@ -363,7 +360,7 @@ __device__ __forceinline__ int w4_xcd_order(int i, int n)
         LAMA_CONV_STARTS;                                                                  \
         LAMA_STAMP_BEGIN;                                                                  \
         using C = W4Cfg<NTR>;                                                              \
-        __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                     \
+        __shared__ __attribute__((aligned(16))) float lds[C::LDS];                         \
         __shared__ float epl[192];                                                         \
         int b = w4_xcd_order(blockIdx.x, gridDim.x);                                       \
         int pi = find_problem(ps, b);                                                      \

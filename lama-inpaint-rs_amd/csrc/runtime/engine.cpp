@@ -227,38 +227,49 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
     return p;
 }
 
-// 3x3 weights for lama_conv3x3w4 / w4n: per output channel and chunk of
-// LAMA_WINO_KC input channels, [u][ky][ci] (u = 0..5) padded to LAMA_WINO4_WKP
-// floats, with U_u = sum over kx of G[u][kx] * w[ky][kx] and
+// 3x3 weights for lama_conv3x3w4 / w4n / w4q, transformed by
+// U_u = sum over kx of G[u][kx] * w[ky][kx] with
 // G = (1/4, 0, 0; -1/6, -1/6, -1/6; -1/6, 1/6, -1/6; 1/24, 1/12, 1/6;
 // 1/24, -1/12, 1/6; 0, 0, 1) -- the Winograd F(4,3) weight transform for the
-// points 0, 1, -1, 2, -2, infinity, evaluated in f64 and rounded once to f32.
+// points 0, 1, -1, 2, -2, infinity, evaluated in f64 and rounded once to f32
+// -- in the order the kernels' waves load them as MFMA operands: per block of
+// 64 output channels (rows past M zero) and chunk of 4 input channels,
+// [wave (wm, wu)][step s = ky * 3 + q][lane (g, j)][c] holds U_u for output
+// channel 32 wm + j, input channel 2g + c of the chunk and position
+// u = 3 wu + q.  A chunk is 64 x 72 floats (T * KC); the block stride is 64
+// rows of wrow = nchunk * 72.
 Packed pack_wino4(Arena &A, int M, int C, const std::function<float(int, int, int)> &get)
 {
     static const double G[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
                                    {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
-    constexpr int KC = LAMA_WINO_KC, WKP = LAMA_WINO4_WKP;
-    static_assert(WKP % KC == 0, "whole channel groups per padded row");
+    constexpr int KC = LAMA_WINO_KC, WK = 72;
+    static_assert(KC == 4, "two channels per lane half");
     Packed p;
     p.M = M;
     p.C = C;
-    p.T = WKP / KC;  // the chunk stride is T * KC floats, as for the other layouts
     p.KC = KC;
+    p.T = 64 * WK / KC;  // chunk stride T * KC = one 64-row block's chunk
     p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
-    p.wrow = p.nchunk * WKP;
-    p.off = A.add((size_t)M * p.wrow);
+    p.wrow = p.nchunk * WK;
+    const int mblocks = (M + 63) / 64;
+    p.off = A.add((size_t)mblocks * 64 * p.wrow);
     float *d = A.h.data() + p.off;
-    for (int co = 0; co < M; ++co)
-        for (int ck = 0; ck < p.nchunk; ++ck)
-            for (int u = 0; u < 6; ++u)
-                for (int ky = 0; ky < 3; ++ky)
-                    for (int kc = 0; kc < KC; ++kc) {
-                        const int ci = ck * KC + kc;
-                        double v = 0;
-                        if (ci < C)
-                            for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
-                        d[((size_t)co * p.nchunk + ck) * WKP + (u * 3 + ky) * KC + kc] = (float)v;
-                    }
+    for (int mb = 0; mb < mblocks; ++mb)
+        for (int ck = 0; ck < p.nchunk; ++ck) {
+            float *blk = d + ((size_t)mb * p.nchunk + ck) * 64 * WK;
+            for (int wave = 0; wave < 4; ++wave)
+                for (int st = 0; st < 9; ++st)
+                    for (int lane = 0; lane < 64; ++lane)
+                        for (int c = 0; c < 2; ++c) {
+                            const int wm = wave >> 1, wu = wave & 1, g = lane >> 5, j = lane & 31;
+                            const int co = mb * 64 + wm * 32 + j, ci = ck * KC + 2 * g + c;
+                            const int ky = st / 3, u = 3 * wu + st % 3;
+                            double v = 0;
+                            if (co < M && ci < C)
+                                for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
+                            blk[((wave * 9 + st) * 64 + lane) * 2 + c] = (float)v;
+                        }
+        }
     return p;
 }
 
@@ -430,6 +441,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_FIN_GROUPS")) fin_groups_force_ = atoi(t);
     if (const char *t = getenv("LAMA_EDGE_TILE")) edge_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_W4_LDSPAD")) w4_ldspad_force_ = atoi(t);
 
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
@@ -685,6 +697,27 @@ int Engine::tile_variant(int family, int OH, int OW) const
     if (edge_force_ == 16) return 1;
     const long t32 = (long)((OW + 31) / 32) * ((OH + 1) / 2), t16 = (long)((OW + 15) / 16) * ((OH + 3) / 4);
     return t16 < t32 ? 1 : 0;
+}
+
+// Dynamic LDS added to each F(4,3) workgroup (bytes), to hold the GEMMs at
+// two workgroups per CU.  The kernels need 33.5 KB and 130 registers, so
+// three fit on a CU; that is faster where the FFC's A and B launches have
+// more workgroups than three per CU or no more than two (1024 x 1024: 73.5
+// vs 72.5 passes/s; 512 x 512: 261.9 vs 259.9), but where they have between
+// two and four per CU (600 x 600: 800 workgroups) a third GEMM workgroup on
+// a CU leaves no room for the SpectralTransform's conv2 (160 registers), the
+// critical path there: 159.8 padded vs 157.9.  LAMA_W4_LDSPAD=0/1 (read at
+// open) forces it off or on.
+unsigned Engine::w4_lds_pad(int h8, int w8, int ks) const
+{
+    if (wino_ != 4) return 0;
+    int tr, tc;
+    tile_shape(F_CONV3, tr, tc, 4, w4_variant(h8, w8));
+    const long tiles = (long)((w8 + tc - 1) / tc) * ((h8 + tr - 1) / tr);
+    const long pair = 16 * tiles * ks;  // A: 8 M blocks; B: 2 M blocks x 4 K ranges; each x ks
+    const bool pad = w4_ldspad_force_ >= 0 ? w4_ldspad_force_ == 1
+                                           : pair > 2 * (long)LAMA_CUS && pair < 4 * (long)LAMA_CUS;
+    return pad ? 24576u : 0u;
 }
 
 // The FFC GEMMs' K split: at small planes the F(4,3) launches have few
@@ -966,6 +999,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
 
     ArenaLayout lay;
     const int ks = ksplit_for(H, W);
+    const unsigned w4_shmem = w4_lds_pad(H8, W8, ks);
     int pk1, pku;  // K split of the SpectralTransform conv1 and of the FourierUnit conv
     pw_ksplit_for(H, W, fg, pk1, pku);
     p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), ks, pk1, pku, lay);
@@ -1055,7 +1089,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         }
         // the head kernel walks its tiles: two resident workgroups per CU
         L.grid = family == F_CONV7 ? std::min(nb, 2u * LAMA_CUS) : nb;
-        L.shmem = 0;
+        L.shmem = (family == F_CONV3 || family == F_CONV3G) && wino_ == 4 ? w4_shmem : 0;
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
         L.ps = prob_starts(probs.data(), probs.size());
         if (probs.size() > LAMA_MAX_PROBS) bad_problem = true;

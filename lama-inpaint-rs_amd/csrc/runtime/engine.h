@@ -227,7 +227,9 @@ private:
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
     int tile_variant(int family, int OH, int OW) const;
+    unsigned w4_lds_pad(int h8, int w8, int ks) const;
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
+    int w4_ldspad_force_ = -1;  // LAMA_W4_LDSPAD: 0 or 1 forces the F(4,3) LDS padding off or on
     int edge_force_ = 0;  // LAMA_EDGE_TILE: 32 or 16 forces the stride-2 / transposed conv tile width
     int fin_groups_force_ = 0;  // LAMA_FIN_GROUPS: 1 or 2 forces the finalize kernel's groups per thread
     int pw_ksplit_force_ = 0;  // LAMA_PW_KSPLIT: 1, 2 or 4 forces the K split of conv1 and the FourierUnit conv
