@@ -456,9 +456,12 @@ __device__ __forceinline__ void pw_compute_chunk(f32x16 (&acc)[C::NACC], const f
 // is written to LDS (at step c - 1) and consumed at step c, so each load has
 // D chunks of MFMA time to land; these small-K GEMMs run one wave per SIMD
 // and are bound by that latency.  A depth that divides the chunk counts (12
-// and 24 at 16 channels) keeps the unrolled group free of early exits.
+// and 24 at 16 channels) keeps the unrolled group free of early exits.  Depth
+// 2 (fewer staging registers) measured fastest beside the direct-weight
+// F(4,3) GEMM: 263.8 vs 262.9 (depth 4) passes/s at 512x512, 162.2 vs 161.0
+// at 600x600.
 #ifndef LAMA_PW_DEPTH
-#define LAMA_PW_DEPTH 4
+#define LAMA_PW_DEPTH 2
 #endif
 template <class C, int D>
 __device__ __forceinline__ void run_segment_pw(f32x16 (&acc)[C::NACC], const ConvSeg &sg_mem, int m0, int M, int ox0,
