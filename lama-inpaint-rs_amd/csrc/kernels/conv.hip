@@ -261,13 +261,59 @@ __device__ __forceinline__ void compute_chunk(f32x16 &acc, const float *wl, cons
     }
 }
 
+// Taps of a lama_convt_rows workgroup (row phase py: output rows 2m+py, both
+// column phases): tap t reads the window offset (dy, dx) and feeds the
+// accumulator of column phase px.  py = 0: phase (0,0) at (0,0); phase
+// (0,1) at (0,0), (0,1).  py = 1: phase (1,0) at (0,0), (1,0); phase (1,1)
+// at (0,0), (0,1), (1,0), (1,1).  The weights are packed in this order.
+__device__ __forceinline__ constexpr int rows_tap_dy(int py, int t) { return py ? (t == 1 || t >= 4 ? 1 : 0) : 0; }
+__device__ __forceinline__ constexpr int rows_tap_dx(int py, int t)
+{
+    return py ? (t == 3 || t == 5 ? 1 : 0) : (t == 2 ? 1 : 0);
+}
+__device__ __forceinline__ constexpr int rows_tap_px(int py, int t) { return py ? (t >= 2 ? 1 : 0) : (t >= 1 ? 1 : 0); }
+
+struct RowsAcc {
+    f32x16 a[2];  // column phases 0 and 1
+};
+
+// MFMAs of one chunk of a lama_convt_rows workgroup: as compute_chunk, with
+// each tap into its column phase's accumulator.
+template <class C>
+__device__ __forceinline__ void compute_chunk(RowsAcc &acc, const float *wl, const float *pl)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
+    const int p = wn * 32 + j;
+    const int pr = p / C::TC, pc = p % C::TC;
+    const float *wrow = wl + (wm * 32 + j) * C::WSTR + g * (C::KC / 2);
+    const float *prow = pl + (pr * C::PCP + pc) * C::KCP + g * (C::KC / 2);
+    constexpr int H = C::KC / 2;
+    float a[2][H], b[2][H];
+    lds_vec<H>(a[0], wrow);
+    lds_vec<H>(b[0], prow + (rows_tap_dy(C::PY, 0) * C::PCP + rows_tap_dx(C::PY, 0)) * C::KCP);
+#pragma unroll
+    for (int t = 0; t < C::T; ++t) {
+        const int cur = t & 1;
+        if (t + 1 < C::T) {
+            lds_vec<H>(a[cur ^ 1], wrow + (t + 1) * C::KC);
+            lds_vec<H>(b[cur ^ 1],
+                       prow + (rows_tap_dy(C::PY, t + 1) * C::PCP + rows_tap_dx(C::PY, t + 1)) * C::KCP);
+        }
+        const int px = rows_tap_px(C::PY, t);
+#pragma unroll
+        for (int c = 0; c < H; ++c)
+            acc.a[px] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][c], b[cur][c], acc.a[px], 0, 0, 0);
+    }
+}
+
 // K loop of one segment.  NBUF = 2: two LDS stages and two register stages,
 // one barrier per chunk.  Chunk k's global loads are issued two chunks ahead
 // (during chunk k-2's MFMAs), written to LDS after chunk k-1's MFMAs and
 // consumed at step k, so each load has two chunks of MFMA time to land.
 // NBUF = 1 (single-chunk segments such as the 4-channel head) stages once.
-template <class C, int NBUF>
-__device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg_mem, int m0, int M, int oy0, int ox0,
+template <class C, int NBUF, class Acc>
+__device__ __forceinline__ void run_segment(Acc &acc, const ConvSeg &sg_mem, int m0, int M, int oy0, int ox0,
                                             float *lds)
 {
     // a register copy: the barriers of the loop would otherwise make the
@@ -296,17 +342,23 @@ __device__ __forceinline__ void run_segment(f32x16 &acc, const ConvSeg &sg_mem, 
         store_chunk<C>(r0, sl, l0, l0 + C::W_LDS);
         load_chunk<C>(r0, sl, sg, min(2, last));
         __syncthreads();
-        for (int ck = 0; ck < n; ck += 2) {
+        // one exit: a break between the two steps made the compiler copy the
+        // accumulators every iteration (and hold two sets of them)
+        int ck = 0;
+        for (; ck + 1 < n; ck += 2) {
             // even step: compute stage 0, stage chunk ck+1 (r1), refill r1 with ck+3
             compute_chunk<C>(acc, l0, l0 + C::W_LDS);
             store_chunk<C>(r1, sl, l1, l1 + C::W_LDS);
             load_chunk<C>(r1, sl, sg, min(ck + 3, last));
             __syncthreads();
-            if (ck + 1 >= n) break;
             // odd step: compute stage 1, stage chunk ck+2 (r0), refill r0 with ck+4
             compute_chunk<C>(acc, l1, l1 + C::W_LDS);
             store_chunk<C>(r0, sl, l0, l0 + C::W_LDS);
             load_chunk<C>(r0, sl, sg, min(ck + 4, last));
+            __syncthreads();
+        }
+        if (ck < n) {  // an odd count: the last chunk is in stage 0
+            compute_chunk<C>(acc, l0, l0 + C::W_LDS);
             __syncthreads();
         }
     }
@@ -735,6 +787,34 @@ struct CfgT {
     static constexpr int LDS = cmax(cmax(P00::LDS, P01::LDS), cmax(P10::LDS, P11::LDS));
 };
 
+// The transposed convolution by row phase (lama_convt_rows): a workgroup
+// computes both column phases of output rows 2m+py for 64 channels x TR x TC
+// input positions, through a (1+py) x 2 window over a (TR+py) x (TC+1)
+// patch -- 3 taps for py = 0, 6 for py = 1 (rows_tap_*).  Each lane then
+// holds output pixels 2n and 2n+1 of a row and stores them as one float2,
+// so every output line is written whole by one workgroup.  The staging
+// members follow Cfg, so the slot and stage code is shared.
+template <int PY_, int TR_, int TC_>
+struct CfgRows {
+    static constexpr int PY = PY_, KH = 1 + PY_, KW = 2, S = 1, KC = 8, TR = TR_, TC = TC_, T = PY_ ? 6 : 3, PAD = 0;
+    static constexpr bool REFLECT = false;
+    static constexpr int PR = TR + PY, PC = TC + 1, PCP = PC;
+    static constexpr int WK = T * KC;
+    static constexpr int WSTR = WK + ((12 - WK % 8) % 8);
+    static constexpr int KCP = KC + 4;
+    static __device__ __forceinline__ constexpr int col(int c) { return c; }
+    static constexpr int W4 = 64 * WK / 4;
+    static constexpr int WITER = (W4 + LAMA_NT - 1) / LAMA_NT;
+    static constexpr int NPIX = PR * PC;
+    static constexpr int NPB = (NPIX + 15) / 16;
+    static constexpr int P_SLOTS = NPB * 16 * KC;
+    static constexpr int PITER = (P_SLOTS + LAMA_NT - 1) / LAMA_NT;
+    static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT - W4) * 4;
+    static constexpr int P_LDS = PR * PCP * KCP + 64;
+    static constexpr int LDS = W_LDS + P_LDS;
+    static_assert(TR * TC == 64, "pixel tile must hold 64 positions");
+};
+
 }  // namespace
 
 // model.1: 7x7, reflect pad 3 (the ReflectionPad2d(3) + valid 7x7 of the
@@ -939,5 +1019,74 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt_q(LAMA_CONV_PAR
     LAMA_CONV_STARTS;
     LAMA_STAMP_BEGIN;
     convt_body<4, 16>(probs, ps);
+    LAMA_STAMP_END;
+}
+
+// The same convolution as two row-phase problems (problem py = 0, 1; see
+// CfgRows): half the workgroups of the four-phase form, each input patch
+// staged twice instead of four times, and whole output rows stored.
+template <class C>
+__device__ __forceinline__ void convt_rows_tile(const ConvProblem &P, int b, float *lds, float *epl)
+{
+    const int mb = b % P.mblocks, t = b / P.mblocks;
+    const int m0 = mb * 64, y0 = (t / P.tiles_x) * C::TR, x0 = (t % P.tiles_x) * C::TC;
+    const float ep = epi_param_load(P, m0);
+    RowsAcc acc;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc.a[i][r] = 0.f;
+    run_segment<C, 2>(acc, P.s0, m0, P.M, y0, x0, lds);
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
+    const int p = wn * 32 + j;
+    const int y = y0 + p / C::TC, x = x0 + p % C::TC;
+    if (y >= P.OH || x >= P.OW) return;
+    LAMA_GLOBAL float *out = gp(P.out) + (long)(2 * y + C::PY) * P.outW + 2 * x;
+    // D[i][j] of a 32x32 MFMA block: lane j + 32 ((i / 4) % 2), register (i / 8) * 4 + i % 4
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int cl = wm * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m0 + cl >= P.M) continue;
+        float e[2] = {acc.a[0][r], acc.a[1][r]};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if (P.bias) e[q] += epl[cl];
+            if (P.scale) e[q] = e[q] * epl[64 + cl] + epl[128 + cl];
+            if (P.relu) e[q] = fmaxf(e[q], 0.f);
+        }
+        *reinterpret_cast<float2 *>(out + (long)(m0 + cl) * P.out_cstride) = make_float2(e[0], e[1]);
+    }
+}
+
+template <int TR, int TC>
+__device__ __forceinline__ void convt_rows_body(const ConvProblem *__restrict__ probs, const ProbStarts &ps)
+{
+    using C0 = CfgRows<0, TR, TC>;
+    using C1 = CfgRows<1, TR, TC>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * cmax(C0::LDS, C1::LDS)];
+    __shared__ float epl[192];
+    int b = blockIdx.x;
+    const int pi = find_problem(ps, b);
+    b = conv_xcd_order(b, probs[pi].nblocks);
+    if (pi == 0)
+        convt_rows_tile<C0>(probs[0], b, lds, epl);
+    else
+        convt_rows_tile<C1>(probs[1], b, lds, epl);
+}
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt_rows(LAMA_CONV_PARAMS)
+{
+    LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
+    convt_rows_body<2, 32>(probs, ps);
+    LAMA_STAMP_END;
+}
+extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_convt_rows_q(LAMA_CONV_PARAMS)
+{
+    LAMA_CONV_STARTS;
+    LAMA_STAMP_BEGIN;
+    convt_rows_body<4, 16>(probs, ps);
     LAMA_STAMP_END;
 }

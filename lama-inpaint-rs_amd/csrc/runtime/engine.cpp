@@ -196,6 +196,38 @@ Packed pack(Arena &A, int M, int C, int T, int KC, const std::function<float(int
     return p;
 }
 
+// ConvTranspose2d k3 s2 p1 op1 weights w [ci][co][3][3] (PyTorch layout) as
+// sub-pixel phase taps.  Phase (py, px) of output pixel (2m+py, 2n+px)
+// reads input (m+a, n+b) for a < 1+py, b < 1+px: kernel row ky = 1 for
+// py = 0, else 2 (a = 0) or 0 (a = 1); the same for columns.
+float convt_tap(const float *w, int cout, int co, int ci, int py, int px, int a, int b)
+{
+    const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
+    return w[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
+}
+
+// One phase's (1+py) x (1+px) taps, row-major (lama_convt).
+Packed pack_convt_phase(Arena &A, int cout, int cin, int ph, const float *w)
+{
+    const int py = ph >> 1, px = ph & 1, nx = 1 + px;
+    return pack(A, cout, cin, (1 + py) * nx, lama_convt_kc(ph), [&](int co, int ci, int t) {
+        return convt_tap(w, cout, co, ci, py, px, t / nx, t % nx);
+    });
+}
+
+// The taps of row phase py, both column phases, in chunks of 8 channels
+// (lama_convt_rows): py = 0: (0,0) of phase (0,0); (0,0), (0,1) of phase
+// (0,1).  py = 1: (0,0), (1,0) of phase (1,0); (0,0), (0,1), (1,0), (1,1)
+// of phase (1,1).
+Packed pack_convt_rows(Arena &A, int cout, int cin, int py, const float *w)
+{
+    static const int tap[2][6][3] = {{{0, 0, 0}, {1, 0, 0}, {1, 0, 1}},
+                                     {{0, 0, 0}, {0, 1, 0}, {1, 0, 0}, {1, 0, 1}, {1, 1, 0}, {1, 1, 1}}};  // px, a, b
+    return pack(A, cout, cin, py ? 6 : 3, 8, [&](int co, int ci, int t) {
+        return convt_tap(w, cout, co, ci, py, tap[py][t][0], tap[py][t][1], tap[py][t][2]);
+    });
+}
+
 // 3x3 weights for lama_conv3x3w: per output channel and chunk of
 // LAMA_WINO_KC input channels, [u][ky][ci] with U_u = sum over kx of G[u][kx] * w[ky][kx],
 // G = (1, 0, 0; 1/2, 1/2, 1/2; 1/2, -1/2, 1/2; 0, 0, 1) -- the Winograd F(2,3)
@@ -429,7 +461,9 @@ bool Engine::open(std::string &err)
         !get_fn(fn_finalize_g2_[1], "lama_finalize10_g2", err) ||
         !get_fn(fn_finalize_g2_[2], "lama_finalize20_g2", err) ||
         !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
-        !get_fn(fn_edge_q_[1], "lama_convt_q", err))
+        !get_fn(fn_edge_q_[1], "lama_convt_q", err) ||
+        !get_fn(fn_convt_rows_[0], "lama_convt_rows", err) ||
+        !get_fn(fn_convt_rows_[1], "lama_convt_rows_q", err))
         return false;
     fn_build_in_ = fn_[F_INPUT];
     if (const char *wv = getenv("LAMA_FFC_WINO")) {
@@ -442,6 +476,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_FIN_GROUPS")) fin_groups_force_ = atoi(t);
     if (const char *t = getenv("LAMA_EDGE_TILE")) edge_force_ = atoi(t);
     if (const char *t = getenv("LAMA_W4_LDSPAD")) w4_ldspad_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_CONVT_ROWS")) convt_rows_ = atoi(t) != 0;
 
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
@@ -550,17 +585,11 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
         std::vector<float> bias;
         if (!S.get(p + ".weight", {U.cin, U.cout, 3, 3}, w, err) || !S.get(p + ".bias", {U.cout}, bias, err))
             return false;
-        // Phase (py, px) of output pixel (2m+py, 2n+px) reads input (m+a, n+b)
-        // with a in [0, 1+py): kernel row ky = 1 for py = 0, else 2 (a = 0)
-        // or 0 (a = 1); the same for columns.
-        for (int ph = 0; ph < 4; ++ph) {
-            const int py = ph >> 1, px = ph & 1, nx = 1 + px;
-            const int cout = U.cout;
-            U.ph[ph] = pack(A, cout, U.cin, (1 + py) * nx, lama_convt_kc(ph), [&](int co, int ci, int t) {
-                const int a = t / nx, b = t % nx;
-                const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
-                return w[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
-            });
+        // sub-pixel phase taps (convt_tap): one pack of all nine, or one per phase
+        if (convt_rows_) {
+            for (int py = 0; py < 2; ++py) U.row[py] = pack_convt_rows(A, U.cout, U.cin, py, w.data());
+        } else {
+            for (int ph = 0; ph < 4; ++ph) U.ph[ph] = pack_convt_phase(A, U.cout, U.cin, ph, w.data());
         }
         U.bias = A.add(U.cout);
         std::copy(bias.begin(), bias.end(), A.h.begin() + U.bias);
@@ -647,6 +676,7 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
 {
     if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_variant(probs[0].OH, probs[0].OW)];
     if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
+    if (family == F_CONVT && convt_rows_) return fn_convt_rows_[tile_variant(family, probs[0].OH, probs[0].OW)];
     if ((family == F_CONV3S2 || family == F_CONVT) && tile_variant(family, probs[0].OH, probs[0].OW) == 1)
         return fn_edge_q_[family == F_CONVT];
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
@@ -1333,10 +1363,10 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     for (int u = 0; u < 3; ++u) {
         const UpW &U = up_[u];
         std::vector<ConvProblem> ph;
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < (convt_rows_ ? 2 : 4); ++k) {
             const size_t oplane = (size_t)(2 * uh[u]) * (2 * uw[u]);
-            ConvProblem q = problem(F_CONVT, seg(usrc[u], U.ph[k], U.cin, uh[u], uw[u]), U.cout, uh[u], uw[u], U.bn, U.cout,
-                                    udst[u], oplane, 2 * uw[u], nullptr);
+            ConvProblem q = problem(F_CONVT, seg(usrc[u], convt_rows_ ? U.row[k] : U.ph[k], U.cin, uh[u], uw[u]), U.cout,
+                                    uh[u], uw[u], U.bn, U.cout, udst[u], oplane, 2 * uw[u], nullptr);
             q.bias = wp(U.bias);
             q.oy_mul = q.ox_mul = 2;
             q.oy_off = k >> 1;
@@ -2353,15 +2383,10 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
                       const float *scale, const float *shift, int relu, float *out, std::string &err)
 {
     Arena A;
+    const int np = convt_rows_ ? 2 : 4;  // problems: the two row phases, or the four phases
     Packed ph[4];
-    for (int k = 0; k < 4; ++k) {
-        const int py = k >> 1, px = k & 1, nx = 1 + px;
-        ph[k] = pack(A, cout, cin, (1 + py) * nx, lama_convt_kc(k), [&](int co, int ci, int t) {
-            const int a = t / nx, b = t % nx;
-            const int ky = py == 0 ? 1 : (a == 0 ? 2 : 0), kx = px == 0 ? 1 : (b == 0 ? 2 : 0);
-            return wt[(((size_t)ci * cout + co) * 3 + ky) * 3 + kx];
-        });
-    }
+    for (int k = 0; k < np; ++k)
+        ph[k] = convt_rows_ ? pack_convt_rows(A, cout, cin, k, wt) : pack_convt_phase(A, cout, cin, k, wt);
     size_t bn = A.add(2 * (size_t)cout), bo = A.add(cout);
     for (int i = 0; i < cout; ++i) {
         A.h[bn + i] = scale ? scale[i] : 1.f;
@@ -2374,7 +2399,7 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
     UPLOAD(dout, nullptr, (size_t)cout * 4 * h * w);
     ConvProblem q[4]{};
     unsigned nb = 0;
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < np; ++k) {
         ConvProblem &c = q[k];
         std::memset(&c, 0, sizeof c);
         c.s0.src = dx;
@@ -2408,11 +2433,11 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
     UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
     if (!check(hip_->hipMemcpy(dq, q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
     Launch L{};
-    L.fn = conv_fn(F_CONVT, q, 4);
+    L.fn = conv_fn(F_CONVT, q, np);
     L.family = F_CONVT;
     L.grid = nb;
     L.arg = dq;
-    L.ps = prob_starts(q, 4);
+    L.ps = prob_starts(q, np);
     L.nparams = 2;
     if (!launch(L, stream_, err) || !check(hip_->hipStreamSynchronize(stream_), "kernel", err)) return false;
     return check(hip_->hipMemcpy(out, dout, (size_t)cout * 4 * h * w * 4, hipMemcpyDeviceToHost), "hipMemcpy", err);

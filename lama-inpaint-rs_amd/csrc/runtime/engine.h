@@ -182,6 +182,7 @@ private:
     };
     struct UpW {
         Packed ph[4];
+        Packed row[2];  // the taps of row phases 0 and 1 (lama_convt_rows)
         size_t bias = 0, bn = 0;
         int cin = 0, cout = 0;
     };
@@ -231,6 +232,7 @@ private:
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
     int w4_ldspad_force_ = -1;  // LAMA_W4_LDSPAD: 0 or 1 forces the F(4,3) LDS padding off or on
     int edge_force_ = 0;  // LAMA_EDGE_TILE: 32 or 16 forces the stride-2 / transposed conv tile width
+    bool convt_rows_ = true;  // LAMA_CONVT_ROWS=0: the transposed convs as four phase problems (lama_convt)
     int fin_groups_force_ = 0;  // LAMA_FIN_GROUPS: 1 or 2 forces the finalize kernel's groups per thread
     int pw_ksplit_force_ = 0;  // LAMA_PW_KSPLIT: 1, 2 or 4 forces the K split of conv1 and the FourierUnit conv
     // K split of the SpectralTransform conv1 (k1) and FourierUnit conv (ku)
@@ -275,6 +277,7 @@ private:
     hipFunction_t fn_finalize_ks_[2] = {};  // lama_finalize10, lama_finalize20 (K split 2, 4)
     hipFunction_t fn_finalize_g2_[3] = {};  // the same three with two element groups per thread
     hipFunction_t fn_edge_q_[2] = {};       // lama_conv3x3s2_q, lama_convt_q (4 x 16 tiles)
+    hipFunction_t fn_convt_rows_[2] = {};   // lama_convt_rows (2 x 32 positions), lama_convt_rows_q (4 x 16)
 
     // profiling
     uint32_t prof_mask_ = 0;
