@@ -44,6 +44,23 @@ static inline constexpr int lama_fft_nb(int h, int w)
 // 16/8/8/8 4.796, 16/16/16/8 4.825, 32/16/16/8 4.831 (the larger chunks
 // cost a workgroup of occupancy).  Their weights are packed in chunks of
 // these sizes.
+// Input channels per K chunk of the stride-2 convs (lama_conv3x3s2) and of
+// the two row phases of the transposed convs (lama_convt_rows); the weights
+// are packed in chunks of these sizes.  Stride-2 chunks of 4 channels take
+// 124 registers and 42 KB of LDS (three workgroups per CU) against 176 and
+// 76 KB at 8 (two): conv3x3s2 0.286-0.293 vs 0.296-0.302 ms per pass at
+// 512x512, 0.400-0.411 vs 0.445 at 600x600.  The row phases measured best at
+// 8 / 8 (0.276-0.281 ms per pass; 16 / 8: 0.281-0.288, 16 / 16: 0.296,
+// 8 / 4: 0.306-0.311).
+#ifndef LAMA_S2_KC
+#define LAMA_S2_KC 4
+#endif
+#ifndef LAMA_CONVT_ROWS_KC0
+#define LAMA_CONVT_ROWS_KC0 8
+#endif
+#ifndef LAMA_CONVT_ROWS_KC1
+#define LAMA_CONVT_ROWS_KC1 8
+#endif
 #ifndef LAMA_CONVT_KC0
 #define LAMA_CONVT_KC0 16
 #define LAMA_CONVT_KC1 8

@@ -777,7 +777,7 @@ using CfgFfc1 = Cfg<1, 1, 1, false, 8, 2, 32>;
 // (the _q kernels), for planes whose width leaves much of a 32-pixel tile
 // row empty (75 wide: 3 x 32 columns hold 78% of the tile, 5 x 16 hold 94%).
 template <int TR, int TC>
-using CfgDownT = Cfg<3, 3, 2, true, 8, TR, TC>;
+using CfgDownT = Cfg<3, 3, 2, true, LAMA_S2_KC, TR, TC>;
 template <int TR, int TC>
 struct CfgT {
     using P00 = Cfg<1, 1, 1, false, LAMA_CONVT_KC0, TR, TC>;
@@ -796,12 +796,13 @@ struct CfgT {
 // members follow Cfg, so the slot and stage code is shared.
 template <int PY_, int TR_, int TC_>
 struct CfgRows {
-    static constexpr int PY = PY_, KH = 1 + PY_, KW = 2, S = 1, KC = 8, TR = TR_, TC = TC_, T = PY_ ? 6 : 3, PAD = 0;
+    static constexpr int PY = PY_, KH = 1 + PY_, KW = 2, S = 1, TR = TR_, TC = TC_, T = PY_ ? 6 : 3, PAD = 0;
+    static constexpr int KC = PY_ ? LAMA_CONVT_ROWS_KC1 : LAMA_CONVT_ROWS_KC0;
     static constexpr bool REFLECT = false;
     static constexpr int PR = TR + PY, PC = TC + 1, PCP = PC;
     static constexpr int WK = T * KC;
     static constexpr int WSTR = WK + ((12 - WK % 8) % 8);
-    static constexpr int KCP = KC + 4;
+    static constexpr int KCP = (KC / 2) % 4 == 0 ? KC + 4 : KC + 2;  // as Cfg
     static __device__ __forceinline__ constexpr int col(int c) { return c; }
     static constexpr int W4 = 64 * WK / 4;
     static constexpr int WITER = (W4 + LAMA_NT - 1) / LAMA_NT;
@@ -813,6 +814,7 @@ struct CfgRows {
     static constexpr int P_LDS = PR * PCP * KCP + 64;
     static constexpr int LDS = W_LDS + P_LDS;
     static_assert(TR * TC == 64, "pixel tile must hold 64 positions");
+    static_assert(KC % 4 == 0, "KC must be a multiple of 4");
 };
 
 }  // namespace

@@ -215,7 +215,8 @@ Packed pack_convt_phase(Arena &A, int cout, int cin, int ph, const float *w)
     });
 }
 
-// The taps of row phase py, both column phases, in chunks of 8 channels
+// The taps of row phase py, both column phases, in K chunks of
+// LAMA_CONVT_ROWS_KC0 / KC1 channels
 // (lama_convt_rows): py = 0: (0,0) of phase (0,0); (0,0), (0,1) of phase
 // (0,1).  py = 1: (0,0), (1,0) of phase (1,0); (0,0), (0,1), (1,0), (1,1)
 // of phase (1,1).
@@ -223,7 +224,7 @@ Packed pack_convt_rows(Arena &A, int cout, int cin, int py, const float *w)
 {
     static const int tap[2][6][3] = {{{0, 0, 0}, {1, 0, 0}, {1, 0, 1}},
                                      {{0, 0, 0}, {0, 1, 0}, {1, 0, 0}, {1, 0, 1}, {1, 1, 0}, {1, 1, 1}}};  // px, a, b
-    return pack(A, cout, cin, py ? 6 : 3, 8, [&](int co, int ci, int t) {
+    return pack(A, cout, cin, py ? 6 : 3, py ? LAMA_CONVT_ROWS_KC1 : LAMA_CONVT_ROWS_KC0, [&](int co, int ci, int t) {
         return convt_tap(w, cout, co, ci, py, tap[py][t][0], tap[py][t][1], tap[py][t][2]);
     });
 }
@@ -533,14 +534,14 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
         const int cin = dc[d][0], cout = dc[d][1];
         const std::string p = "model." + std::to_string(d + 2);
         if (!S.get(p + ".ffc.convl2l.weight", {cout, cin, 3, 3}, w, err)) return false;
-        down_[d] = pack(A, cout, cin, 9, 8, [&](int co, int ci, int t) { return w[((size_t)co * cin + ci) * 9 + t]; });
+        down_[d] = pack(A, cout, cin, 9, LAMA_S2_KC, [&](int co, int ci, int t) { return w[((size_t)co * cin + ci) * 9 + t]; });
         if (!fold_bns(A, S, {{p + ".bn_l", cout}}, down_bn_[d], err)) return false;
     }
     // model.4: 256 -> 128 local + 384 global, stacked along M
     if (!S.get("model.4.ffc.convl2l.weight", {128, 256, 3, 3}, w, err) ||
         !S.get("model.4.ffc.convl2g.weight", {384, 256, 3, 3}, w2, err))
         return false;
-    down_[2] = pack(A, 512, 256, 9, 8, [&](int co, int ci, int t) {
+    down_[2] = pack(A, 512, 256, 9, LAMA_S2_KC, [&](int co, int ci, int t) {
         return co < 128 ? w[((size_t)co * 256 + ci) * 9 + t] : w2[((size_t)(co - 128) * 256 + ci) * 9 + t];
     });
     if (!fold_bns(A, S, {{"model.4.bn_l", 128}, {"model.4.bn_g", 384}}, down_bn_[2], err)) return false;
@@ -2318,7 +2319,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
     const int wino = family == F_CONV3 ? wino_ : 0;
-    const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : 8;
+    const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : family == F_CONV3S2 ? LAMA_S2_KC : 8;
     if ((size_t)4 * KC * h * w >= ((size_t)1 << 32)) {  // 32-bit staging offsets within a K chunk
         err = "op_conv2d: plane too large";
         return false;
