@@ -78,7 +78,7 @@ static inline constexpr int lama_convt_kc(int phase)
 #endif
 
 // output tile of the 7x7 tail kernel (rows x columns) and the adjacent
-// pixels each of its threads computes
+// pixels each thread of its two channel halves computes
 #ifndef LAMA_TAIL_ROWS
 #define LAMA_TAIL_ROWS 8
 #endif
@@ -86,7 +86,7 @@ static inline constexpr int lama_convt_kc(int phase)
 #define LAMA_TAIL_COLS 64
 #endif
 #ifndef LAMA_TAIL_PX
-#define LAMA_TAIL_PX 2
+#define LAMA_TAIL_PX 4
 #endif
 
 #ifdef __HIP_DEVICE_COMPILE__

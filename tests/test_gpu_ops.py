@@ -166,11 +166,14 @@ def test_irfft2(engine, fft_mode, h, w):
     assert rel_err(got, ref) < TOL
 
 
-@pytest.mark.parametrize("h,w", [(16, 64), (24, 40), (8, 8), (64, 128)])
-def test_tail(engine, h, w):
-    rng = np.random.default_rng(h + w)
-    x = rng.standard_normal((64, h, w), np.float32)
-    wt = (rng.standard_normal((3, 64, 7, 7)) * 0.02).astype(np.float32)
+# cin 7 and 1: odd channel counts leave the kernel's second channel half idle
+# in the last step; 9 x 70 spans two column tiles with a partial row tile
+@pytest.mark.parametrize("h,w,cin", [(16, 64, 64), (24, 40, 64), (8, 8, 64), (64, 128, 64), (24, 40, 7),
+                                     (9, 70, 1), (600 // 8 * 8, 75, 64)])
+def test_tail(engine, h, w, cin):
+    rng = np.random.default_rng(h + w + cin)
+    x = rng.standard_normal((cin, h, w), np.float32)
+    wt = (rng.standard_normal((3, cin, 7, 7)) * 0.02).astype(np.float32)
     b = (rng.standard_normal(3) * 0.05).astype(np.float32)
     got = engine.op_tail(x, wt, b)
     z = O.conv2d(O.reflect_pad(x, 3), wt, b, pad=0, stride=1, reflect=False)
