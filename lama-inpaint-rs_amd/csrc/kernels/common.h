@@ -26,6 +26,12 @@
 #ifndef LAMA_FFT_SPLIT_LDS
 #define LAMA_FFT_SPLIT_LDS (32 * 1024)
 #endif
+// Columns per block of the 256 x 256 planes' column launches (16 threads per
+// column, four-step transforms; the exchange buffer is 256 x this x 8 bytes,
+// at most LAMA_FFT_SPLIT_LDS).
+#ifndef LAMA_FFT_C4
+#define LAMA_FFT_C4 16
+#endif
 
 // Complex values per ping-pong buffer of the single-block FFT kernels: the
 // row-pair layout [(h+1)/2][w] or the half spectrum [h][w/2+1], rounded up to

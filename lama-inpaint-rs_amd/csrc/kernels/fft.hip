@@ -1200,39 +1200,141 @@ __device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
     }
 }
 
+// ---- column launches of the 256 x 256 planes: four-step transforms ------
+//
+// Each block takes LAMA_FFT_C4 = 16 adjacent columns of one channel (the
+// Nyquist column 128 has a block of its own, through rfft2_cols_ct /
+// irfft2_cols_ct with one column), 16 threads per column.  Thread (column
+// cc, t) holds rows t + 16 j (j = 0..15) in registers and the 256-point
+// transform runs as 256 = 16 x 16 (Gentleman-Sande four-step):
+//   Y_t[k1] = sum_j x[t + 16 j] W16^(j k1)     (16-point DFT in registers)
+//   Y_t[k1] *= W256^(t k1)                     (twiddles from the table)
+//   X[k1 + 16 k2] = sum_t Y_t[k1] W16^(t k2)   (after one exchange through
+//                                               LDS, in registers again)
+// with W_n = exp(sign 2 pi i / n).  Thread (cc, k1) then holds rows
+// k1 + 16 k2, the same pattern as it loaded.  A wave's loads are 4 rows x 16
+// columns (128-byte runs of complex values) and its stores 4 rows x 64 bytes
+// per real plane, against 64- and 32-byte runs with 8-column blocks; one
+// exchange replaces three Stockham passes and their barriers.
+
+constexpr int kC4 = LAMA_FFT_C4, kC4T = 16 * kC4;  // columns per block, threads per block
+static_assert(kC4T <= LAMA_FFT_NT, "the block fits the FFT launch bound");
+// the twiddles follow the exchange buffer (or the Nyquist block's two buffers)
+constexpr int kC4Tw = 256 * kC4 > 2 * 256 * SplitCt<256>::CB ? 256 * kC4 : 2 * 256 * SplitCt<256>::CB;
+static_assert(kC4T >= 256 && 128 % kC4 == 0, "one twiddle per thread; whole blocks below the Nyquist column");
+
+// Block i of a launch of n blocks, renumbered so that the dispatcher's
+// round-robin over the eight XCDs (block i to XCD i mod 8) hands each XCD a
+// contiguous range: the column blocks of one channel then share an L2, which
+// holds the 128-byte lines their row runs split between them.
+__device__ __forceinline__ int fft_xcd_order(int i, int n)
+{
+    const int x = i & 7, q = n >> 3, r = n & 7;
+    return x * q + min(x, r) + (i >> 3);
+}
+
+// 16-point DFT in registers (radix 4 x 4): v[n] -> sum_n v[n] exp(s 2 pi i n k / 16)
+__device__ __forceinline__ void dft16(float2 (&v)[16], int s)
+{
+    // W16^m for m = b * c (b, c = 0..3): exp(s 2 pi i m / 16)
+    constexpr float C1 = 0.92387953251128675613f, S1 = 0.38268343236508977173f, H = 0.70710678118654752440f;
+    float2 u[4][4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        float2 q[4] = {v[b], v[b + 4], v[b + 8], v[b + 12]};
+        dft<4>(q, s);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) u[b][c] = q[c];
+    }
+    // twiddles W16^(b c): (b, c) = (1,1) 1, (1,2) 2, (1,3) 3, (2,1) 2, (2,2) 4, (2,3) 6, (3,1) 3, (3,2) 6, (3,3) 9
+    const float2 w1 = make_float2(C1, s * S1), w2 = make_float2(H, s * H), w3 = make_float2(S1, s * C1);
+    const float2 w4 = make_float2(0.f, (float)s), w6 = make_float2(-H, s * H), w9 = make_float2(-C1, -s * S1);
+    u[1][1] = cmul(u[1][1], w1);
+    u[1][2] = cmul(u[1][2], w2);
+    u[1][3] = cmul(u[1][3], w3);
+    u[2][1] = cmul(u[2][1], w2);
+    u[2][2] = cmul(u[2][2], w4);
+    u[2][3] = cmul(u[2][3], w6);
+    u[3][1] = cmul(u[3][1], w3);
+    u[3][2] = cmul(u[3][2], w6);
+    u[3][3] = cmul(u[3][3], w9);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float2 q[4] = {u[0][c], u[1][c], u[2][c], u[3][c]};
+        dft<4>(q, s);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) v[c + 4 * d] = q[d];
+    }
+}
+
+// The four-step transform of this block's 16 columns (v: rows t + 16 j on
+// entry, rows k1 + 16 k2 on return, (cc, t) = (tid % 16, tid / 16)).  `ex`
+// holds 256 x kC4 complex values, `tw` the 256 twiddles exp(-2 pi i k / 256).
+__device__ __forceinline__ void col256_four_step(float2 (&v)[16], float2 *ex, const float2 *tw, int sign)
+{
+    const int cc = threadIdx.x % kC4, t = threadIdx.x / kC4;
+    dft16(v, sign);
+#pragma unroll
+    for (int k1 = 1; k1 < 16; ++k1) v[k1] = cmul(v[k1], twd(tw, t * k1, sign));
+    // exchange: thread (cc, t) writes Y_t[k1] at [k1][t][cc]; thread (cc, k1) reads [k1][0..15][cc]
+#pragma unroll
+    for (int k1 = 0; k1 < 16; ++k1) ex[(k1 * 16 + t) * kC4 + cc] = v[k1];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = ex[(t * 16 + j) * kC4 + cc];
+    dft16(v, sign);
+}
+
+// tmp -> stacked [2C][256][129]: forward column transforms, ortho scale
+__device__ __forceinline__ void rfft2_cols_256_c4(const FftArgs &A, float2 *sm, int c, int x0)
+{
+    constexpr int H = 256, Wh = 129;
+    float2 *ex = sm, *tw = sm + kC4Tw;
+    const int cc = threadIdx.x % kC4, t = threadIdx.x / kC4;
+    const float2 tv = gp(reinterpret_cast<const float2 *>(A.col.tw))[threadIdx.x % H];
+    const LAMA_GLOBAL float2 *src = gp(reinterpret_cast<const float2 *>(A.tmp)) + (long)c * H * Wh + x0 + cc;
+    float2 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = src[(t + 16 * j) * Wh];
+    if (threadIdx.x < H) tw[threadIdx.x] = tv;
+    __syncthreads();
+    col256_four_step(v, ex, tw, -1);
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh + x0 + cc, *dim = dre + H * Wh;
+#pragma unroll
+    for (int k2 = 0; k2 < 16; ++k2) {
+        dre[(t + 16 * k2) * Wh] = v[k2].x * A.scale;
+        dim[(t + 16 * k2) * Wh] = v[k2].y * A.scale;
+    }
+}
+
+// stacked [2C][256][129] -> tmp: inverse column transforms
+__device__ __forceinline__ void irfft2_cols_256_c4(const FftArgs &A, float2 *sm, int c, int x0)
+{
+    constexpr int H = 256, Wh = 129;
+    float2 *ex = sm, *tw = sm + kC4Tw;
+    const int cc = threadIdx.x % kC4, t = threadIdx.x / kC4;
+    const float2 tv = gp(reinterpret_cast<const float2 *>(A.col.tw))[threadIdx.x % H];
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh + x0 + cc, *sim = sre + H * Wh;
+    float2 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = make_float2(sre[(t + 16 * j) * Wh], sim[(t + 16 * j) * Wh]);
+    if (threadIdx.x < H) tw[threadIdx.x] = tv;
+    __syncthreads();
+    col256_four_step(v, ex, tw, 1);
+    LAMA_GLOBAL float2 *dst = gp(reinterpret_cast<float2 *>(A.tmp)) + (long)c * H * Wh + x0 + cc;
+#pragma unroll
+    for (int k2 = 0; k2 < 16; ++k2) dst[(t + 16 * k2) * Wh] = v[k2];
+}
+
 }  // namespace
 
-#define LAMA_FFT_SPLIT_CT(N)                                                                                         \
+#define LAMA_FFT_SPLIT_ROWS(N)                                                                                       \
     extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
     {                                                                                                                \
         side_priority();                                                                                             \
         LAMA_STAMP_SCOPE;                                                                                            \
         extern __shared__ float2 sm[];                                                                               \
         rfft2_rows_ct<N>(*args, sm);                                                                                 \
-    }                                                                                                                \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
-    {                                                                                                                \
-        side_priority();                                                                                             \
-        LAMA_STAMP_SCOPE;                                                                                            \
-        extern __shared__ float2 sm[];                                                                               \
-        using S = SplitCt<N>;                                                                                        \
-        const int c = blockIdx.x / S::CCH, ch = blockIdx.x % S::CCH;                                                 \
-        if (ch < S::CCH - 1)                                                                                         \
-            rfft2_cols_ct<N, S::CB>(*args, sm, c, ch * S::CB);                                                       \
-        else                                                                                                         \
-            rfft2_cols_ct<N, 1>(*args, sm, c, ch * S::CB);                                                           \
-    }                                                                                                                \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
-    {                                                                                                                \
-        side_priority();                                                                                             \
-        LAMA_STAMP_SCOPE;                                                                                            \
-        extern __shared__ float2 sm[];                                                                               \
-        using S = SplitCt<N>;                                                                                        \
-        const int c = blockIdx.x / S::CCH, ch = blockIdx.x % S::CCH;                                                 \
-        if (ch < S::CCH - 1)                                                                                         \
-            irfft2_cols_ct<N, S::CB>(*args, sm, c, ch * S::CB);                                                      \
-        else                                                                                                         \
-            irfft2_cols_ct<N, 1>(*args, sm, c, ch * S::CB);                                                          \
     }                                                                                                                \
     extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
     {                                                                                                                \
@@ -1241,6 +1343,60 @@ __device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
         extern __shared__ float2 sm[];                                                                               \
         irfft2_rows_ct<N>(*args, sm);                                                                                \
     }
-LAMA_FFT_SPLIT_CT(256)
-LAMA_FFT_SPLIT_CT(128)
-#undef LAMA_FFT_SPLIT_CT
+LAMA_FFT_SPLIT_ROWS(256)
+LAMA_FFT_SPLIT_ROWS(128)
+#undef LAMA_FFT_SPLIT_ROWS
+
+// 128 x 128 planes: Stockham column blocks of SplitCt<128>::CB columns, in
+// XCD-contiguous order
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols_128(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
+{
+    side_priority();
+    LAMA_STAMP_SCOPE;
+    extern __shared__ float2 sm[];
+    using S = SplitCt<128>;
+    const int blk = fft_xcd_order(blockIdx.x, (int)gridDim.x), c = blk / S::CCH, ch = blk % S::CCH;
+    if (ch < S::CCH - 1)
+        rfft2_cols_ct<128, S::CB>(*args, sm, c, ch * S::CB);
+    else
+        rfft2_cols_ct<128, 1>(*args, sm, c, ch * S::CB);
+}
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols_128(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
+{
+    side_priority();
+    LAMA_STAMP_SCOPE;
+    extern __shared__ float2 sm[];
+    using S = SplitCt<128>;
+    const int blk = fft_xcd_order(blockIdx.x, (int)gridDim.x), c = blk / S::CCH, ch = blk % S::CCH;
+    if (ch < S::CCH - 1)
+        irfft2_cols_ct<128, S::CB>(*args, sm, c, ch * S::CB);
+    else
+        irfft2_cols_ct<128, 1>(*args, sm, c, ch * S::CB);
+}
+
+// 256 x 256 planes: 128 / kC4 four-step blocks and the Nyquist column per
+// channel, kC4T threads per block (the host's launch shape, Engine::push_fft)
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols_256(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
+{
+    side_priority();
+    LAMA_STAMP_SCOPE;
+    extern __shared__ float2 sm[];
+    constexpr int NB = 128 / kC4 + 1;
+    const int blk = fft_xcd_order(blockIdx.x, (int)gridDim.x), c = blk / NB, ch = blk % NB;
+    if (ch < NB - 1)
+        rfft2_cols_256_c4(*args, sm, c, ch * kC4);
+    else
+        rfft2_cols_ct<256, 1>(*args, sm, c, 128);
+}
+extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols_256(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)
+{
+    side_priority();
+    LAMA_STAMP_SCOPE;
+    extern __shared__ float2 sm[];
+    constexpr int NB = 128 / kC4 + 1;
+    const int blk = fft_xcd_order(blockIdx.x, (int)gridDim.x), c = blk / NB, ch = blk % NB;
+    if (ch < NB - 1)
+        irfft2_cols_256_c4(*args, sm, c, ch * kC4);
+    else
+        irfft2_cols_ct<256, 1>(*args, sm, c, 128);
+}

@@ -857,6 +857,13 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
     if (H == W && (H == 256 || H == 128) && !(gen && atoi(gen) == 1) && g.rows_per_block == per_block &&
         g.cols_per_block == per_block)
         g.ct_split = H;
+    // the 256 x 256 column launches: four-step blocks of LAMA_FFT_C4 columns
+    // (16 threads each) plus one Nyquist-column block per channel
+    if (g.ct_split == 256) {
+        g.grid_cols = (unsigned)(C * (128 / LAMA_FFT_C4 + 1));
+        g.block_cols = 16 * LAMA_FFT_C4;
+        g.lds_cols = (std::max<size_t>(256 * LAMA_FFT_C4, 2 * (size_t)per_block * 256) + 256) * f2;
+    }
     return true;
 }
 
@@ -886,6 +893,7 @@ void Engine::push_fft(Plan &p, bool inverse, const FftGeom &g, void *arg, int st
         const bool rows = inverse ? k == 1 : k == 0;
         L.fn = g.ct_split ? fn_split_ct_[g.ct_split == 256 ? 0 : 1][inverse ? 2 + k : k] : fn_split_[inverse ? 2 + k : k];
         L.grid = rows ? g.grid_rows : g.grid_cols;
+        L.block = !rows && g.block_cols ? g.block_cols : LAMA_FFT_NT;
         L.shmem = (unsigned)(rows ? g.lds_rows : g.lds_cols);
         L.bytes = k == 0 ? bytes_a : bytes_b;
         p.launches.push_back(L);

@@ -69,6 +69,7 @@ struct FftGeom {
     size_t tmp_bytes = 0;           // interleaved complex [C][H][W/2+1]
     int ct = 0;                     // single-block square plane with compile-time kernels: 1 + index in kFftCtSide, else 0
     int ct_split = 0;               // split square plane with compile-time kernels (128 or 256), else 0
+    unsigned block_cols = 0;        // threads per column-launch block when not LAMA_FFT_NT
 };
 
 struct ArenaLayout {
