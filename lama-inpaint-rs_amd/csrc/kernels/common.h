@@ -23,6 +23,10 @@
 // or columns per block = this / (2 * 8 * plane side)).  32 KB rather than 64:
 // a block then fits on a CU beside the FFC GEMM's two workgroups (51 KB each),
 // so the side stream's transforms are not held back by that GEMM's launches.
+// F(4,3) weights: two MFMA steps per 16-byte load (1) or one per 8-byte load (0)
+#ifndef LAMA_W4_WX4
+#define LAMA_W4_WX4 1
+#endif
 #ifndef LAMA_FFT_SPLIT_LDS
 #define LAMA_FFT_SPLIT_LDS (32 * 1024)
 #endif

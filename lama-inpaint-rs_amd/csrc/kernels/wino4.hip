@@ -97,18 +97,37 @@ __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int 
 
 // A wave's MFMA A operands of one chunk: for steps s = ky * 3 + q (position
 // u = 3 wu + q) lane (g, j) holds the transformed weights of output channel
-// wm * 32 + j and input channels 2g, 2g + 1 of the chunk, 64 lanes x 8
-// contiguous bytes per step (`wb` is the wave's lane's first float).
+// wm * 32 + j and input channels 2g, 2g + 1 of the chunk.  LAMA_W4_WX4: steps
+// 2p and 2p + 1 (p < 4) are one 16-byte load per lane (64 lanes x 16
+// contiguous bytes), step 8 an 8-byte one -- five loads per chunk instead of
+// nine; else 64 lanes x 8 contiguous bytes per step.  `wb` is the wave's
+// first float (WX4) or its lane's.
 template <class C>
 __device__ __forceinline__ void w4_load_w(float (&w)[2 * C::NS], const LAMA_GLOBAL float *wb, int ck)
 {
     const LAMA_GLOBAL float *p = wb + (long)ck * C::WCH;
+#if LAMA_W4_WX4
+    static_assert(C::NS == 9, "four step pairs and a last step");
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(p + q * 256 + lane * 4);
+        w[4 * q] = v.x;
+        w[4 * q + 1] = v.y;
+        w[4 * q + 2] = v.z;
+        w[4 * q + 3] = v.w;
+    }
+    const float2 v = *reinterpret_cast<const LAMA_GLOBAL float2 *>(p + 1024 + lane * 2);
+    w[16] = v.x;
+    w[17] = v.y;
+#else
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
         const float2 v = *reinterpret_cast<const LAMA_GLOBAL float2 *>(p + s * 128);
         w[2 * s] = v.x;
         w[2 * s + 1] = v.y;
     }
+#endif
 }
 
 // The input rows d0..d5 of each of the thread's items of chunk `ck`.
@@ -216,7 +235,8 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
         w4_slots<C>(sl, sg, oy0, ox0);
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         // the M block's weights (64 rows of wrow floats), then this wave's and lane's operands
-        const LAMA_GLOBAL float *wb = gp(sg.wt) + (long)mb * 64 * sg.wrow + wave * (C::NS * 128) + lane * 2;
+        const LAMA_GLOBAL float *wb =
+            gp(sg.wt) + (long)mb * 64 * sg.wrow + wave * (C::NS * 128) + (LAMA_W4_WX4 ? 0 : lane * 2);
         float *l0 = lds, *l1 = lds + C::V_LDS;
         float w0[2 * C::NS], w1[2 * C::NS];
         W4Stage<C> r0, r1;

@@ -269,7 +269,8 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
 // 64 output channels (rows past M zero) and chunk of 4 input channels,
 // [wave (wm, wu)][step s = ky * 3 + q][lane (g, j)][c] holds U_u for output
 // channel 32 wm + j, input channel 2g + c of the chunk and position
-// u = 3 wu + q.  A chunk is 64 x 72 floats (T * KC); the block stride is 64
+// u = 3 wu + q (with LAMA_W4_WX4, steps 2p and 2p + 1 of a wave interleaved
+// as [p][lane][step 2p + h][c], step 8 after them as [lane][c]).  A chunk is 64 x 72 floats (T * KC); the block stride is 64
 // rows of wrow = nchunk * 72.
 Packed pack_wino4(Arena &A, int M, int C, const std::function<float(int, int, int)> &get)
 {
@@ -300,7 +301,13 @@ Packed pack_wino4(Arena &A, int M, int C, const std::function<float(int, int, in
                             double v = 0;
                             if (co < M && ci < C)
                                 for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
-                            blk[((wave * 9 + st) * 64 + lane) * 2 + c] = (float)v;
+                            // LAMA_W4_WX4: steps 2q, 2q + 1 interleaved per lane (one 16-byte
+                            // load), step 8 after them
+                            const size_t at = LAMA_W4_WX4 ? (size_t)wave * 9 * 128 +
+                                                                (st < 8 ? (st / 2) * 256 + lane * 4 + (st % 2) * 2
+                                                                        : 1024 + lane * 2)
+                                                          : ((size_t)(wave * 9 + st) * 64 + lane) * 2;
+                            blk[at + c] = (float)v;
                         }
         }
     return p;
