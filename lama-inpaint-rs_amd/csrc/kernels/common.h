@@ -195,6 +195,7 @@ struct ConvProblem {
     int tiles_x, tiles_y, mblocks, nblocks;
     const float *bias, *addend, *scale, *shift;
     int relu;
+    int vec_in;  // F(4,3) kernels: the input rows as 16-byte loads (plane width a multiple of 4)
     const float *res;
     float *out;
     long out_cstride;  // floats between output channel planes

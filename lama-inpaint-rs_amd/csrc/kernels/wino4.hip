@@ -38,8 +38,12 @@
 
 namespace {
 
-template <int NTR_>
+template <int NTR_, bool V4_ = false>
 struct W4Cfg {
+    // V4: the plane width is a multiple of 4, so each tile's inputs d1..d4 are
+    // one aligned 16-byte load (d0 and d5, reflect-mapped at the edges, two
+    // scalar ones): three loads per item instead of six
+    static constexpr bool V4 = V4_;
     static constexpr int KC = LAMA_WINO_KC;      // input channels per chunk
     static constexpr int NU = 6, KY = 3;         // Winograd positions, kernel rows
     static constexpr int NUW = NU / 2;           // positions per wave
@@ -91,6 +95,12 @@ __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int 
             const int ix = reflect1(ox0 + 4 * t - 1 + c, sg.IW);
             sl.po[it][c] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + ix));
         }
+        if constexpr (C::V4) {
+            // d1..d4 in place; a tile past the plane's right edge (outputs
+            // dropped) reads the row's last quad instead
+            const int x4 = min(ox0 + 4 * t, sg.IW - 4);
+            sl.po[it][1] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + x4));
+        }
         sl.vl[it] = idx < C::NITEM ? r * C::VRS + t * C::KCP + ci : C::IR * C::VRS + (idx - C::NITEM) % 64;
     }
 }
@@ -140,10 +150,24 @@ __device__ __forceinline__ void w4_load_d(W4Stage<C> &st, const W4Slots<C> &sl, 
     const int c0 = min(ck * C::KC, sg.C - 1);
     const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
     const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
+    if constexpr (C::V4) {
+        const unsigned last4 = last - 12u;  // the last quad: 16-byte aligned, as the plane size is
 #pragma unroll
-    for (int it = 0; it < C::VITER; ++it)
+        for (int it = 0; it < C::VITER; ++it) {
+            const float4 m = *at_byte<float4>(src, min(sl.po[it][1], last4));
+            st.d[it][0] = *at_byte<float>(src, min(sl.po[it][0], last));
+            st.d[it][1] = m.x;
+            st.d[it][2] = m.y;
+            st.d[it][3] = m.z;
+            st.d[it][4] = m.w;
+            st.d[it][5] = *at_byte<float>(src, min(sl.po[it][5], last));
+        }
+    } else {
 #pragma unroll
-        for (int c = 0; c < 6; ++c) st.d[it][c] = *at_byte<float>(src, min(sl.po[it][c], last));
+        for (int it = 0; it < C::VITER; ++it)
+#pragma unroll
+            for (int c = 0; c < 6; ++c) st.d[it][c] = *at_byte<float>(src, min(sl.po[it][c], last));
+    }
 }
 
 // V = B^T d of each item into the LDS stage `vl`.
@@ -380,11 +404,16 @@ __device__ __forceinline__ int w4_xcd_order(int i, int n)
         LAMA_CONV_STARTS;                                                                  \
         LAMA_STAMP_BEGIN;                                                                  \
         using C = W4Cfg<NTR>;                                                              \
+        using C4 = W4Cfg<NTR, true>;                                                       \
+        static_assert(C4::LDS == C::LDS, "one LDS layout");                               \
         __shared__ __attribute__((aligned(16))) float lds[C::LDS];                         \
         __shared__ float epl[192];                                                         \
         int b = w4_xcd_order(blockIdx.x, gridDim.x);                                       \
         int pi = find_problem(ps, b);                                                      \
-        w4_tile<C>(probs[pi], b, lds, epl);                                                \
+        if (probs[pi].vec_in && (probs[pi].s0.IW & 3) == 0)                                 \
+            w4_tile<C4>(probs[pi], b, lds, epl);                                           \
+        else                                                                               \
+            w4_tile<C>(probs[pi], b, lds, epl);                                            \
         LAMA_STAMP_END;                                                                    \
     }
 LAMA_W4_KERNEL(lama_conv3x3w4, 16)

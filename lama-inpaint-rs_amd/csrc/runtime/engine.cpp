@@ -1265,6 +1265,11 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             kslices(raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8, W8,
                                 nullptr)),
                     ks, (long)384 * P8)};
+        // 16-byte input loads in A only: the same loads in B as well made B
+        // faster but slowed the spectral chain beside it more (512x512:
+        // 272.3-272.4 passes/s with A only, 270.8-270.9 with both, 271.3-271.6
+        // with neither)
+        for (ConvProblem &q : probs) q.vec_in = wino_ == 4 && W8 % 4 == 0;
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
                     k % 2 ? EV_A1 : EV_A0);
@@ -2381,6 +2386,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.out_cstride = (long)oh * ow;
     q.outW = q.OW;
     q.oy_mul = q.ox_mul = 1;
+    q.vec_in = wino == 4 && family == F_CONV3 && w % 4 == 0;  // both F(4,3) load paths, by width
     pw_xcd_pad(family, q);
     UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
     if (!check(hip_->hipMemcpy(dq, &q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;

@@ -248,6 +248,11 @@ W4_CASES = WINO_CASES + [
     (8, 64, 5, 75),       # the 600x600 bottleneck width: 75 = 2 x 32 + 11 (or 64 + 11)
     (16, 32, 9, 32),      # the 256x256 bottleneck width
     (4, 70, 7, 3),        # narrower than one Winograd tile
+    # widths that are multiples of 4 take the 16-byte input loads: a partial
+    # last block (36 = 32 + 4, 100 = 64 + 32 + 4) and a plane of one quad
+    (12, 40, 6, 36),
+    (8, 96, 11, 100),
+    (4, 8, 5, 4),
 ]
 
 
