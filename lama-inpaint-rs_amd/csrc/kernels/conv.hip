@@ -892,6 +892,98 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv7x7(LAMA_CONV_PAR
     LAMA_STAMP_END;
 }
 
+// model.1 with each wave's weights in registers (the plan's head: 4 input
+// and 64 output channels, one chunk).  Lane (g, j) of wave (wm, wn) holds the
+// MFMA A operands of output channel wm * 32 + j, input channels 2g and 2g + 1,
+// for all 49 taps (98 registers), loaded once; LDS holds only the two patch
+// buffers (15 KB instead of 68 KB with the staged weights), so three
+// workgroups share a CU instead of two.  The host caps the grid at three per
+// CU; each workgroup walks tiles blockIdx.x, + gridDim.x, ... as lama_conv7x7
+// does, with the next tile's patch loaded into registers during this tile's
+// MFMAs.
+extern "C" __global__ void __launch_bounds__(LAMA_NT) __attribute__((amdgpu_waves_per_eu(3, 3)))
+lama_conv7x7r(LAMA_CONV_PARAMS)
+{
+    using C = CfgHead;
+    __shared__ __attribute__((aligned(16))) float pls[2 * C::P_LDS];
+    __shared__ float epl[192];
+    float *const pl0 = pls, *const pl1 = pls + C::P_LDS;
+    LAMA_STAMP_BEGIN;
+    const ConvProblem &P = probs[0];
+    const ConvSeg sg = P.s0;
+    const int ntiles = P.nblocks;
+    int t = blockIdx.x;
+    if (t >= ntiles) {  // whole workgroup
+        LAMA_STAMP_END;
+        return;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
+    auto origin = [&](int tile, int &oy0, int &ox0) {
+        oy0 = (tile / P.tiles_x) * C::TR;
+        ox0 = (tile % P.tiles_x) * C::TC;
+    };
+    Slots<C> sl;
+    Stage<C> cur, nxt;
+    int oy0, ox0, ny0, nx0;
+    origin(t, oy0, ox0);
+    make_pslots<C>(sl, sg, oy0, ox0);
+    load_p<C>(cur, sl, sg, 0);
+    // this lane's A operands: packed row wm * 32 + j, floats tap * KC + 2g, +1
+    float a[C::T][2];
+    {
+        const LAMA_GLOBAL float *wr = gp(sg.wt) + (long)min(wm * 32 + j, P.M - 1) * sg.wrow + g * (C::KC / 2);
+#pragma unroll
+        for (int tp = 0; tp < C::T; ++tp) {
+            a[tp][0] = wr[tp * C::KC];
+            a[tp][1] = wr[tp * C::KC + 1];
+        }
+    }
+    const float ep = epi_param_load(P, 0);
+    int tn = min(t + (int)gridDim.x, ntiles - 1);  // the last tile is re-read instead of branching
+    origin(tn, ny0, nx0);
+    make_pslots<C>(sl, sg, ny0, nx0);
+    load_p<C>(nxt, sl, sg, 0);
+    store_p<C>(cur, sl, pl0);
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    __syncthreads();
+    EpiPre pre;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pre.add[r] = pre.res[r] = 0.f;
+    const int p = wn * 32 + j, pr = p / C::TC, pc = p % C::TC;
+    const int pbase = (pr * C::PCP + C::col(pc)) * C::KCP + g * (C::KC / 2);
+    for (int i = 0;; ++i) {
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+        const float *prow = ((i & 1) ? pl1 : pl0) + pbase;
+        float b[2][2];
+        lds_vec<2>(b[0], prow);
+#pragma unroll
+        for (int tp = 0; tp < C::T; ++tp) {
+            const int cb = tp & 1;
+            if (tp + 1 < C::T) {
+                const int ky = (tp + 1) / C::KW, kx = (tp + 1) % C::KW;
+                lds_vec<2>(b[cb ^ 1], prow + (ky * C::PCP + C::col(kx)) * C::KCP);
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tp][0], b[cb][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tp][1], b[cb][1], acc, 0, 0, 0);
+        }
+        epilogue<C::TR, C::TC, false>(acc, pre, P, epl, 0, oy0, ox0);
+        t += gridDim.x;
+        if (t >= ntiles) break;
+        oy0 = ny0;
+        ox0 = nx0;
+        store_p<C>(nxt, sl, (i & 1) ? pl0 : pl1);
+        tn = min(t + (int)gridDim.x, ntiles - 1);
+        origin(tn, ny0, nx0);
+        make_pslots<C>(sl, sg, ny0, nx0);
+        load_p<C>(nxt, sl, sg, 0);
+        __syncthreads();
+    }
+    LAMA_STAMP_END;
+}
+
 // XCD-contiguous order within each problem of the stride-2 and transposed
 // convolutions: the dispatcher deals workgroups to the eight XCDs
 // round-robin (workgroup i to XCD i mod 8), each XCD with its own L2.  Block j

@@ -468,7 +468,7 @@ bool Engine::open(std::string &err)
         !get_fn(fn_finalize_g2_[0], "lama_finalize_g2", err) ||
         !get_fn(fn_finalize_g2_[1], "lama_finalize10_g2", err) ||
         !get_fn(fn_finalize_g2_[2], "lama_finalize20_g2", err) ||
-        !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
+        !get_fn(fn_head_r_, "lama_conv7x7r", err) || !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
         !get_fn(fn_edge_q_[1], "lama_convt_q", err) ||
         !get_fn(fn_convt_rows_[0], "lama_convt_rows", err) ||
         !get_fn(fn_convt_rows_[1], "lama_convt_rows_q", err))
@@ -485,6 +485,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_EDGE_TILE")) edge_force_ = atoi(t);
     if (const char *t = getenv("LAMA_W4_LDSPAD")) w4_ldspad_force_ = atoi(t);
     if (const char *t = getenv("LAMA_CONVT_ROWS")) convt_rows_ = atoi(t) != 0;
+    if (const char *t = getenv("LAMA_HEAD_R")) head_r_ = atoi(t) != 0;
 
     for (int s = 0; s < 3; ++s)
         for (int f = 0; f < 2; ++f)
@@ -682,6 +683,8 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
 hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
 {
+    // the head as one chunk and one M block: the kernel with register-resident weights
+    if (family == F_CONV7 && head_r_ && n == 1 && probs[0].s0.nchunk == 1 && probs[0].mblocks == 1) return fn_head_r_;
     if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_variant(probs[0].OH, probs[0].OW)];
     if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
     if (family == F_CONVT && convt_rows_) return fn_convt_rows_[tile_variant(family, probs[0].OH, probs[0].OW)];
@@ -1133,8 +1136,9 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
                  family != F_CONV1))
                 bad_problem = true;
         }
-        // the head kernel walks its tiles: two resident workgroups per CU
-        L.grid = family == F_CONV7 ? std::min(nb, 2u * LAMA_CUS) : nb;
+        // the head kernels walk their tiles: three (register weights) or two
+        // (weights in LDS) resident workgroups per CU
+        L.grid = family == F_CONV7 ? std::min(nb, (L.fn == fn_head_r_ ? 3u : 2u) * LAMA_CUS) : nb;
         L.shmem = (family == F_CONV3 || family == F_CONV3G) && wino_ == 4 ? w4_shmem : 0;
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
         L.ps = prob_starts(probs.data(), probs.size());

@@ -278,6 +278,8 @@ private:
     hipFunction_t fn_finalize_ks_[2] = {};  // lama_finalize10, lama_finalize20 (K split 2, 4)
     hipFunction_t fn_finalize_g2_[3] = {};  // the same three with two element groups per thread
     hipFunction_t fn_edge_q_[2] = {};       // lama_conv3x3s2_q, lama_convt_q (4 x 16 tiles)
+    hipFunction_t fn_head_r_ = nullptr;     // lama_conv7x7r (the 4 -> 64 head, weights in registers)
+    bool head_r_ = true;                    // LAMA_HEAD_R=0: the head through lama_conv7x7 (weights in LDS)
     hipFunction_t fn_convt_rows_[2] = {};   // lama_convt_rows (2 x 32 positions), lama_convt_rows_q (4 x 16)
 
     // profiling
