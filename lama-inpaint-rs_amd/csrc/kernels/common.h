@@ -8,6 +8,11 @@
 #define LAMA_CUS 256     // compute units of an MI355X (grid sizing of tile-walking kernels)
 // input channels per K chunk of the pointwise (1x1) convolutions; their
 // weights are packed in chunks of this many
+// conv2 (lama_conv1x1_res*): 1 = 64 x 32 tiles whose waves split each
+// 2 * LAMA_PW_KC-channel chunk's K slots in halves; 0 = 64 x 64 tiles
+#ifndef LAMA_PW_RES_KH
+#define LAMA_PW_RES_KH 1
+#endif
 #ifndef LAMA_PW_KC
 #define LAMA_PW_KC 16
 #endif

@@ -376,18 +376,24 @@ __device__ __forceinline__ void run_segment(Acc &acc, const ConvSeg &sg_mem, int
 // differ by 32 banks.  VW = 4: planes are 16-byte aligned with N % 4 == 0
 // (one float4 load per run); VW = 2: 8-byte aligned with N % 2 == 0 and
 // N >= 4 (two float2 loads); VW = 1: four clamped scalar loads.
-template <int KC_, int VW_, int NPX_>
+// KH (K halves, NPX = 32): wave (wm, kh) takes channels wm*32.. +32, all 32
+// pixels, and half of every chunk's K slots (kh = wave & 1); the two halves'
+// sums meet in LDS after the K loop.  Half the dependent MFMA chain per wave
+// and twice the workgroups of a 64-pixel tile, for the conv2 launch, which
+// runs nearly alone on the FFC's critical path.
+template <int KC_, int VW_, int NPX_, bool KH_ = false>
 struct PwCfg {
     static constexpr int VW = VW_;  // activation load width: float4, float2 or scalar
     static constexpr bool VEC = VW_ > 1;
-    static constexpr int KC = KC_, NPX = NPX_, NACC = NPX / 64;
+    static constexpr bool KH = KH_;
+    static constexpr int KC = KC_, NPX = NPX_, NACC = KH ? 1 : NPX / 64;
     static constexpr int WSTR = KC + 4;              // weight row stride, = 4 (mod 8)
     static constexpr int HALF = KC / 2 * NPX + 32;   // one lane half's channel rows
     static constexpr int W_LDS = 64 * WSTR;
     static constexpr int LDS = W_LDS + 2 * HALF;
     static constexpr int WITER = 64 * KC / 4 / LAMA_NT;   // weight float4s per thread
     static constexpr int XITER = KC * NPX / 4 / LAMA_NT;  // activation runs per thread
-    static_assert(NPX == 64 || NPX == 128, "64 or 128 pixels per tile");
+    static_assert(KH ? NPX == 32 && KC % 16 == 0 : NPX == 64 || NPX == 128, "64 or 128 pixels per tile, 32 with KH");
     static_assert(WITER * LAMA_NT * 4 == 64 * KC && XITER * LAMA_NT * 4 == KC * NPX, "whole float4 slots");
     static_assert(KC % 8 == 0 && WSTR % 8 == 4 && HALF % 64 == 32, "bank placement");
 };
@@ -489,6 +495,19 @@ __device__ __forceinline__ void pw_compute_chunk(f32x16 (&acc)[C::NACC], const f
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, j = lane & 31;
     constexpr int H = C::KC / 2;
+    if constexpr (C::KH) {
+        // K slots g * H + wn * H/2 + c of the chunk (c < H/2): this wave's half
+        constexpr int HH = H / 2;
+        const float *wrow = lds + (wm * 32 + j) * C::WSTR + g * H + wn * HH;
+        const float *xrow = lds + C::W_LDS + g * C::HALF + wn * HH * C::NPX + j;
+        float a[HH], b[HH];
+        lds_vec<HH>(a, wrow);
+#pragma unroll
+        for (int c = 0; c < HH; ++c) b[c] = xrow[c * C::NPX];
+#pragma unroll
+        for (int c = 0; c < HH; ++c) acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c], b[c], acc[0], 0, 0, 0);
+        return;
+    }
     const float *wrow = lds + (wm * 32 + j) * C::WSTR + g * H;
     const float *xrow = lds + C::W_LDS + g * C::HALF + wn * (C::NPX / 2) + j;
     float a[H];
@@ -704,7 +723,9 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
     EpiPre pre[C::NACC];
 #pragma unroll
     for (int h = 0; h < C::NACC; ++h) {
-        if constexpr (PREFETCH) {
+        if constexpr (PREFETCH && C::KH) {
+            if (wn == 0) epilogue_prefetch<1, 32>(pre[h], P, m0, 0, ox0);  // the K-half that stores
+        } else if constexpr (PREFETCH) {
             epilogue_prefetch<1, 64>(pre[h], P, m0, 0, ox0 + wn * (C::NPX / 2 - 32) + h * 32);
         } else {
 #pragma unroll
@@ -725,6 +746,22 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
         sg.nchunk = P.kchunks;
     }
     run_segment_pw<C, D>(acc, sg, m0, P.M, ox0, lds);
+    if constexpr (C::KH) {
+        // K half 1 hands its sums to half 0 (the staging buffers are free
+        // after the K loop's last barrier), which runs the epilogue
+        const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
+        float *xs = lds + wm * 16 * 64 + lane;
+        if (wn == 1)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xs[r * 64] = acc[0][r];
+        if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+        __syncthreads();
+        if (wn == 1) return;  // no barrier follows
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][r] += xs[r * 64];
+        epilogue<1, 32, PREFETCH>(acc[0], pre[0], P, epl, m0, 0, ox0, (long)ks * P.out_kstride);
+        return;
+    }
     if (threadIdx.x < 192) epl[threadIdx.x] = ep;
     __syncthreads();
 #pragma unroll
@@ -1054,13 +1091,13 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 // conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
 // N % 4 == 0, lama_conv1x1_v2 8-byte aligned planes with N % 2 == 0 and
 // N >= 4; lama_conv1x1_s takes any N.
-#define LAMA_PW_KERNEL(NAME, KC, VW, NPX, PREFETCH, D)                                                      \
+#define LAMA_PW_KERNEL(NAME, KC, VW, NPX, PREFETCH, D, KH)                                                  \
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(LAMA_CONV_PARAMS) \
     {                                                                                                       \
         side_priority();                                                                                    \
         LAMA_CONV_STARTS;                                                                                   \
         LAMA_STAMP_BEGIN;                                                                                   \
-        using C = PwCfg<KC, VW, NPX>;                                                                      \
+        using C = PwCfg<KC, VW, NPX, KH>;                                                                  \
         __shared__ __attribute__((aligned(16))) float lds[2 * C::LDS];                                      \
         __shared__ float epl[192];                                                                          \
         int b = blockIdx.x;                                                                                 \
@@ -1071,15 +1108,21 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 #ifndef LAMA_PW_DEPTH_RES
 #define LAMA_PW_DEPTH_RES LAMA_PW_DEPTH
 #endif
-LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, 4, 64, false, LAMA_PW_DEPTH)
-LAMA_PW_KERNEL(lama_conv1x1_v2, LAMA_PW_KC, 2, 64, false, LAMA_PW_DEPTH)
-LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, 1, 64, false, LAMA_PW_DEPTH)
+LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, 4, 64, false, LAMA_PW_DEPTH, false)
+LAMA_PW_KERNEL(lama_conv1x1_v2, LAMA_PW_KC, 2, 64, false, LAMA_PW_DEPTH, false)
+LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, 1, 64, false, LAMA_PW_DEPTH, false)
 
 // The SpectralTransform conv2, whose epilogue adds the l2g partial and the
 // residual (fetched before the K loop).
-LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, 4, 64, true, LAMA_PW_DEPTH_RES)
-LAMA_PW_KERNEL(lama_conv1x1_res_v2, LAMA_PW_KC, 2, 64, true, LAMA_PW_DEPTH_RES)
-LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, 1, 64, true, LAMA_PW_DEPTH_RES)
+#if LAMA_PW_RES_KH
+LAMA_PW_KERNEL(lama_conv1x1_res, 2 * LAMA_PW_KC, 4, 32, true, LAMA_PW_DEPTH_RES, true)
+LAMA_PW_KERNEL(lama_conv1x1_res_v2, 2 * LAMA_PW_KC, 2, 32, true, LAMA_PW_DEPTH_RES, true)
+LAMA_PW_KERNEL(lama_conv1x1_res_s, 2 * LAMA_PW_KC, 1, 32, true, LAMA_PW_DEPTH_RES, true)
+#else
+LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, 4, 64, true, LAMA_PW_DEPTH_RES, false)
+LAMA_PW_KERNEL(lama_conv1x1_res_v2, LAMA_PW_KC, 2, 64, true, LAMA_PW_DEPTH_RES, false)
+LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, 1, 64, true, LAMA_PW_DEPTH_RES, false)
+#endif
 #undef LAMA_PW_KERNEL
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions

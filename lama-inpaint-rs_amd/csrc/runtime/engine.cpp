@@ -110,7 +110,7 @@ void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
         tc = 64;
     } else if (family == F_CONV1 || family == F_CONV1R) {
         tr = 1;
-        tc = 64;
+        tc = family == F_CONV1R && LAMA_PW_RES_KH ? 32 : 64;  // conv2: K-half tiles of 64 x 32
     } else if ((family == F_CONV3S2 || family == F_CONVT) && w4v == 1) {  // the _q kernels
         tr = 4;
         tc = 16;
@@ -1366,6 +1366,10 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
         ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
                                  ffc_dst(k) + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
+        // K-half tiles walk chunks of 2 * LAMA_PW_KC channels (a 1x1 row is its
+        // channels in order, so only the chunk count differs)
+        static_assert(!LAMA_PW_RES_KH || 192 % (2 * LAMA_PW_KC) == 0, "whole conv2 chunks");
+        if (LAMA_PW_RES_KH) q2.s0.nchunk = 192 / (2 * LAMA_PW_KC);
         q2.addend = gc_buf(k);
         q2.naddend = ks;  // the l2g K slices
         q2.addend_kstride = (long)384 * P8;
