@@ -8,14 +8,18 @@
 #define LAMA_CUS 256     // compute units of an MI355X (grid sizing of tile-walking kernels)
 // input channels per K chunk of the pointwise (1x1) convolutions; their
 // weights are packed in chunks of this many
-// conv2 (lama_conv1x1_res*): 1 = 64 x 32 tiles whose waves split each
-// 2 * LAMA_PW_KC-channel chunk's K slots in halves; 0 = 64 x 64 tiles
-#ifndef LAMA_PW_RES_KH
-#define LAMA_PW_RES_KH 1
+// Pointwise convolutions over float4-aligned planes whose 64 x 64 tiles would
+// give at most two workgroups per CU: 1 = the K-half kernels
+// (lama_conv1x1_kh, lama_conv1x1_res_kh: 64 x 32 tiles whose waves split each
+// 2 * LAMA_PW_KC-channel chunk's K slots in halves), 0 = 64 x 64 tiles there
+// too.  Larger planes and those with N % 4 != 0 keep 64 x 64.
+#ifndef LAMA_PW_KH
+#define LAMA_PW_KH 1
 #endif
 #ifndef LAMA_PW_KC
 #define LAMA_PW_KC 16
 #endif
+
 #define LAMA_FFT_NT 512  // threads per FFT block (8 waves)
 // pointwise convolutions: all M blocks of a pixel strip on one XCD
 #ifndef LAMA_PW_XCD
@@ -28,6 +32,14 @@
 // or columns per block = this / (2 * 8 * plane side)).  32 KB rather than 64:
 // a block then fits on a CU beside the FFC GEMM's two workgroups (51 KB each),
 // so the side stream's transforms are not held back by that GEMM's launches.
+// F(4,3) input rows as 16-byte loads in the g2l launch as well as in the l2l +
+// l2g one (where the plane width is a multiple of 4).  With 64 x 64 pointwise
+// tiles this made the GEMM faster but the spectral chain beside it slower
+// (512x512: 270.8-270.9 passes/s against 272.3-272.4 with A alone); with the
+// K-half pointwise tiles it gains (279.8-279.9 against 277.8-278.1).
+#ifndef LAMA_W4_VEC_B
+#define LAMA_W4_VEC_B 1
+#endif
 // F(4,3) weights: two MFMA steps per 16-byte load (1) or one per 8-byte load (0)
 #ifndef LAMA_W4_WX4
 #define LAMA_W4_WX4 1

@@ -1088,7 +1088,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 }
 
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
-// conv), 64 x 64 tiles.  lama_conv1x1 needs 16-byte aligned planes with
+// conv): lama_conv1x1_kh in 64 x 32 K-half tiles, the others in 64 x 64
+// tiles.  lama_conv1x1 and _kh need 16-byte aligned planes with
 // N % 4 == 0, lama_conv1x1_v2 8-byte aligned planes with N % 2 == 0 and
 // N >= 4; lama_conv1x1_s takes any N.
 #define LAMA_PW_KERNEL(NAME, KC, VW, NPX, PREFETCH, D, KH)                                                  \
@@ -1109,20 +1110,16 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 #define LAMA_PW_DEPTH_RES LAMA_PW_DEPTH
 #endif
 LAMA_PW_KERNEL(lama_conv1x1, LAMA_PW_KC, 4, 64, false, LAMA_PW_DEPTH, false)
+LAMA_PW_KERNEL(lama_conv1x1_kh, 2 * LAMA_PW_KC, 4, 32, false, LAMA_PW_DEPTH, true)
 LAMA_PW_KERNEL(lama_conv1x1_v2, LAMA_PW_KC, 2, 64, false, LAMA_PW_DEPTH, false)
 LAMA_PW_KERNEL(lama_conv1x1_s, LAMA_PW_KC, 1, 64, false, LAMA_PW_DEPTH, false)
 
 // The SpectralTransform conv2, whose epilogue adds the l2g partial and the
 // residual (fetched before the K loop).
-#if LAMA_PW_RES_KH
-LAMA_PW_KERNEL(lama_conv1x1_res, 2 * LAMA_PW_KC, 4, 32, true, LAMA_PW_DEPTH_RES, true)
-LAMA_PW_KERNEL(lama_conv1x1_res_v2, 2 * LAMA_PW_KC, 2, 32, true, LAMA_PW_DEPTH_RES, true)
-LAMA_PW_KERNEL(lama_conv1x1_res_s, 2 * LAMA_PW_KC, 1, 32, true, LAMA_PW_DEPTH_RES, true)
-#else
 LAMA_PW_KERNEL(lama_conv1x1_res, LAMA_PW_KC, 4, 64, true, LAMA_PW_DEPTH_RES, false)
+LAMA_PW_KERNEL(lama_conv1x1_res_kh, 2 * LAMA_PW_KC, 4, 32, true, LAMA_PW_DEPTH_RES, true)
 LAMA_PW_KERNEL(lama_conv1x1_res_v2, LAMA_PW_KC, 2, 64, true, LAMA_PW_DEPTH_RES, false)
 LAMA_PW_KERNEL(lama_conv1x1_res_s, LAMA_PW_KC, 1, 64, true, LAMA_PW_DEPTH_RES, false)
-#endif
 #undef LAMA_PW_KERNEL
 
 // ConvTranspose2d k3 s2 p1 op1 as four sub-pixel phase convolutions

@@ -100,6 +100,10 @@ ProbStarts prob_starts(const ConvProblem *q, size_t n)
 // Pixel tile (rows x columns) of a conv family; `w4v` is the tile variant
 // (Engine::tile_variant): the F(4,3) block shape, or for the stride-2 and
 // transposed convolutions 0 = 2 x 32, 1 = 4 x 16.
+// Channels per K chunk of the pointwise kernel a plane of tile variant v runs
+// (Engine::tile_variant: 0 = the K-half kernels, 1 = the 64 x 64 ones).
+int pw_kc(int v) { return v == 0 ? 2 * LAMA_PW_KC : LAMA_PW_KC; }
+
 void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
 {
     if ((family == F_CONV3 || family == F_CONV3G) && wino == 4) {  // lama_conv3x3w4 / w4n / w4q
@@ -110,7 +114,7 @@ void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
         tc = 64;
     } else if (family == F_CONV1 || family == F_CONV1R) {
         tr = 1;
-        tc = family == F_CONV1R && LAMA_PW_RES_KH ? 32 : 64;  // conv2: K-half tiles of 64 x 32
+        tc = w4v == 0 ? 32 : 64;  // variant 0: the K-half kernels' tiles
     } else if ((family == F_CONV3S2 || family == F_CONVT) && w4v == 1) {  // the _q kernels
         tr = 4;
         tc = 16;
@@ -468,7 +472,8 @@ bool Engine::open(std::string &err)
         !get_fn(fn_finalize_g2_[0], "lama_finalize_g2", err) ||
         !get_fn(fn_finalize_g2_[1], "lama_finalize10_g2", err) ||
         !get_fn(fn_finalize_g2_[2], "lama_finalize20_g2", err) ||
-        !get_fn(fn_head_r_, "lama_conv7x7r", err) || !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
+        !get_fn(fn_head_r_, "lama_conv7x7r", err) || !get_fn(fn_pw_kh_[0], "lama_conv1x1_kh", err) ||
+        !get_fn(fn_pw_kh_[1], "lama_conv1x1_res_kh", err) || !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
         !get_fn(fn_edge_q_[1], "lama_convt_q", err) ||
         !get_fn(fn_convt_rows_[0], "lama_convt_rows", err) ||
         !get_fn(fn_convt_rows_[1], "lama_convt_rows_q", err))
@@ -576,6 +581,8 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
                                 : pack(A, 128, 512, 9, 8, local);
             F.l2g = wino_ == 4 ? pack_wino4(A, 384, 128, l2gw) : wino_ ? pack_wino(A, 384, 128, l2gw)
                                                                      : pack(A, 384, 128, 9, 8, l2gw);
+            // rows of C channels in order: each launch sets the chunk count of
+            // its kernel (pw_kc)
             F.conv2 = pack(A, 384, 192, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
             F.conv1 = pack(A, 192, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c1[(size_t)co * 384 + ci]; });
             F.fu = pack(A, 384, 384, 1, LAMA_PW_KC, [&](int co, int ci, int) { return fu[(size_t)co * 384 + ci]; });
@@ -699,6 +706,7 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
         if (N % 4 != 0 || (uintptr_t)s.src % 16 != 0) vw = std::min(vw, 2);
         if (N % 2 != 0 || N < 4 || (uintptr_t)s.src % 8 != 0) vw = 1;
     }
+    if (vw == 4 && tile_variant(family, probs[0].OH, probs[0].OW, probs[0].M) == 0) return fn_pw_kh_[family == F_CONV1R];
     return vw == 4 ? fn_[family] : vw == 2 ? fn_pw_v2_[family == F_CONV1R] : fn_pw_any_[family == F_CONV1R];
 }
 
@@ -730,9 +738,19 @@ int Engine::w4_variant(int OH, int OW) const
 // plane with fewer tiles than 2 x 32 (0), which is where the width leaves
 // much of a 32-pixel row empty (75: 3 x 32 columns for 75, 5 x 16 for 80).
 // LAMA_EDGE_TILE=32 or 16 (read at open) forces one.
-int Engine::tile_variant(int family, int OH, int OW) const
+int Engine::tile_variant(int family, int OH, int OW, int M) const
 {
     if (family == F_CONV3 || family == F_CONV3G) return w4_variant(OH, OW);
+    // pointwise over N = OH * OW pixels into M channels: 0 = the K-half
+    // kernels, for float4-aligned planes whose 64 x 64 tiles would give at
+    // most two workgroups per CU (512x512: 277.8-278.1 vs 274.8 passes/s with
+    // conv1 and the FU conv in them, 256x256 429-436 vs 426; at 1024x1024 and
+    // 2048x2048, with three or more workgroups per CU, 64 x 64 tiles were
+    // 1-2% faster); 1 = 64 x 64 tiles
+    if (family == F_CONV1 || family == F_CONV1R) {
+        const long n = (long)OH * OW, tiles = (n + 63) / 64 * ((M + 63) / 64);
+        return LAMA_PW_KH && n % 4 == 0 && tiles <= 2 * LAMA_CUS ? 0 : 1;
+    }
     if (family != F_CONV3S2 && family != F_CONVT) return 0;
     if (edge_force_ == 32) return 0;
     if (edge_force_ == 16) return 1;
@@ -816,8 +834,12 @@ void Engine::pw_ksplit_for(int h, int w, const FftGeom &fg, int &k1, int &ku) co
         while (s < LAMA_PW_KSPLIT_MAX && nb * 2 * s <= LAMA_PW_KSPLIT_WG) s *= 2;
         return s;
     };
-    k1 = pick((p8 + 63) / 64 * 3);
-    ku = pick((ps + 63) / 64 * 6);
+    auto blocks = [&](long n, int m) {  // workgroups of the launch's tile variant
+        const long tc = tile_variant(F_CONV1, 1, (int)n, m) == 0 ? 32 : 64;
+        return (n + tc - 1) / tc * ((m + 63) / 64);
+    };
+    k1 = pick(blocks(p8, 192));
+    ku = pick(blocks(ps, 384));
 }
 
 bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
@@ -1093,6 +1115,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         s.wrow = pk.wrow;
         return s;
     };
+    bool bad_problem = false;
     auto problem = [&](int family, const ConvSeg &s0, int M, int OH, int OW, size_t bn, int bn_n, float *o,
                        size_t ocs, int outW, const float *res) {
         ConvProblem q{};
@@ -1101,11 +1124,17 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc, wino_, tile_variant(family, OH, OW));
+        tile_shape(family, tr, tc, wino_, tile_variant(family, OH, OW, M));
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
         q.mblocks = (M + 63) / 64;
         q.nblocks = q.tiles_x * q.tiles_y * q.mblocks;
+        if (family == F_CONV1 || family == F_CONV1R) {
+            // the chunk count of the kernel's chunk size over the packed row
+            const int kc = pw_kc(tile_variant(family, OH, OW, M));
+            q.s0.nchunk = (q.s0.C + kc - 1) / kc;
+            if (q.s0.nchunk * kc > q.s0.wrow) bad_problem = true;
+        }
         q.scale = wp(bn);
         q.shift = wp(bn + bn_n);
         q.relu = 1;
@@ -1116,7 +1145,6 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.oy_mul = q.ox_mul = 1;
         return q;
     };
-    bool bad_problem = false;
     auto conv_launch = [&](int family, std::vector<ConvProblem> probs, int step, double flops, double bytes,
                            int stream = S_MAIN, int wait_ev = -1, int record_ev = -1) {
         Launch L{};
@@ -1130,6 +1158,9 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         for (auto &q : probs) {
             nb += (unsigned)q.nblocks;
             const bool pw = family == F_CONV1 || family == F_CONV1R;
+            // the float4 kernel's tile width is the one the problem was tiled for
+            if (pw && (tile_variant(family, q.OH, q.OW, q.M) == 0) != (L.fn == fn_pw_kh_[family == F_CONV1R]))
+                bad_problem = true;
             const int tx = pw && q.ksplit <= 1 && q.nblocks == pw_xcd_blocks(q) ? (q.tiles_x + 7) / 8 * 8 : q.tiles_x;
             if (q.nblocks != std::max(1, q.ksplit) * tx * q.tiles_y * q.mblocks ||
                 (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2] &&
@@ -1269,10 +1300,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             kslices(raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8, W8,
                                 nullptr)),
                     ks, (long)384 * P8)};
-        // 16-byte input loads in A only: the same loads in B as well made B
-        // faster but slowed the spectral chain beside it more (512x512:
-        // 272.3-272.4 passes/s with A only, 270.8-270.9 with both, 271.3-271.6
-        // with neither)
+        // 16-byte input loads where the plane width allows (B: LAMA_W4_VEC_B)
         for (ConvProblem &q : probs) q.vec_in = wino_ == 4 && W8 % 4 == 0;
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
@@ -1298,6 +1326,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         // own stream: waits for x_g(k) (conv2(k-1), or model.4 for k = 0) and
         // records EV_B for finalize(k); else in the main stream's order
         const int xg = k == 0 ? EV_FORK : ((k - 1) % 2 ? EV_S1 : EV_S0);
+        if (LAMA_W4_VEC_B)
+            for (ConvProblem &q : probs) q.vec_in = wino_ == 4 && W8 % 4 == 0;
         conv_launch(F_CONV3G, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
                     f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9),
                     b_stream ? S_G2L : S_MAIN, b_stream || k > 0 ? xg : -1, b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1);
@@ -1366,10 +1396,6 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
         ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
                                  ffc_dst(k) + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
-        // K-half tiles walk chunks of 2 * LAMA_PW_KC channels (a 1x1 row is its
-        // channels in order, so only the chunk count differs)
-        static_assert(!LAMA_PW_RES_KH || 192 % (2 * LAMA_PW_KC) == 0, "whole conv2 chunks");
-        if (LAMA_PW_RES_KH) q2.s0.nchunk = 192 / (2 * LAMA_PW_KC);
         q2.addend = gc_buf(k);
         q2.naddend = ks;  // the l2g K slices
         q2.addend_kstride = (long)384 * P8;
@@ -2040,7 +2066,11 @@ SpecPlan *Engine::spec_plan_for(int h, int w, std::string &err)
         q.M = M;
         q.OH = 1;
         q.OW = N;
-        q.tiles_x = (N + 63) / 64;
+        int tr, tc;
+        const int v = tile_variant(F_CONV1, 1, N, M);
+        tile_shape(F_CONV1, tr, tc, 0, v);
+        q.s0.nchunk = (C + pw_kc(v) - 1) / pw_kc(v);
+        q.tiles_x = (N + tc - 1) / tc;
         q.tiles_y = 1;
         q.mblocks = (M + 63) / 64;
         q.nblocks = q.tiles_x * q.mblocks;
@@ -2347,7 +2377,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
     const int wino = family == F_CONV3 ? wino_ : 0;
-    const int KC = family == F_CONV1 ? LAMA_PW_KC : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : family == F_CONV3S2 ? LAMA_S2_KC : 8;
+    const int KC = family == F_CONV1 ? pw_kc(tile_variant(F_CONV1, 1, h * w, cout)) : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : family == F_CONV3S2 ? LAMA_S2_KC : 8;
     if ((size_t)4 * KC * h * w >= ((size_t)1 << 32)) {  // 32-bit staging offsets within a K chunk
         err = "op_conv2d: plane too large";
         return false;
@@ -2381,7 +2411,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.OH = family == F_CONV1 ? 1 : oh;
     q.OW = family == F_CONV1 ? oh * ow : ow;
     int tr, tc;
-    tile_shape(family, tr, tc, wino, tile_variant(family, q.OH, q.OW));
+    tile_shape(family, tr, tc, wino, tile_variant(family, q.OH, q.OW, q.M));
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
     q.mblocks = (cout + 63) / 64;

@@ -228,7 +228,7 @@ private:
     int wino_ = 4;
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
-    int tile_variant(int family, int OH, int OW) const;
+    int tile_variant(int family, int OH, int OW, int M = 0) const;
     unsigned w4_lds_pad(int h8, int w8, int ks) const;
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
     int w4_ldspad_force_ = -1;  // LAMA_W4_LDSPAD: 0 or 1 forces the F(4,3) LDS padding off or on
@@ -279,6 +279,7 @@ private:
     hipFunction_t fn_finalize_g2_[3] = {};  // the same three with two element groups per thread
     hipFunction_t fn_edge_q_[2] = {};       // lama_conv3x3s2_q, lama_convt_q (4 x 16 tiles)
     hipFunction_t fn_head_r_ = nullptr;     // lama_conv7x7r (the 4 -> 64 head, weights in registers)
+    hipFunction_t fn_pw_kh_[2] = {};        // lama_conv1x1_kh, lama_conv1x1_res_kh (64 x 32 K-half tiles)
     bool head_r_ = true;                    // LAMA_HEAD_R=0: the head through lama_conv7x7 (weights in LDS)
     hipFunction_t fn_convt_rows_[2] = {};   // lama_convt_rows (2 x 32 positions), lama_convt_rows_q (4 x 16)
 

@@ -41,6 +41,7 @@ def run_plans():
             "conv3x3": eng.kernel_name(h, w, "conv3x3"), "conv3x3g2l": eng.kernel_name(h, w, "conv3x3g2l"),
             "rfft2": eng.kernel_name(h, w, "rfft2"), "irfft2": eng.kernel_name(h, w, "irfft2"),
             "conv1x1": eng.kernel_name(h, w, "conv1x1"), "finalize": eng.kernel_name(h, w, "finalize"),
+            "conv1x1res": eng.kernel_name(h, w, "conv1x1res"),
         }
     out["plans"] = res
     # the u8 flow and the isolated SpectralTransform plan at two shapes
