@@ -712,11 +712,13 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
 
 // F(4,3) blocks of 32 Winograd tiles: 2 rows x 64 pixels (lama_conv3x3w4),
 // 4 x 32 (w4n) or 8 x 16 (w4q).  The shape that covers the plane with the
-// fewest blocks, 4 x 32 on a tie; LAMA_W4_TILE=64, 32 or 16 (read at open)
-// forces one.  Measured (passes/s, 32 / 16 / 64-pixel blocks): 512x512
-// 253.6 / 248.6 / 228.7 (32 blocks each for 32 and 16), 600x600 142.7 /
-// 151.1 / 124.9 (75-wide planes: 57 / 50 / 76 blocks), 1024x1024 71.4 /
-// 69.0 / 68.4, 256x256 381.1 / 376.5 / 383.0.
+// fewest blocks, 2 x 64 on a tie; LAMA_W4_TILE=64, 32 or 16 (read at open)
+// forces one.  Measured with the current kernels (passes/s, 64 / 32-pixel
+// blocks, each as many blocks): 512x512 281.2 / 277.8-278.0, 1024x1024
+// 79.7-80.1 / 77.6-77.7, 2048x2048 20.63-20.71 / 20.43-20.54; 600x600 (76 /
+// 57 / 50 blocks of 64 / 32 / 16 pixels) 148.8 / - / 166.4.  (With the
+// LDS-staged weights and 64 x 64 pointwise tiles 2 x 64 had been the
+// slowest: 512x512 228.7 vs 253.6.)
 int Engine::w4_variant(int OH, int OW) const
 {
     if (w4_force_ == 64) return 0;
@@ -726,9 +728,10 @@ int Engine::w4_variant(int OH, int OW) const
         const int tr = 2 << v, tc = 128 / tr;
         return (long)((OW + tc - 1) / tc) * ((OH + tr - 1) / tr);
     };
+    // fewest blocks; on a tie 2 x 64 before 4 x 32 before 8 x 16
     int best = 1;
-    for (int v : {2, 0})
-        if (blocks(v) < blocks(best)) best = v;
+    if (blocks(2) < blocks(best)) best = 2;
+    if (blocks(0) <= blocks(best)) best = 0;
     return best;
 }
 
@@ -798,7 +801,9 @@ int Engine::ksplit_for(int h, int w) const
 }
 
 // Groups of 4 elements per finalize thread (1 or 2): two where one group per
-// thread would give between 2.5 and 4 blocks per CU.  Measured: at 75 x 75
+// thread would give fewer blocks than CUs or between 2.5 and 4 per CU.
+// Measured: at 32 x 32 (128 blocks with one group) two groups gave 448.8-450.4
+// vs 431.3-437.1 passes/s; at 75 x 75
 // 768 blocks ran slower beside the concurrent kernels than 384 (157.4 vs
 // 158.9 passes/s); at 64 x 64 512 blocks ran faster than 256 (260.2 vs
 // 258.5); at 128 x 128 and 256 x 256 planes (8 and 32 blocks per CU) one
@@ -807,7 +812,7 @@ int Engine::fin_groups(size_t plane) const
 {
     if (fin_groups_force_ == 1 || fin_groups_force_ == 2) return fin_groups_force_;
     const size_t blocks = 128 * ((plane + 4 * LAMA_NT - 1) / (4 * LAMA_NT));
-    return 2 * blocks > 5 * (size_t)LAMA_CUS && blocks <= 4 * (size_t)LAMA_CUS ? 2 : 1;
+    return blocks < (size_t)LAMA_CUS || (2 * blocks > 5 * (size_t)LAMA_CUS && blocks <= 4 * (size_t)LAMA_CUS) ? 2 : 1;
 }
 
 // The K split of the SpectralTransform's two pointwise convolutions that

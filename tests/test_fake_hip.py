@@ -53,7 +53,8 @@ def test_every_shape_plans_and_issues_its_launches(fake_lib, weights_file):
         assert v["issued"] == v["launch_count"], shape
         assert v["conv3x3"] == v["conv3x3g2l"], shape
     # the F(4,3) block shape that covers each bottleneck plane with the fewest blocks
-    assert p["512x512"]["conv3x3"] == "lama_conv3x3w4n"
+    assert p["512x512"]["conv3x3"] == "lama_conv3x3w4"
+    assert p["256x256"]["conv3x3"] == "lama_conv3x3w4n"
     assert p["600x600"]["conv3x3"] == "lama_conv3x3w4q"
     assert p["600x592"]["conv3x3"] == "lama_conv3x3w4q"
     assert p["16x1024"]["conv3x3"] == "lama_conv3x3w4"
@@ -65,7 +66,7 @@ def test_every_shape_plans_and_issues_its_launches(fake_lib, weights_file):
     assert p["1024x1024"]["rfft2"] == "lama_rfft2_rows_128"
     # finalize sums 5 partials unsplit, 20 with the 256x256 K split (s = 4)
     assert p["512x512"]["finalize"] == "lama_finalize"
-    assert p["256x256"]["finalize"] == "lama_finalize20"
+    assert p["256x256"]["finalize"] == "lama_finalize20_g2"  # 128 blocks with one group: two
     # two element groups per thread where one would give 2.5-4 blocks per CU
     assert p["600x600"]["finalize"] == "lama_finalize_g2"
     assert p["1024x1024"]["finalize"] == "lama_finalize"

@@ -396,14 +396,14 @@ def test_forward_ksplit_variants_256(pkg, engine, oracle_cal, monkeypatch, ks):
             assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
 
 
-@pytest.mark.parametrize("h,w,kernel,fft", [(512, 512, "lama_conv3x3w4n", "lama_rfft2_64"),
+@pytest.mark.parametrize("h,w,kernel,fft", [(512, 512, "lama_conv3x3w4", "lama_rfft2_64"),
                                             (600, 600, "lama_conv3x3w4q", "lama_rfft2_75"),
                                             (600, 592, "lama_conv3x3w4q", "lama_rfft2"),
                                             (256, 256, "lama_conv3x3w4n", "lama_rfft2_32"),
                                             (16, 1024, "lama_conv3x3w4", "lama_rfft2")])
 def test_ffc_block_shape_per_plane(pkg, engine, h, w, kernel, fft):
     """The FFC GEMMs take the F(4,3) block shape that covers the bottleneck
-    plane with the fewest blocks of 32 tiles (4 x 32 px on a tie): 75-rows
+    plane with the fewest blocks of 32 tiles (2 x 64 px on a tie): 75-rows
     planes 10 x 5 blocks of 8 x 16 instead of 19 x 3 of 4 x 32; a plane of 2
     rows and 128 columns 2 blocks of 2 x 64 instead of 4 of 4 x 32.  Square
     32, 64 and 75 planes take the FFT kernels with the shape compiled in."""

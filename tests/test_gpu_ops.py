@@ -203,7 +203,7 @@ WINO_CASES = [
 @pytest.mark.parametrize("cin,cout,h,w", WINO_CASES)
 def test_conv3x3_winograd(engine, cin, cout, h, w):
     """The FFC 3x3 convolution as the default engine runs it (Winograd F(4,3)
-    along x in 32-pixel blocks, lama_conv3x3w4n) against the oracle's direct
+    along x in the block shape the plane selects) against the oracle's direct
     sum.  The transforms round differently from the direct sum, within the same
     1e-5 relative bound."""
     rng = np.random.default_rng(cin * 100 + cout + w)
