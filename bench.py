@@ -196,8 +196,8 @@ def main():
 
     conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv3x3g2l", "conv1x1", "convt", "conv1x1res"]
     conv_flops = sum(fam[f]["flops"] for f in conv_fams) / 3
-    # executed MFMA work: the Winograd FFC families issue 2/3 of their
-    # algorithmic (direct-convolution) FLOPs
+    # executed MFMA work: the Winograd FFC families issue a fraction `issued`
+    # of their algorithmic (direct-convolution) FLOPs (F(4,3): 1/2, F(2,3): 2/3)
     wino_fams = ("conv3x3", "conv3x3g2l")
     conv_flops_exec = conv_flops - sum(fam[f]["flops"] for f in wino_fams) / 3 * (1.0 - issued)
     fft_ms = sum(fam[f]["ms"] for f in ("rfft2", "irfft2")) / 3
