@@ -390,8 +390,11 @@ __device__ __forceinline__ int w4_xcd_order(int i, int n)
 }
 }  // namespace
 
+// (the cap: 128 measured 283.6-284.5 passes/s at 512x512 against 281.1-281.9
+// at 120, the same 138 registers with a different schedule; 132 to 144 gave
+// two waves per SIMD and 192-265 passes/s)
 #ifndef LAMA_W4_NUM_VGPR
-#define LAMA_W4_NUM_VGPR 120
+#define LAMA_W4_NUM_VGPR 128
 #endif
 #if LAMA_W4_NUM_VGPR > 0
 #define LAMA_W4_REGS __attribute__((amdgpu_num_vgpr(LAMA_W4_NUM_VGPR)))
