@@ -100,6 +100,12 @@ ProbStarts prob_starts(const ConvProblem *q, size_t n)
 // Pixel tile (rows x columns) of a conv family; `w4v` is the tile variant
 // (Engine::tile_variant): the F(4,3) block shape, or for the stride-2 and
 // transposed convolutions 0 = 2 x 32, 1 = 4 x 16.
+// Resident workgroups per CU the register-weight head kernel's grid is capped at
+// (512x512: 72.8-73.6 us per pass at 3 against 78.5-80.7 at 2 or 4)
+#ifndef LAMA_HEAD_WGS
+#define LAMA_HEAD_WGS 3
+#endif
+
 // Channels per K chunk of the pointwise kernel a plane of tile variant v runs
 // (Engine::tile_variant: 0 = the K-half kernels, 1 = the 64 x 64 ones).
 int pw_kc(int v) { return v == 0 ? 2 * LAMA_PW_KC : LAMA_PW_KC; }
@@ -1174,7 +1180,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         }
         // the head kernels walk their tiles: three (register weights) or two
         // (weights in LDS) resident workgroups per CU
-        L.grid = family == F_CONV7 ? std::min(nb, (L.fn == fn_head_r_ ? 3u : 2u) * LAMA_CUS) : nb;
+        L.grid = family == F_CONV7 ? std::min(nb, (L.fn == fn_head_r_ ? (unsigned)LAMA_HEAD_WGS : 2u) * LAMA_CUS) : nb;
         L.shmem = (family == F_CONV3 || family == F_CONV3G) && wino_ == 4 ? w4_shmem : 0;
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
         L.ps = prob_starts(probs.data(), probs.size());
