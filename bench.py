@@ -7,10 +7,12 @@ blurred-noise image with a ~25% brush-stroke mask.  A "step" is one forward
 pass; the input tensor is resident in HBM before the timed region starts.
 
 Prints one JSON line: passes/s, the roofline of the dominant kernel (the FFC
-3x3 implicit-GEMM family, algorithmic FLOPs per launch / mean launch time from
-HIP events on its stream, against the 157.3 TFLOP/s FP32 MFMA peak), and the
-CPU baseline (the C restatement of the reference CPU engine, timed on this
-host's cores on one bounded pass).
+3x3 convolutions as Winograd F(4,3) along x: the FLOPs of that algorithm's
+MFMA products per launch / mean launch time on the device clock, against the
+157.3 TFLOP/s FP32 MFMA peak; the direct-convolution equivalent rate beside
+it), the host enqueue time of one pass, and the CPU baseline (the C
+restatement of the reference CPU engine, timed on this host's cores: median
+of three passes at 512x512 and at 256x256).
 """
 import argparse
 import json
@@ -91,9 +93,11 @@ def main():
     # (family conv3x3g2l), one kernel
     dom_fams = ["conv3x3", "conv3x3g2l"]
     # the FFC 3x3 convolutions run as Winograd F(4,3) along x (LAMA_FFC_WINO=2:
-    # F(2,3); 0: the direct implicit GEMM); FLOPs are the convolution's
-    # algorithmic count in every case, of which F(4,3) issues 1/2 and F(2,3)
-    # 2/3 as MFMA work
+    # F(2,3); 0: the direct implicit GEMM).  The engine counts each launch's
+    # direct-convolution FLOPs, 2 Cin Cout 9 H W; the algorithm's own MFMA
+    # products are the fraction `issued` of that: F(4,3) multiplies 6
+    # transformed positions x 3 kernel rows per 4 output pixels (18 of the
+    # direct 36 products, 1/2), F(2,3) 4 x 3 per 2 (12 of 18, 2/3)
     wv = os.environ.get("LAMA_FFC_WINO", "4")
     wino = 0 if wv == "0" else 2 if wv == "2" else 4
     # the plan's own kernel for the FFC GEMMs at this size (the F(4,3) block
@@ -123,6 +127,21 @@ def main():
     eng.synchronize()
     fam = eng.profile_read()
     eng.profile(())
+
+    # host enqueue time of one pass: the launch loop alone (forward_device
+    # returns once every launch is queued), on an idle device so that no
+    # queue back-pressure is counted; the pass's device time beside it
+    enq, walls = [], []
+    for _ in range(max(5, min(20, args.steps))):
+        eng.synchronize()
+        t = time.perf_counter()
+        eng.forward_device(d_in, S, S, d_out)
+        t1 = time.perf_counter()
+        eng.synchronize()
+        enq.append(t1 - t)
+        walls.append(time.perf_counter() - t)
+    enqueue_ms = float(np.median(enq)) * 1e3
+    isolated_ms = float(np.median(walls)) * 1e3
 
     out = np.empty((3, S, S), np.float32)
     eng.download(out, d_out)
@@ -184,7 +203,11 @@ def main():
         launch_ms = launch_ms_events_a
         flops_launch = dA["flops"] / max(1, dA["launches"])
         clock_a = clock_b = None
-    achieved = flops_launch / (launch_ms * 1e-3) / 1e12
+    # the F(4,3) algorithm's FLOPs (its MFMA products) per launch, and the
+    # direct-convolution count the same launch replaces
+    exec_launch = flops_launch * issued
+    achieved = exec_launch / (launch_ms * 1e-3) / 1e12
+    achieved_direct = flops_launch / (launch_ms * 1e-3) / 1e12
     traffic = None
     if args.traffic and os.path.exists(args.traffic):
         with open(args.traffic) as fh:
@@ -196,8 +219,8 @@ def main():
 
     conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv3x3g2l", "conv1x1", "convt", "conv1x1res"]
     conv_flops = sum(fam[f]["flops"] for f in conv_fams) / 3
-    # executed MFMA work: the Winograd FFC families issue a fraction `issued`
-    # of their algorithmic (direct-convolution) FLOPs (F(4,3): 1/2, F(2,3): 2/3)
+    # executed MFMA work: the Winograd FFC families at the fraction `issued`
+    # of their direct-convolution FLOPs (1/2 for F(4,3), 2/3 for F(2,3))
     wino_fams = ("conv3x3", "conv3x3g2l")
     conv_flops_exec = conv_flops - sum(fam[f]["flops"] for f in wino_fams) / 3 * (1.0 - issued)
     fft_ms = sum(fam[f]["ms"] for f in ("rfft2", "irfft2")) / 3
@@ -218,12 +241,23 @@ def main():
 
         cs = args.cpu_size or S
         net = O.OracleNet(O.read_safetensors(wpath))
-        cimg = H.synth_image(cs, cs, 1)
-        cmask, _ = H.synth_mask_strokes(cs, cs, 0.25, 2)
-        cx = H.build_input(cimg, cmask)
-        t = time.perf_counter()
-        net.forward(cx)
-        cpu_s = time.perf_counter() - t
+
+        def cpu_passes(n, reps=3):
+            """Seconds of `reps` whole-image passes at n x n (weights preloaded)."""
+            cimg = H.synth_image(n, n, 1)
+            cmask, _ = H.synth_mask_strokes(n, n, 0.25, 2)
+            cx = H.build_input(cimg, cmask)
+            ts = []
+            for _ in range(reps):
+                t = time.perf_counter()
+                net.forward(cx)
+                ts.append(time.perf_counter() - t)
+            return ts
+
+        # the workload size, median of three; 256x256 (configs[0]'s shape) beside it
+        cpu_ts = cpu_passes(cs)
+        cpu_s = float(np.median(cpu_ts))
+        cpu_ts256 = cpu_passes(256) if cs != 256 else cpu_ts
         scale = (cs / S) ** 2  # work scales with the pixel count
         cpu_model = "unknown"
         try:
@@ -248,9 +282,12 @@ def main():
             pass
         cpu = {"value": round(scale / cpu_s, 5), "unit": "passes/s", "cores": O.lib().or_num_threads(),
                "cpu_model": cpu_model, "lscpu": lscpu, "kind": "port",
-               "sample": f"one {cs}x{cs} whole-image pass of the C restatement of cpu.rs "
-                         f"(-O3 -ffp-contract=off, OpenMP), {cpu_s:.2f} s"
-                         + ("" if cs == S else f", scaled by pixel count to {S}x{S}")}
+               "sample": f"median of three {cs}x{cs} whole-image passes of the C restatement of cpu.rs "
+                         f"(-O3 -ffp-contract=off, OpenMP, weights preloaded): {cpu_s:.2f} s"
+                         + ("" if cs == S else f", scaled by pixel count to {S}x{S}"),
+               "pass_s": [round(v, 3) for v in cpu_ts],
+               "passes_per_s_256": round(1.0 / float(np.median(cpu_ts256)), 4),
+               "pass_s_256": [round(v, 3) for v in cpu_ts256]}
 
     line = {
         "metric": "512x512 inpaint passes/sec (FP32, batch 1)",
@@ -272,26 +309,29 @@ def main():
         "roofline": {"bound": "mfma",
                      "kernel": (dom_kernel + f" (FFC 3x3 convolutions as {method}, {geometry}"
                                 + "; timed: both launches of every FFC of the sampled passes, A = l2l + l2g "
-                                  "(4.83 GFLOP) and B = g2l (3.62 GFLOP), each from its first workgroup's start "
-                                  "to its last workgroup's end on the device clock; they overlap each other and "
-                                  "the spectral branch on three streams, so a duration includes the time the "
-                                  "launch shares the CUs; achieved counts the convolution's algorithmic FLOPs)"),
+                                  "and B = g2l, each from its first workgroup's start to its last workgroup's end "
+                                  "on the device clock; they overlap each other and the spectral branch on three "
+                                  "streams, so a duration includes the time the launch shares the CUs)"),
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
-                     "flops_per_launch": flops_launch, "launch_ms": round(launch_ms, 5),
+                     "flops_kind": (f"the {method} algorithm's MFMA products, {issued:.4g} of the direct "
+                                    "convolution's 2 Cin Cout 9 H W"),
+                     "flops_per_launch": exec_launch,
+                     "direct_flops_per_launch": flops_launch,
+                     "achieved_direct_equivalent": round(achieved_direct, 2),
+                     "launch_ms": round(launch_ms, 5),
                      "launch_ms_source": ("kernel clock (s_memrealtime stamps of every workgroup)"
                                           if clock_a is not None else "HIP events (A launches)"),
                      "launches_timed": int(n_dom),
                      "launch_ms_a": round(clock_a, 5) if clock_a is not None else None,
                      "launch_ms_b": round(clock_b, 5) if clock_b is not None else None,
-                     "launch_ms_a_events": round(launch_ms_events_a, 5),
-                     "mfma_issued_frac": round(achieved * issued / PEAK_FP32_MFMA, 4)},
-        # all conv families' algorithmic (direct-convolution) FLOPs over the
-        # pass's wall time, and the MFMA work actually executed (Winograd
-        # families at 2/3) over the same time
+                     "launch_ms_a_events": round(launch_ms_events_a, 5)},
+        # all conv families' direct-convolution FLOPs over the pass's wall
+        # time, and the MFMA work actually executed (the Winograd families at
+        # `issued`) over the same time
         "pass_conv_tflops": round(conv_flops / (ms * 1e9), 2),
         "pass_conv_frac_of_peak": round(conv_flops / (ms * 1e9) / PEAK_FP32_MFMA, 4),
-        "pass_conv_flops_kind": "algorithmic",
+        "pass_conv_flops_kind": "direct convolution (2 Cin Cout Kh Kw Hout Wout)",
         "pass_conv_executed_tflops": round(conv_flops_exec / (ms * 1e9), 2),
         "pass_conv_executed_frac_of_peak": round(conv_flops_exec / (ms * 1e9) / PEAK_FP32_MFMA, 4),
         "fft_gbps": round(fft_bytes / (fft_ms * 1e6), 1) if fft_ms > 0 else None,
@@ -299,6 +339,10 @@ def main():
         "host_io_passes_per_s": round(host_io, 3),
         "host_io_path": "lama_hip_inpaint: u8 image + mask in, u8 composite out (PCIe-inclusive)",
         "host_f32_io_passes_per_s": round(host_f32_io, 3),
+        "host_enqueue_ms_per_pass": round(enqueue_ms, 4),
+        "isolated_pass_ms": round(isolated_ms, 4),
+        "host_enqueue_note": ("host time of forward_device (the launch loop alone, device idle at the call), "
+                              "median; isolated_pass_ms: the same call through its synchronize"),
         "spectral_block_us": round(spec_us, 2),
         "spectral_block_workload": f"BASELINE configs[2]: SpectralTransform of FFCs 0..17 on 384x{h8}x{h8}, "
                                    "conv1 -> rfft2 -> FU conv -> irfft2 -> conv2, one stream",
