@@ -334,6 +334,38 @@ def test_cli_sections_config4_2048_with_1024_hole(H, engine, tmp_path, weights_d
 
 
 @pytest.mark.gpu
+def test_cli_tile_config4_2048_with_300_hole(H, engine, tmp_path, weights_dir):
+    """BASELINE configs[4] --tile as specified: a 2048 x 2048 image with a
+    seeded 300 x 300 hole runs one 600 x 600 window (tile_rect, main.rs:740-777;
+    the README's --tile timing is this window).  The output is bit-exact with
+    crop-run-paste (main.rs:378-443) restated over the engine; the window's
+    composite is within 1/255 max and 0.1 levels mean of the CPU oracle's on
+    the same window; every pixel outside the hole keeps its source bytes."""
+    import oracle_api as O
+    img = H.synth_image(2048, 2048, 1)
+    mask, _ = H.synth_mask_rect(2048, 2048, 300, 300, 2)
+    ip, mp = write_case(H, str(tmp_path), img, mask)
+    out = str(tmp_path / "o.png")
+    print("case tile 2048 / 300 hole", flush=True)
+    r = run_cli("--image", ip, "--mask", mp, "--output", out, "--weights", weights_dir["cal"], "--gpu", "--tile",
+                timeout=600)
+    assert r.returncode == 0, r.stderr
+    t = H.tile_rect(mask)
+    assert t.side == 600, t.side
+    assert f"tile: 600x600 window at ({t.x0},{t.y0})".encode() in r.stderr, r.stderr
+    got = H.png_read_rgb(out)
+    assert np.array_equal(got, _tile_by_hand(H, engine, img, mask))
+    assert np.array_equal(got[mask == 0], img[mask == 0])
+    # the window against the oracle: the same crop, build_input and composite
+    sub, sm = img[t.y0:t.y0 + 600, t.x0:t.x0 + 600], mask[t.y0:t.y0 + 600, t.x0:t.x0 + 600]
+    x = H.build_input(sub, sm, 0, 0)
+    ref = H.composite(sub, sm, O.OracleNet(O.read_safetensors(weights_dir["cal"])).forward(x), 0, 0)
+    win = got[t.y0:t.y0 + 600, t.x0:t.x0 + 600]
+    d = np.abs(win.astype(int) - ref.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
+
+
+@pytest.mark.gpu
 def test_cli_dump_step_matches_the_oracle(H, tmp_path, weights_dir):
     """LAMA_DUMP_STEP=<n> (cuda.rs:1572-1574, 1647-1662): the CLI's pass
     writes /tmp/gpu_step_<n>.f32 in the reference's layout (local planes, then

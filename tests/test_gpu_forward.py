@@ -230,6 +230,33 @@ def test_forward_2048_whole_image(pkg, engine):
     assert engine.launch_count(h, w) == 1 + 3 + 36 * 10 + 3 + 1
 
 
+@pytest.mark.timeout(900)
+def test_forward_2048_whole_image_against_the_oracle(pkg, engine, oracle_cal):
+    """configs[4] whole image at its full size against the CPU oracle
+    (main.rs:212-313 through cpu.rs:741-751): a 2048 x 2048 blurred-noise
+    image with a seeded 300 x 300 hole; every plan step within the per-layer
+    bound, the composite within 1/255 max and 0.1 levels mean, unmasked pixels
+    bit-exact.  The oracle pass takes about a minute on 16 host threads."""
+    h = w = 2048
+    H = pkg.host_api
+    img = H.synth_image(h, w, 1)
+    mask, _ = H.synth_mask_rect(h, w, 300, 300, 2)
+    x = H.build_input(img, mask)
+    print(f"case oracle {h}x{w} rect 300", flush=True)
+    got, got_steps = engine.forward_steps(x, list(range(29)))
+    ref, ref_steps = oracle_cal.forward(x, steps=True)
+    for s in range(29):
+        e = rel_err(got_steps[s], ref_steps[s])
+        assert e < STEP_TOL, f"step {s}: rel err {e:.3e}"
+        got_steps[s] = ref_steps[s] = None
+    assert rel_err(got, ref) < STEP_TOL
+    u8g = H.composite(img, mask, got, 0, 0)
+    u8r = H.composite(img, mask, ref, 0, 0)
+    d = np.abs(u8g.astype(int) - u8r.astype(int))
+    assert d.max() <= 1 and d.mean() <= 0.1, (d.max(), d.mean())
+    assert np.array_equal(u8g[mask == 0], img[mask == 0])
+
+
 def test_graph_replays_match_eager(pkg, engine, monkeypatch):
     """The forward captured as one HIP graph and replayed: every replay, with
     eager work and synchronisations in between, equals the per-launch path
