@@ -65,15 +65,19 @@ int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int 
                             float *d_output, void *stream, char *err, size_t errlen);
 
 /* lama_hip_forward_device that allocates nothing.  It has no counterpart in
- * the reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * the reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid it).  A stream under graph capture is
+ * refused with an error: a captured pass would replay against whatever
+ * descriptors the shared array holds at replay time.
  * The pass's activations, partial sums, FFT scratch and launch descriptors
  * live in a device array of LAMA_SCRATCH_BYTES = 192 MiB (`lama_scratch`, a
  * code object of its own that lama_hip_open loads once per device per
- * process; the device holds it until the process ends).  Shapes whose arena
+ * process, so every process that opens a context holds it on that device
+ * until it ends; if that load fails, the open still succeeds and only this
+ * entry point returns the error).  Shapes whose arena
  * exceeds it are rejected with an error: up to 512 x 512 fits (177 MiB).
  * The call makes no hipMalloc, hipFree, event or graph creation (and no
- * per-family profiling); the caller passes device input and output as for
+ * per-family profiling or launch timeline); the caller passes device input and output as for
  * lama_hip_forward_device.  Every context on a GPU shares that GPU's array,
  * which keeps the last call's contents; no kernel of the pass reads what the
  * pass has not written, and the launch descriptors are re-uploaded on

@@ -179,7 +179,9 @@ __device__ __forceinline__ int reflect1(int i, int n)
 #endif
 
 // One K segment of an implicit-GEMM convolution.  `src` is planar
-// [C][IH][IW]; `wt` points at row 0 of the packed weights
+// [C][IH][IW] with channel planes `cs` floats apart (cs >= IH * IW; the
+// bottleneck planes are padded to a multiple of 4 floats so that every plane
+// is 16-byte aligned); `wt` points at row 0 of the packed weights
 // [M][nchunk][taps][KC] (KC input channels per chunk, zero-padded).
 struct ConvSeg {
     const float *src;
@@ -187,7 +189,7 @@ struct ConvSeg {
     int C, IH, IW;
     int nchunk;
     int wrow;  // floats per packed weight row = nchunk * taps * KC
-    int pad_;
+    int cs;    // floats between input channel planes
 };
 
 // The first workgroup of problems 1..3 of a grouped conv launch (INT32_MAX
@@ -268,6 +270,9 @@ struct FftArgs {
     int pad_;
     long in_pstride, feat_pstride;
     const float *in_scale, *in_shift, *feat_scale, *feat_shift;
+    // floats between the planes of the real side (rfft input, irfft output
+    // and feat; >= H * W) and of the stacked spectrum (>= H * Wh)
+    long rs, ss;
 };
 
 // Most K slices of the pointwise convolutions that feed a transform.

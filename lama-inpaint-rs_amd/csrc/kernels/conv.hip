@@ -131,7 +131,7 @@ __device__ __forceinline__ void make_pslots(Slots<C> &sl, const ConvSeg &sg, int
             g = zero ? 0 : iy * sg.IW + ix;
         }
         sl.pl[it] = in ? (r * C::PCP + C::col(c)) * C::KCP + cl : C::PR * C::PCP * C::KCP + l;
-        sl.po[it] = 4u * (unsigned)(min(cl, C::KC - 1) * sg.IH * sg.IW + g);
+        sl.po[it] = 4u * (unsigned)(min(cl, C::KC - 1) * sg.cs + g);
         sl.pc[it] = (in && !zero) ? cl : -1;
     }
 }
@@ -168,13 +168,13 @@ __device__ __forceinline__ void load_w(Stage<C> &st, const Slots<C> &sl, const C
 template <class C>
 __device__ __forceinline__ void load_p(Stage<C> &st, const Slots<C> &sl, const ConvSeg &sg, int ck)
 {
-    // 32-bit byte offsets from the chunk's first plane (below 4 * KC * plane,
+    // 32-bit byte offsets from the chunk's first plane (below 4 * KC * cs,
     // which the host bounds); slots of channels past C (zero weights) read the
     // last float of the source instead
-    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const unsigned plane = (unsigned)(sg.IH * sg.IW), cs = (unsigned)sg.cs;
     const int c0 = ck * C::KC;
-    const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
-    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
+    const unsigned last = 4u * ((unsigned)(min(sg.C - c0, C::KC) - 1) * cs + plane - 1u);
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * cs;
 #pragma unroll
     for (int it = 0; it < C::PITER; ++it) {
         const float v = *at_byte<float>(src, min(sl.po[it], last));
@@ -373,9 +373,11 @@ __device__ __forceinline__ void run_segment(Acc &acc, const ConvSeg &sg_mem, int
 // 16-byte LDS store, no transpose), and each MFMA's B operand is one 4-byte
 // LDS read per lane: lane half g reads 32 consecutive pixels of channel
 // g*KC/2 + c.  The two halves' rows sit in separate regions whose bases
-// differ by 32 banks.  VW = 4: planes are 16-byte aligned with N % 4 == 0
-// (one float4 load per run); VW = 2: 8-byte aligned with N % 2 == 0 and
-// N >= 4 (two float2 loads); VW = 1: four clamped scalar loads.
+// differ by 32 banks.  Channel planes lie cs floats apart.  VW = 4: planes
+// 16-byte aligned with cs % 4 == 0 (one float4 load per run; the last run of
+// a plane may cover up to 3 floats of padding past N, which only feed the
+// unstored columns past N); VW = 2: 8-byte aligned with N % 2 == 0, cs even
+// and N >= 4 (two float2 loads); VW = 1: four clamped scalar loads.
 // KH (K halves, NPX = 32): wave (wm, kh) takes channels wm*32.. +32, all 32
 // pixels, and half of every chunk's K slots (kh = wave & 1); the two halves'
 // sums meet in LDS after the K loop.  Half the dependent MFMA chain per wave
@@ -414,7 +416,7 @@ struct PwStage {
 template <class C>
 __device__ __forceinline__ void pw_make_slots(PwSlots<C> &sl, const ConvSeg &sg, int m0, int M, int ox0)
 {
-    const int tid = threadIdx.x, N = sg.IH * sg.IW;
+    const int tid = threadIdx.x, N = sg.IH * sg.IW, N4 = (N + 3) & ~3;
 #pragma unroll
     for (int it = 0; it < C::WITER; ++it) {
         const int idx = tid + it * LAMA_NT, row = idx / (C::KC / 4), c4 = idx % (C::KC / 4);
@@ -426,10 +428,11 @@ __device__ __forceinline__ void pw_make_slots(PwSlots<C> &sl, const ConvSeg &sg,
         const int idx = tid + it * LAMA_NT, ci = idx / (C::NPX / 4), q = idx % (C::NPX / 4);
         sl.xc[it] = ci;
         sl.xl[it] = (ci / (C::KC / 2)) * C::HALF + (ci % (C::KC / 2)) * C::NPX + 4 * q;
-        // runs past the plane read the last whole run (VW = 4; N % 4 == 0, so
-        // no run straddles the end) or clamp per float2 pair / element
-        sl.xp[it] = C::VW == 4 ? min(ox0 + 4 * q, N - 4) : ox0 + 4 * q;
-        sl.xo[it] = 4u * (unsigned)(ci * N + sl.xp[it]);
+        // VW = 4 (cs % 4 == 0): runs past the plane read the last whole run
+        // of the padded plane (its pixels past N feed only the tile columns
+        // past N, which are not stored); else clamp per float2 pair / element
+        sl.xp[it] = C::VW == 4 ? min(ox0 + 4 * q, N4 - 4) : ox0 + 4 * q;
+        sl.xo[it] = 4u * (unsigned)(ci * sg.cs + sl.xp[it]);
     }
 }
 
@@ -445,11 +448,13 @@ __device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &
         st.w[4 * it + 2] = v.z;
         st.w[4 * it + 3] = v.w;
     }
-    const int N = sg.IH * sg.IW;
+    const int N = sg.IH * sg.IW, cs = sg.cs;
     const int c0 = ck * C::KC, clast = sg.C - 1 - c0;  // channels past C read a valid plane (zero weights)
-    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * N;
-    // VEC: runs of channels past C (zero weights) read the source's last run
-    const unsigned vlast = 4u * ((unsigned)min(sg.C - c0, C::KC) * (unsigned)N - 4u);
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * cs;
+    // VEC: runs of channels past C (zero weights) read the last valid
+    // channel's last run (VW = 4: of the plane padded to a multiple of 4)
+    const unsigned vlast =
+        4u * ((unsigned)(min(sg.C - c0, C::KC) - 1) * (unsigned)cs + (unsigned)(C::VW == 4 ? (N + 3) & ~3 : N) - 4u);
 #pragma unroll
     for (int it = 0; it < C::XITER; ++it) {
         if constexpr (C::VW == 4) {
@@ -469,7 +474,7 @@ __device__ __forceinline__ void pw_load_chunk(PwStage<C> &st, const PwSlots<C> &
             st.x[4 * it + 2] = b.x;
             st.x[4 * it + 3] = b.y;
         } else {
-            const LAMA_GLOBAL float *q = src + (long)min(sl.xc[it], clast) * N;
+            const LAMA_GLOBAL float *q = src + (long)min(sl.xc[it], clast) * cs;
 #pragma unroll
             for (int e = 0; e < 4; ++e) st.x[4 * it + e] = q[min(sl.xp[it] + e, N - 1)];
         }
@@ -740,7 +745,7 @@ __device__ __forceinline__ void pw_tile(const ConvProblem &P, int b, float *lds,
     ConvSeg sg = P.s0;
     if (P.ksplit > 1) {
         const int c0 = ks * P.kchunks * C::KC;
-        sg.src += (long)c0 * sg.IH * sg.IW;
+        sg.src += (long)c0 * sg.cs;
         sg.wt += c0;  // 1x1 rows: chunk k at k * KC floats
         sg.C -= c0;
         sg.nchunk = P.kchunks;
@@ -1089,9 +1094,9 @@ extern "C" __global__ void __launch_bounds__(LAMA_NT) lama_conv3x3(LAMA_CONV_PAR
 
 // 1x1 convolutions over flat planes (SpectralTransform conv1, FourierUnit
 // conv): lama_conv1x1_kh in 64 x 32 K-half tiles, the others in 64 x 64
-// tiles.  lama_conv1x1 and _kh need 16-byte aligned planes with
-// N % 4 == 0, lama_conv1x1_v2 8-byte aligned planes with N % 2 == 0 and
-// N >= 4; lama_conv1x1_s takes any N.
+// tiles.  lama_conv1x1 and _kh need 16-byte aligned planes with a plane
+// stride cs % 4 == 0 (N padded up to it), lama_conv1x1_v2 8-byte aligned
+// planes with N % 2 == 0, cs even and N >= 4; lama_conv1x1_s takes any N.
 #define LAMA_PW_KERNEL(NAME, KC, VW, NPX, PREFETCH, D, KH)                                                  \
     extern "C" __global__ void __launch_bounds__(LAMA_NT) NAME(LAMA_CONV_PARAMS) \
     {                                                                                                       \

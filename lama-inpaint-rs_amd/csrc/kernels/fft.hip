@@ -319,7 +319,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
     // of at most LAMA_FFT_NT * 8 row-pair elements (two quads per thread).
     TwFetch tw;
     tw.issue(A, threadIdx.x);
-    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
+    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * A.rs;
     const KsIn kin = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, c);
     const int NT = LAMA_FFT_NT;
     if ((W & 3) == 0 && (H & 1) == 0) {  // row pairs as float4 quads
@@ -375,7 +375,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2(const FftAr
     }
     __syncthreads();
     float2 *q = stockham(A.col, twc, o, r, Wh, 1, Wh, A.col.sign_fwd);
-    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh, *dim = dre + (long)H * Wh;
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * A.ss, *dim = dre + A.ss;
     for (int idx = threadIdx.x; idx < H * Wh; idx += blockDim.x) {
         const float2 v = q[idx];
         dre[idx] = v.x * A.scale;
@@ -401,8 +401,8 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     const int NT = LAMA_FFT_NT;
     TwFetch tw;
     tw.issue(A, threadIdx.x);
-    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + (long)H * Wh;
-    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * A.ss, *sim = sre + A.ss;
+    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * A.rs;
     const KsIn kre = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c);
     const KsIn kim = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c + 1);
     const KsIn kf = ks_in(A.feat_np, A.feat_pstride, A.feat_scale, A.feat_shift, c);
@@ -454,7 +454,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2(const FftA
     }
     __syncthreads();
     float2 *q = stockham(A.row, twr, o, r, HP, W, 1, -A.row.sign_fwd);
-    LAMA_GLOBAL float *d = gp(A.out) + (long)c * H * W;
+    LAMA_GLOBAL float *d = gp(A.out) + (long)c * A.rs;
     if (vec) {
         auto emit = [&](int i4, float4 fv) {
             const int idx = i4 * 4, y = idx / W, x = idx - y * W;
@@ -517,7 +517,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_rows(const 
     const int p0 = (blockIdx.x - c * nchunk) * PB, np = min(PB, HP - p0);
     float2 *b0 = sm, *b1 = sm + PB * W, *twr = sm + 2 * PB * W;
     load_table(A.row.tw, W, twr);
-    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W + (long)(2 * p0) * W;
+    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * A.rs + (long)(2 * p0) * W;
     const int rows = min(2 * np, H - 2 * p0);  // real rows present in this block
     for (int idx = threadIdx.x; idx < np * W; idx += blockDim.x) {
         const int p = idx / W, x = idx - p * W;
@@ -555,7 +555,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_cols(const 
     }
     __syncthreads();
     const float2 *q = stockham(A.col, twc, b0, b1, nc, 1, nc, A.col.sign_fwd);
-    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh + x0, *dim = dre + (long)H * Wh;
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * A.ss + x0, *dim = dre + A.ss;
     for (int idx = threadIdx.x; idx < H * nc; idx += blockDim.x) {
         const int y = idx / nc, j = idx - y * nc;
         const float2 v = q[idx];
@@ -576,7 +576,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_cols(const
     const int x0 = (blockIdx.x - c * nchunk) * CB, nc = min(CB, Wh - x0);
     float2 *b0 = sm, *b1 = sm + H * CB, *twc = sm + 2 * H * CB;
     load_table(A.col.tw, H, twc);
-    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh + x0, *sim = sre + (long)H * Wh;
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * A.ss + x0, *sim = sre + A.ss;
     for (int idx = threadIdx.x; idx < H * nc; idx += blockDim.x) {
         const int y = idx / nc, j = idx - y * nc;
         b0[idx] = make_float2(sre[(long)y * Wh + j], sim[(long)y * Wh + j]);
@@ -627,7 +627,7 @@ extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_rows(const
     }
     __syncthreads();
     const float2 *q = stockham(A.row, twr, b0, b1, np, W, 1, -A.row.sign_fwd);
-    const long base = (long)c * H * W + (long)(2 * p0) * W;
+    const long base = (long)c * A.rs + (long)(2 * p0) * W;
     const LAMA_GLOBAL float *f = gp(A.feat) + base;
     LAMA_GLOBAL float *d = gp(A.out) + base;
     for (int idx = threadIdx.x; idx < rows * W; idx += blockDim.x) {
@@ -798,7 +798,7 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
     const int c = blockIdx.x;
     // prologue: every global load before the first LDS write
     float2 tv = ct_twiddle_fetch<N>(A);
-    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * H * W;
+    const LAMA_GLOBAL float *src = gp(A.in) + (long)c * A.rs;
     const KsIn kin = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, c);
     if constexpr (P::VEC) {
         constexpr int W4 = W / 4, NQ = HP * W4, RQ = (NQ + NT - 1) / NT;
@@ -873,7 +873,7 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
     }
     __syncthreads();
     float2 *q = ct_stockham<H, 1, Wh, 1, Wh, SF, IP>(o, r, twc);
-    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh, *dim = dre + H * Wh;
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * A.ss, *dim = dre + A.ss;
     for (int idx = threadIdx.x; idx < H * Wh; idx += NT) {
         const float2 v = q[idx];
         dre[idx] = v.x * A.scale;
@@ -893,8 +893,8 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
     const int c = blockIdx.x;
     // prologue: twiddles, this block's spectrum and the `f +` addend
     float2 tv = ct_twiddle_fetch<N>(A);
-    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh, *sim = sre + H * Wh;
-    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * H * W;
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * A.ss, *sim = sre + A.ss;
+    const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * A.rs;
     const KsIn kre = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c);
     const KsIn kim = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c + 1);
     const KsIn kf = ks_in(A.feat_np, A.feat_pstride, A.feat_scale, A.feat_shift, c);
@@ -970,7 +970,7 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
     float2 *q = ct_stockham<W, 1, HP, W, 1, -SF, IP>(o, r, twr);
     if constexpr (P::VEC) {
         constexpr int N4 = H * W / 4;
-        LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + (long)c * H * W);
+        LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + (long)c * A.rs);
 #pragma unroll
         for (int k = 0; k < FP; ++k) {
             const int i4 = threadIdx.x + k * NT;
@@ -985,7 +985,7 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
             d4[i4] = o4;
         }
     } else {
-        LAMA_GLOBAL float *d = gp(A.out) + (long)c * H * W;
+        LAMA_GLOBAL float *d = gp(A.out) + (long)c * A.rs;
         const float *qf = reinterpret_cast<const float *>(q);
 #pragma unroll
         for (int k = 0; k < FP; ++k) {
@@ -1054,7 +1054,7 @@ __device__ __forceinline__ void rfft2_rows_ct(const FftArgs &A, float2 *sm)
     const int c = blockIdx.x / S::RCH, p0 = (blockIdx.x % S::RCH) * PB;
     const float2 tv = gp(reinterpret_cast<const float2 *>(A.row.tw))[min((int)threadIdx.x, W - 1)];
     const LAMA_GLOBAL float4 *src =
-        reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.in) + ((long)c * N + 2 * p0) * W);
+        reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.in) + (long)c * A.rs + (long)(2 * p0) * W);
     float4 qa[RQ], qb[RQ];
 #pragma unroll
     for (int k = 0; k < RQ; ++k) {
@@ -1107,7 +1107,7 @@ __device__ __forceinline__ void rfft2_cols_ct(const FftArgs &A, float2 *sm, int 
     }
     __syncthreads();
     const float2 *q = ct_stockham<H, 1, NC, 1, NC, -1>(b0, b1, twc);
-    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh + x0, *dim = dre + H * Wh;
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * A.ss + x0, *dim = dre + A.ss;
     for (int idx = threadIdx.x; idx < H * NC; idx += NT) {
         const int y = idx / NC, j = idx % NC;
         const float2 u = q[idx];
@@ -1124,7 +1124,7 @@ __device__ __forceinline__ void irfft2_cols_ct(const FftArgs &A, float2 *sm, int
     constexpr int H = S::H, Wh = S::Wh, CB = S::CB, NT = S::NT, L = (H * NC + NT - 1) / NT;
     float2 *b0 = sm, *b1 = sm + H * CB, *twc = sm + 2 * H * CB;
     const float2 tv = gp(reinterpret_cast<const float2 *>(A.col.tw))[min((int)threadIdx.x, H - 1)];
-    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh + x0, *sim = sre + H * Wh;
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * A.ss + x0, *sim = sre + A.ss;
     float2 v[L];
 #pragma unroll
     for (int k = 0; k < L; ++k) {
@@ -1158,7 +1158,7 @@ __device__ __forceinline__ void irfft2_rows_ct(const FftArgs &A, float2 *sm)
     float2 *b0 = sm, *b1 = sm + PB * W, *twr = sm + 2 * PB * W;
     const int c = blockIdx.x / S::RCH, p0 = (blockIdx.x % S::RCH) * PB;
     const float2 tv = gp(reinterpret_cast<const float2 *>(A.row.tw))[min((int)threadIdx.x, W - 1)];
-    const long base = ((long)c * N + 2 * p0) * W;
+    const long base = (long)c * A.rs + (long)(2 * p0) * W;
     const LAMA_GLOBAL float4 *f4 = reinterpret_cast<const LAMA_GLOBAL float4 *>(gp(A.feat) + base);
     float4 fpre[NF];
 #pragma unroll
@@ -1299,7 +1299,7 @@ __device__ __forceinline__ void rfft2_cols_256_c4(const FftArgs &A, float2 *sm, 
     if (threadIdx.x < H) tw[threadIdx.x] = tv;
     __syncthreads();
     col256_four_step(v, ex, tw, -1);
-    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * H * Wh + x0 + cc, *dim = dre + H * Wh;
+    LAMA_GLOBAL float *dre = gp(A.out) + (long)(2 * c) * A.ss + x0 + cc, *dim = dre + A.ss;
 #pragma unroll
     for (int k2 = 0; k2 < 16; ++k2) {
         dre[(t + 16 * k2) * Wh] = v[k2].x * A.scale;
@@ -1314,7 +1314,7 @@ __device__ __forceinline__ void irfft2_cols_256_c4(const FftArgs &A, float2 *sm,
     float2 *ex = sm, *tw = sm + kC4Tw;
     const int cc = threadIdx.x % kC4, t = threadIdx.x / kC4;
     const float2 tv = gp(reinterpret_cast<const float2 *>(A.col.tw))[threadIdx.x % H];
-    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * H * Wh + x0 + cc, *sim = sre + H * Wh;
+    const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * A.ss + x0 + cc, *sim = sre + A.ss;
     float2 v[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = make_float2(sre[(t + 16 * j) * Wh], sim[(t + 16 * j) * Wh]);

@@ -68,7 +68,7 @@ __device__ __forceinline__ void wino_slots(WSlots &sl, const ConvSeg &sg, int m0
         sl.wl[it] = row * C::WSTR + c4 * 4;
         sl.wg[it] = min(m0 + row, M - 1) * sg.wrow + c4 * 4;
     }
-    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const unsigned cs = (unsigned)sg.cs;
 #pragma unroll
     for (int it = 0; it < C::VITER; ++it) {
         const int idx = tid + it * LAMA_NT;
@@ -77,7 +77,7 @@ __device__ __forceinline__ void wino_slots(WSlots &sl, const ConvSeg &sg, int m0
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int ix = reflect1(ox0 + 2 * t - 1 + c, sg.IW);
-            sl.po[it][c] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + ix));
+            sl.po[it][c] = 4u * ((unsigned)ci * cs + (unsigned)(iy * sg.IW + ix));
         }
         sl.vl[it] = (r * C::NU * C::NT + t) * C::KCP + ci;
     }
@@ -97,10 +97,10 @@ __device__ __forceinline__ void wino_load(WStage &st, const WSlots &sl, const Co
     }
     // channels past C (zero weights) read the last float of the source; the
     // zero chunk that pads the count to even reads within channel C - 1
-    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const unsigned plane = (unsigned)(sg.IH * sg.IW), cs = (unsigned)sg.cs;
     const int c0 = min(ck * C::KC, sg.C - 1);
-    const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
-    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
+    const unsigned last = 4u * ((unsigned)(min(sg.C - c0, C::KC) - 1) * cs + plane - 1u);
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * cs;
 #pragma unroll
     for (int it = 0; it < C::VITER; ++it)
 #pragma unroll

@@ -82,7 +82,7 @@ template <class C>
 __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int oy0, int ox0)
 {
     const int tid = threadIdx.x;
-    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const unsigned cs = (unsigned)sg.cs;
 #pragma unroll
     for (int it = 0; it < C::VITER; ++it) {
         // items past NITEM (a partial last round) read clamped, valid
@@ -93,13 +93,13 @@ __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int 
 #pragma unroll
         for (int c = 0; c < 6; ++c) {
             const int ix = reflect1(ox0 + 4 * t - 1 + c, sg.IW);
-            sl.po[it][c] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + ix));
+            sl.po[it][c] = 4u * ((unsigned)ci * cs + (unsigned)(iy * sg.IW + ix));
         }
         if constexpr (C::V4) {
             // d1..d4 in place; a tile past the plane's right edge (outputs
             // dropped) reads the row's last quad instead
             const int x4 = min(ox0 + 4 * t, sg.IW - 4);
-            sl.po[it][1] = 4u * ((unsigned)ci * plane + (unsigned)(iy * sg.IW + x4));
+            sl.po[it][1] = 4u * ((unsigned)ci * cs + (unsigned)(iy * sg.IW + x4));
         }
         sl.vl[it] = idx < C::NITEM ? r * C::VRS + t * C::KCP + ci : C::IR * C::VRS + (idx - C::NITEM) % 64;
     }
@@ -146,12 +146,13 @@ __device__ __forceinline__ void w4_load_d(W4Stage<C> &st, const W4Slots<C> &sl, 
 {
     // channels past C (zero weights) read the last float of the source; the
     // zero chunk that pads the count to even reads within channel C - 1
-    const unsigned plane = (unsigned)(sg.IH * sg.IW);
+    const unsigned plane = (unsigned)(sg.IH * sg.IW), cs = (unsigned)sg.cs;
     const int c0 = min(ck * C::KC, sg.C - 1);
-    const unsigned last = 4u * ((unsigned)min(sg.C - c0, C::KC) * plane - 1u);
-    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * plane;
+    const unsigned last = 4u * ((unsigned)(min(sg.C - c0, C::KC) - 1) * cs + plane - 1u);
+    const LAMA_GLOBAL float *src = gp(sg.src) + (long)c0 * cs;
     if constexpr (C::V4) {
-        const unsigned last4 = last - 12u;  // the last quad: 16-byte aligned, as the plane size is
+        // the last quad: 16-byte aligned, as the plane size and stride are
+        const unsigned last4 = last - 12u;
 #pragma unroll
         for (int it = 0; it < C::VITER; ++it) {
             const float4 m = *at_byte<float4>(src, min(sl.po[it][1], last4));
@@ -248,7 +249,7 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
     ConvSeg sg = P.s0;  // held in registers across the barriers
     if (P.ksplit > 1) {
         const int c0 = ks * P.kchunks * C::KC;
-        sg.src += (long)c0 * sg.IH * sg.IW;
+        sg.src += (long)c0 * sg.cs;
         sg.wt += (long)ks * P.kchunks * C::WCH;
         sg.C -= c0;
         sg.nchunk = P.kchunks;

@@ -356,6 +356,15 @@ bool fold_bns(Arena &A, const WeightSrc &S, const std::vector<std::pair<std::str
 
 bool is_pow2(int n) { return n > 0 && (n & (n - 1)) == 0; }
 
+// Plane stride of the bottleneck activations and of the stacked spectrum:
+// the plane length rounded up to a multiple of 4 floats, so that every plane
+// of a 256-byte aligned buffer is 16-byte aligned and the float4 kernels run
+// on planes of any length (75 x 75 = 5625, 75 x 38 = 2850 at 600 x 600).
+// The padding floats are never read as data: the pointwise kernels' last
+// float4 run of a plane feeds only output columns past the plane, which are
+// not stored, and the transforms and 3x3 convolutions index rows.
+size_t pad4(size_t n) { return (n + 3) & ~(size_t)3; }
+
 }  // namespace
 
 void Engine::release_scratch_owner()
@@ -429,29 +438,36 @@ bool Engine::open(std::string &err)
     // process, with that device current -- its code object is loaded and the
     // array's address on this device looked up (hipModuleGetGlobal, the
     // module-loaded form of hipGetSymbolAddress); every later use goes through
-    // that address.
+    // that address.  A failed set-up (for instance no room on a nearly full
+    // device) is not an error of the open: only forward_device_noalloc then
+    // fails, with this message.
     id_ = ++g_engine_ids;
     {
         std::lock_guard<std::mutex> lk(g_scratch_mu);
         DeviceScratch &d = g_scratch[device_];
         if (!d.ptr) {
+            std::string serr;
             hipModule_t m = nullptr;
-            if (!check(hip_->hipModuleLoadData(&m, lama_scratch_hsaco_start), "hipModuleLoadData(scratch)", err))
-                return false;
             hipDeviceptr_t p = nullptr;
             size_t n = 0;
-            if (!check(hip_->hipModuleGetGlobal(&p, &n, m, "lama_scratch"), "hipModuleGetGlobal(lama_scratch)", err)) {
-                hip_->hipModuleUnload(m);
-                return false;
+            if (!check(hip_->hipModuleLoadData(&m, lama_scratch_hsaco_start), "hipModuleLoadData(scratch)", serr)) {
+                m = nullptr;
+            } else if (!check(hip_->hipModuleGetGlobal(&p, &n, m, "lama_scratch"), "hipModuleGetGlobal(lama_scratch)",
+                              serr)) {
+                p = nullptr;
+            } else if (!p || n < LAMA_SCRATCH_BYTES) {
+                serr = "lama_scratch: " + std::to_string(n) + " bytes, expected " + std::to_string(LAMA_SCRATCH_BYTES);
+                p = nullptr;
             }
-            if (!p || n < LAMA_SCRATCH_BYTES) {
-                hip_->hipModuleUnload(m);
-                err = "lama_scratch: " + std::to_string(n) + " bytes, expected " + std::to_string(LAMA_SCRATCH_BYTES);
-                return false;
+            if (p) {
+                d.mod = m;
+                d.ptr = p;
+                d.bytes = n;
+            } else {
+                if (m) hip_->hipModuleUnload(m);
+                hip_->hipGetLastError();  // the failure is reported by the entry point, not by a later call
+                scratch_err_ = serr;
             }
-            d.mod = m;
-            d.ptr = p;
-            d.bytes = n;
         }
         scratch_ = d.ptr;
     }
@@ -494,6 +510,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_FIN_GROUPS")) fin_groups_force_ = atoi(t);
     if (const char *t = getenv("LAMA_EDGE_TILE")) edge_force_ = atoi(t);
+    if (const char *t = getenv("LAMA_PW_TILE")) pw_force_ = atoi(t);
     if (const char *t = getenv("LAMA_W4_LDSPAD")) w4_ldspad_force_ = atoi(t);
     if (const char *t = getenv("LAMA_CONVT_ROWS")) convt_rows_ = atoi(t) != 0;
     if (const char *t = getenv("LAMA_HEAD_R")) head_r_ = atoi(t) != 0;
@@ -704,15 +721,19 @@ hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) co
     if ((family == F_CONV3S2 || family == F_CONVT) && tile_variant(family, probs[0].OH, probs[0].OW) == 1)
         return fn_edge_q_[family == F_CONVT];
     if (family != F_CONV1 && family != F_CONV1R) return fn_[family];
-    // the widest activation loads every plane of the launch allows
-    int vw = 4;
+    // the widest activation loads every plane of the launch allows: float4
+    // runs need 16-byte aligned planes a multiple of 4 floats apart (the last
+    // run of a plane may then read up to 3 floats of its padding)
+    bool v4 = true, v2 = true;
     for (size_t i = 0; i < n; ++i) {
         const ConvSeg &s = probs[i].s0;
         const size_t N = (size_t)s.IH * s.IW;
-        if (N % 4 != 0 || (uintptr_t)s.src % 16 != 0) vw = std::min(vw, 2);
-        if (N % 2 != 0 || N < 4 || (uintptr_t)s.src % 8 != 0) vw = 1;
+        if (s.cs % 4 != 0 || (uintptr_t)s.src % 16 != 0) v4 = false;
+        if (N % 2 != 0 || s.cs % 2 != 0 || N < 4 || (uintptr_t)s.src % 8 != 0) v2 = false;
     }
-    if (vw == 4 && tile_variant(family, probs[0].OH, probs[0].OW, probs[0].M) == 0) return fn_pw_kh_[family == F_CONV1R];
+    const int vw = v4 ? 4 : v2 ? 2 : 1;
+    if (vw == 4 && tile_variant(family, probs[0].OH, probs[0].OW, probs[0].M, probs[0].s0.cs) == 0)
+        return fn_pw_kh_[family == F_CONV1R];
     return vw == 4 ? fn_[family] : vw == 2 ? fn_pw_v2_[family == F_CONV1R] : fn_pw_any_[family == F_CONV1R];
 }
 
@@ -747,18 +768,20 @@ int Engine::w4_variant(int OH, int OW) const
 // plane with fewer tiles than 2 x 32 (0), which is where the width leaves
 // much of a 32-pixel row empty (75: 3 x 32 columns for 75, 5 x 16 for 80).
 // LAMA_EDGE_TILE=32 or 16 (read at open) forces one.
-int Engine::tile_variant(int family, int OH, int OW, int M) const
+int Engine::tile_variant(int family, int OH, int OW, int M, long cs) const
 {
     if (family == F_CONV3 || family == F_CONV3G) return w4_variant(OH, OW);
-    // pointwise over N = OH * OW pixels into M channels: 0 = the K-half
-    // kernels, for float4-aligned planes whose 64 x 64 tiles would give at
-    // most two workgroups per CU (512x512: 277.8-278.1 vs 274.8 passes/s with
-    // conv1 and the FU conv in them, 256x256 429-436 vs 426; at 1024x1024 and
-    // 2048x2048, with three or more workgroups per CU, 64 x 64 tiles were
-    // 1-2% faster); 1 = 64 x 64 tiles
+    // pointwise over N = OH * OW pixels into M channels, input planes cs
+    // floats apart (0: N): 0 = the K-half kernels, for float4-aligned planes
+    // (cs % 4 == 0) whose 64 x 64 tiles would give at most two workgroups per
+    // CU (512x512: 277.8-278.1 vs 274.8 passes/s with conv1 and the FU conv
+    // in them, 256x256 429-436 vs 426; at 1024x1024 and 2048x2048, with three
+    // or more workgroups per CU, 64 x 64 tiles were 1-2% faster); 1 = 64 x 64
+    // tiles
     if (family == F_CONV1 || family == F_CONV1R) {
         const long n = (long)OH * OW, tiles = (n + 63) / 64 * ((M + 63) / 64);
-        return LAMA_PW_KH && n % 4 == 0 && tiles <= 2 * LAMA_CUS ? 0 : 1;
+        const bool kh = pw_force_ ? pw_force_ == 32 : tiles <= 2 * LAMA_CUS;
+        return LAMA_PW_KH && (cs ? cs : n) % 4 == 0 && kh ? 0 : 1;
     }
     if (family != F_CONV3S2 && family != F_CONVT) return 0;
     if (edge_force_ == 32) return 0;
@@ -768,24 +791,20 @@ int Engine::tile_variant(int family, int OH, int OW, int M) const
 }
 
 // Dynamic LDS added to each F(4,3) workgroup (bytes), to hold the GEMMs at
-// two workgroups per CU.  The kernels need 33.5 KB and 130 registers, so
-// three fit on a CU; that is faster where the FFC's A and B launches have
-// more workgroups than three per CU or no more than two (1024 x 1024: 73.5
-// vs 72.5 passes/s; 512 x 512: 261.9 vs 259.9), but where they have between
-// two and four per CU (600 x 600: 800 workgroups) a third GEMM workgroup on
-// a CU leaves no room for the SpectralTransform's conv2 (160 registers), the
-// critical path there: 159.8 padded vs 157.9.  LAMA_W4_LDSPAD=0/1 (read at
-// open) forces it off or on.
+// two workgroups per CU.  The kernels need 33.5 KB and 132-138 registers, so
+// three fit on a CU.  Padding was faster where the FFC's A and B launches
+// have between two and four workgroups per CU (600 x 600: 800 workgroups)
+// while the SpectralTransform's 1x1 convolutions ran with per-element loads
+// on the unaligned 75 x 75 planes (159.8 padded vs 157.9 passes/s); with the
+// planes at 16-byte aligned strides and float4 loads, three GEMM workgroups
+// per CU are faster there (175.2-175.3 vs 161.5-171.9), so it is off unless
+// LAMA_W4_LDSPAD=1 (read at open) forces it on.
 unsigned Engine::w4_lds_pad(int h8, int w8, int ks) const
 {
-    if (wino_ != 4) return 0;
-    int tr, tc;
-    tile_shape(F_CONV3, tr, tc, 4, w4_variant(h8, w8));
-    const long tiles = (long)((w8 + tc - 1) / tc) * ((h8 + tr - 1) / tr);
-    const long pair = 16 * tiles * ks;  // A: 8 M blocks; B: 2 M blocks x 4 K ranges; each x ks
-    const bool pad = w4_ldspad_force_ >= 0 ? w4_ldspad_force_ == 1
-                                           : pair > 2 * (long)LAMA_CUS && pair < 4 * (long)LAMA_CUS;
-    return pad ? 24576u : 0u;
+    (void)h8;
+    (void)w8;
+    (void)ks;
+    return wino_ == 4 && w4_ldspad_force_ == 1 ? 24576u : 0u;
 }
 
 // The FFC GEMMs' K split: at small planes the F(4,3) launches have few
@@ -845,8 +864,8 @@ void Engine::pw_ksplit_for(int h, int w, const FftGeom &fg, int &k1, int &ku) co
         while (s < LAMA_PW_KSPLIT_MAX && nb * 2 * s <= LAMA_PW_KSPLIT_WG) s *= 2;
         return s;
     };
-    auto blocks = [&](long n, int m) {  // workgroups of the launch's tile variant
-        const long tc = tile_variant(F_CONV1, 1, (int)n, m) == 0 ? 32 : 64;
+    auto blocks = [&](long n, int m) {  // workgroups of the launch's tile variant (padded planes)
+        const long tc = tile_variant(F_CONV1, 1, (int)n, m, (long)pad4(n)) == 0 ? 32 : 64;
         return (n + tc - 1) / tc * ((m + 63) / 64);
     };
     k1 = pick(blocks(p8, 192));
@@ -1003,7 +1022,8 @@ size_t Engine::arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t
                             ArenaLayout &L)
 {
     const size_t P = (size_t)H * W, P2 = (size_t)(H / 2) * (W / 2), P4 = (size_t)(H / 4) * (W / 4);
-    const size_t P8 = (size_t)(H / 8) * (W / 8), PS = (size_t)(H / 8) * ((W / 8) / 2 + 1);
+    // bottleneck and spectrum planes at their padded strides
+    const size_t P8 = pad4((size_t)(H / 8) * (W / 8)), PS = pad4((size_t)(H / 8) * ((W / 8) / 2 + 1));
     size_t off = 0;
     auto take = [&](size_t bytes) {
         size_t o = off;
@@ -1072,6 +1092,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     const int Wh = W8 / 2 + 1;
     const size_t P = (size_t)H * W, P2 = (size_t)H2 * W2, P4 = (size_t)H4 * W4, P8 = (size_t)H8 * W8;
     const size_t PS = (size_t)H8 * Wh;
+    // plane strides of the bottleneck activations and the spectrum (pad4)
+    const size_t P8s = pad4(P8), PSs = pad4(PS);
 
     FftLen frow, fcol;
     std::vector<float> twr, twc;
@@ -1115,7 +1137,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         std::memcpy(desc.data() + o, src, bytes);
         return (void *)(base + o_desc + o);
     };
-    auto seg = [&](const float *src, const Packed &pk, int C, int IH, int IW) {
+    auto seg = [&](const float *src, const Packed &pk, int C, int IH, int IW, size_t cs = 0) {
         ConvSeg s{};
         s.src = src;
         s.wt = wp(pk.off);
@@ -1124,6 +1146,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         s.IW = IW;
         s.nchunk = pk.nchunk;
         s.wrow = pk.wrow;
+        s.cs = (int)(cs ? cs : (size_t)IH * IW);
         return s;
     };
     bool bad_problem = false;
@@ -1135,14 +1158,14 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc, wino_, tile_variant(family, OH, OW, M));
+        tile_shape(family, tr, tc, wino_, tile_variant(family, OH, OW, M, s0.cs));
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
         q.mblocks = (M + 63) / 64;
         q.nblocks = q.tiles_x * q.tiles_y * q.mblocks;
         if (family == F_CONV1 || family == F_CONV1R) {
             // the chunk count of the kernel's chunk size over the packed row
-            const int kc = pw_kc(tile_variant(family, OH, OW, M));
+            const int kc = pw_kc(tile_variant(family, OH, OW, M, s0.cs));
             q.s0.nchunk = (q.s0.C + kc - 1) / kc;
             if (q.s0.nchunk * kc > q.s0.wrow) bad_problem = true;
         }
@@ -1170,8 +1193,10 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             nb += (unsigned)q.nblocks;
             const bool pw = family == F_CONV1 || family == F_CONV1R;
             // the float4 kernel's tile width is the one the problem was tiled for
-            if (pw && (tile_variant(family, q.OH, q.OW, q.M) == 0) != (L.fn == fn_pw_kh_[family == F_CONV1R]))
+            if (pw && (tile_variant(family, q.OH, q.OW, q.M, q.s0.cs) == 0) != (L.fn == fn_pw_kh_[family == F_CONV1R]))
                 bad_problem = true;
+            // every input plane stride set, and at least the plane
+            if (q.s0.cs < q.s0.IH * q.s0.IW || (q.s1.nchunk > 0 && q.s1.cs < q.s1.IH * q.s1.IW)) bad_problem = true;
             const int tx = pw && q.ksplit <= 1 && q.nblocks == pw_xcd_blocks(q) ? (q.tiles_x + 7) / 8 * 8 : q.tiles_x;
             if (q.nblocks != std::max(1, q.ksplit) * tx * q.tiles_y * q.mblocks ||
                 (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2] &&
@@ -1201,7 +1226,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
                 2, 2.0 * 64 * 128 * 9 * P2, f4 * (64 * P + 128 * P2 + 128 * 64 * 9));
     conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a2, down_[1], 128, H2, W2), 256, H4, W4, down_bn_[1], 256, a3, P4, W4, nullptr)},
                 3, 2.0 * 128 * 256 * 9 * P4, f4 * (128 * P2 + 256 * P4 + 256 * 128 * 9));
-    conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a3, down_[2], 256, H4, W4), 512, H8, W8, down_bn_[2], 512, X, P8, W8, nullptr)},
+    conv_launch(F_CONV3S2, {problem(F_CONV3S2, seg(a3, down_[2], 256, H4, W4), 512, H8, W8, down_bn_[2], 512, X, P8s, W8, nullptr)},
                 4, 2.0 * 256 * 512 * 9 * P8, f4 * (256 * P4 + 512 * P8 + 512 * 256 * 9), S_MAIN, -1, EV_FORK);
 
     // FFT descriptors (the same buffers serve all 36 spectral transforms)
@@ -1216,6 +1241,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     fa.rows_per_block = fg.rows_per_block;
     fa.cols_per_block = fg.cols_per_block;
     fa.tmp = fg.split ? (float *)(base + o_tmp) : nullptr;
+    fa.rs = (long)P8s;
+    fa.ss = (long)PSs;
     fa.in = Fb;
     fa.out = Sb;
     fa.in_np = fa.feat_np = 1;
@@ -1235,7 +1262,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             fk.out = Sb;
             fk.feat = nullptr;
             fk.in_np = pk1;
-            fk.in_pstride = (long)192 * P8;
+            fk.in_pstride = (long)192 * P8s;
             fk.in_scale = wp(Fw.bn1);
             fk.in_shift = wp(Fw.bn1 + 192);
             fk.feat_np = 1;
@@ -1243,12 +1270,12 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             fk.in = S2;
             fk.out = G;
             fk.in_np = pku;
-            fk.in_pstride = (long)384 * PS;
+            fk.in_pstride = (long)384 * PSs;
             fk.in_scale = wp(Fw.fu_bn);
             fk.in_shift = wp(Fw.fu_bn + 384);
             fk.feat = Fb;
             fk.feat_np = pk1;
-            fk.feat_pstride = (long)192 * P8;
+            fk.feat_pstride = (long)192 * P8s;
             fk.feat_scale = wp(Fw.bn1);
             fk.feat_shift = wp(Fw.bn1 + 192);
             d_irfft_k[k] = put(&fk, sizeof fk);
@@ -1267,7 +1294,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     auto ffc_src = [&](int k) { return k % 2 == 0 ? X : Y; };
     auto ffc_dst = [&](int k) { return k % 2 == 0 ? Y : X; };
     auto ffc_res = [&](int k) -> const float * { return k % 2 == 0 ? nullptr : X; };
-    auto gc_buf = [&](int k) { return GC + (size_t)(k % 2) * ks * 384 * P8; };
+    auto gc_buf = [&](int k) { return GC + (size_t)(k % 2) * ks * 384 * P8s; };
     auto raw = [](ConvProblem q) {
         q.scale = q.shift = nullptr;
         q.relu = 0;
@@ -1276,7 +1303,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     // LQ plane of local partial q of FFC k: the ks l2l slices at 0 .. ks-1, then
     // the 4 ks g2l slices of FFC parity k % 2
     auto lq_plane = [&](int k, int q) {
-        return LQ + (size_t)(q < ks ? q : q + (k % 2) * LAMA_G2L_RANGES * ks) * 128 * P8;
+        return LQ + (size_t)(q < ks ? q : q + (k % 2) * LAMA_G2L_RANGES * ks) * 128 * P8s;
     };
     // a problem split into s K slices of the packed chunks (F(4,3) kernels)
     auto kslices = [&](ConvProblem q, int s, long out_kstride) {
@@ -1299,18 +1326,18 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         static_assert(RC % 8 == 0 && RC % (2 * LAMA_WINO_KC) == 0, "whole K chunks (Winograd: chunk pairs) per range");
         const int c0 = q == 0 ? 0 : 128 + RC * (q - 1), nch = q == 0 ? 128 : RC;
         const Packed &pk = Fw.local;
-        ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8, pk, nch, H8, W8);
+        ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8s, pk, nch, H8, W8, P8s);
         sq.wt = wp(pk.off) + (size_t)(c0 / pk.KC) * pk.T * pk.KC;  // chunk c0/KC of the packed rows
         sq.nchunk = nch / pk.KC;
-        return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, lq_plane(k, q), P8, W8, nullptr));
+        return raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, lq_plane(k, q), P8s, W8, nullptr));
     };
     auto launch_a = [&](int k) {
         const FfcW &Fw = ffc_[k];
         std::vector<ConvProblem> probs{
-            kslices(part(k, 0), ks, (long)128 * P8),
-            kslices(raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8), 384, H8, W8, 0, 0, gc_buf(k), P8, W8,
-                                nullptr)),
-                    ks, (long)384 * P8)};
+            kslices(part(k, 0), ks, (long)128 * P8s),
+            kslices(raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8, P8s), 384, H8, W8, 0, 0, gc_buf(k), P8s,
+                                W8, nullptr)),
+                    ks, (long)384 * P8s)};
         // 16-byte input loads where the plane width allows (B: LAMA_W4_VEC_B)
         for (ConvProblem &q : probs) q.vec_in = wino_ == 4 && W8 % 4 == 0;
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
@@ -1326,11 +1353,11 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             // split: the g2l ranges as the K slices of one problem (F(4,3) kernels)
             const FfcW &Fw = ffc_[k];
             const Packed &pk = Fw.local;
-            ConvSeg sq = seg(ffc_src(k) + (size_t)128 * P8, pk, 384, H8, W8);
+            ConvSeg sq = seg(ffc_src(k) + (size_t)128 * P8s, pk, 384, H8, W8, P8s);
             sq.wt = wp(pk.off) + (size_t)(128 / pk.KC) * pk.T * pk.KC;
             sq.nchunk = 384 / pk.KC;
-            probs.push_back(kslices(raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, lq_plane(k, ks), P8, W8, nullptr)),
-                                    LAMA_G2L_RANGES * ks, (long)128 * P8));
+            probs.push_back(kslices(raw(problem(F_CONV3, sq, 128, H8, W8, 0, 0, lq_plane(k, ks), P8s, W8, nullptr)),
+                                    LAMA_G2L_RANGES * ks, (long)128 * P8s));
         } else {
             for (int q = 1; q <= LAMA_G2L_RANGES; ++q) probs.push_back(part(k, q));
         }
@@ -1350,20 +1377,20 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         for (int q = 0; q < np; ++q) fa2.part[q] = lq_plane(k, q);
         fa2.nparts = np;
         fa2.C = 128;
-        fa2.plane = (long)P8;
+        fa2.plane = (long)P8s;  // the padding floats too: whole float4 groups
         fa2.scale = wp(Fw.bn_l);
         fa2.shift = wp(Fw.bn_l + 128);
         fa2.res = ffc_res(k);
         fa2.out = ffc_dst(k);
         Launch L{};
-        const int g = fin_groups(P8);
+        const int g = fin_groups(P8s);
         const int ki = ks == 1 ? 0 : ks == 2 ? 1 : 2;
         L.fn = g == 2 ? fn_finalize_g2_[ki] : ki == 0 ? fn_[F_FINAL] : fn_finalize_ks_[ki - 1];
         L.family = F_FINAL;
         L.stream = S_MAIN;
         L.wait_ev = b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1;
         L.record_ev = -1;
-        L.grid = (unsigned)(128 * ((P8 + 4 * LAMA_NT * g - 1) / (4 * LAMA_NT * g)));
+        L.grid = (unsigned)(128 * ((P8s + 4 * LAMA_NT * g - 1) / (4 * LAMA_NT * g)));
         L.arg = put(&fa2, sizeof fa2);
         L.nparams = 1;
         L.step_end = -1;
@@ -1387,17 +1414,17 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         const FfcW &Fw = ffc_[k];
         // SpectralTransform conv1: f = ReLU(BN(W1 x_g)) over flat planes
         conv_launch(F_CONV1,
-                    {pw_kslices(problem(F_CONV1, seg(ffc_src(k) + 128 * P8, Fw.conv1, 384, 1, (int)P8), 192, 1, (int)P8,
-                                        Fw.bn1, 192, Fb, P8, (int)P8, nullptr),
-                                pk1, (long)192 * P8)},
+                    {pw_kslices(problem(F_CONV1, seg(ffc_src(k) + 128 * P8s, Fw.conv1, 384, 1, (int)P8, P8s), 192, 1,
+                                        (int)P8, Fw.bn1, 192, Fb, P8s, (int)P8, nullptr),
+                                pk1, (long)192 * P8s)},
                     -1, 2.0 * 384 * 192 * P8, f4 * (384 * P8 + pk1 * 192 * P8 + 192 * 384), S_SIDE,
                     k == 0 ? EV_FORK : -1);
         push_fft(p, false, fg, d_rfft_k[k], S_SIDE, f4 * pk1 * 192 * P8, 8.0 * 192 * PS);
         // FourierUnit conv over the stacked spectrum + BN + ReLU
         conv_launch(F_CONV1,
-                    {pw_kslices(problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS), 384, 1, (int)PS, Fw.fu_bn, 384, S2, PS,
-                                        (int)PS, nullptr),
-                                pku, (long)384 * PS)},
+                    {pw_kslices(problem(F_CONV1, seg(Sb, Fw.fu, 384, 1, (int)PS, PSs), 384, 1, (int)PS, Fw.fu_bn, 384,
+                                        S2, PSs, (int)PS, nullptr),
+                                pku, (long)384 * PSs)},
                     -1, 2.0 * 384 * 384 * PS, f4 * ((1 + pku) * 384 * PS + 384 * 384), S_SIDE);
         push_fft(p, true, fg, d_irfft_k[k], S_SIDE, 8.0 * pku * 192 * PS, (1 + pk1) * f4 * 192 * P8);  // + the fused feat read
     };
@@ -1405,11 +1432,11 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         const FfcW &Fw = ffc_[k];
         const float *res = ffc_res(k);
         // global: BN_g(l2g(x_l) + conv2(f + ifft)) (+ residual)
-        ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8), 384, 1, (int)P8, Fw.bn_g, 384,
-                                 ffc_dst(k) + 128 * P8, P8, (int)P8, res ? res + 128 * P8 : nullptr);
+        ConvProblem q2 = problem(F_CONV1R, seg(G, Fw.conv2, 192, 1, (int)P8, P8s), 384, 1, (int)P8, Fw.bn_g, 384,
+                                 ffc_dst(k) + 128 * P8s, P8s, (int)P8, res ? res + 128 * P8s : nullptr);
         q2.addend = gc_buf(k);
         q2.naddend = ks;  // the l2g K slices
-        q2.addend_kstride = (long)384 * P8;
+        q2.addend_kstride = (long)384 * P8s;
         conv_launch(F_CONV1R, {q2}, k % 2 == 1 ? 5 + k / 2 : -1, 2.0 * 192 * 384 * P8,
                     f4 * (192 * P8 + 384 * P8 * (res ? 3 : 2) + 384 * 192), S_SIDE, k % 2 ? EV_A1 : EV_A0,
                     k % 2 ? EV_S1 : EV_S0);
@@ -1431,7 +1458,9 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         std::vector<ConvProblem> ph;
         for (int k = 0; k < (convt_rows_ ? 2 : 4); ++k) {
             const size_t oplane = (size_t)(2 * uh[u]) * (2 * uw[u]);
-            ConvProblem q = problem(F_CONVT, seg(usrc[u], convt_rows_ ? U.row[k] : U.ph[k], U.cin, uh[u], uw[u]), U.cout,
+            ConvProblem q = problem(F_CONVT,
+                                    seg(usrc[u], convt_rows_ ? U.row[k] : U.ph[k], U.cin, uh[u], uw[u], u == 0 ? P8s : 0),
+                                    U.cout,
                                     uh[u], uw[u], U.bn, U.cout, udst[u], oplane, 2 * uw[u], nullptr);
             q.bias = wp(U.bias);
             q.oy_mul = q.ox_mul = 2;
@@ -1503,15 +1532,15 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         return false;
     }
     // dump sources per step (nullptr: derived on the host)
-    p.step_src.assign(kSteps, {nullptr, 0});
-    p.step_src[1] = {a1, 64 * P};
-    p.step_src[2] = {a2, 128 * P2};
-    p.step_src[3] = {a3, 256 * P4};
-    for (int s = 4; s <= 23; ++s) p.step_src[s] = {X, 512 * P8};
-    p.step_src[24] = {a3, 256 * P4};
-    p.step_src[25] = {a2, 128 * P2};
-    p.step_src[26] = {a1, 64 * P};
-    p.step_src[28] = {out, 3 * P};
+    p.step_src.assign(kSteps, {nullptr, 0, 0, 0});
+    p.step_src[1] = {a1, 64, P, P};
+    p.step_src[2] = {a2, 128, P2, P2};
+    p.step_src[3] = {a3, 256, P4, P4};
+    for (int s = 4; s <= 23; ++s) p.step_src[s] = {X, 512, P8, P8s};
+    p.step_src[24] = {a3, 256, P4, P4};
+    p.step_src[25] = {a2, 128, P2, P2};
+    p.step_src[26] = {a1, 64, P, P};
+    p.step_src[28] = {out, 3, P, P};
 
     p.desc_host = std::move(desc);
     p.desc_off = o_desc;
@@ -1706,19 +1735,29 @@ bool Engine::run(Plan &p, hipStream_t s, float *const *steps, std::string &err, 
             if (stp < 0) continue;
             const bool want = steps[stp] || (stp == 26 && steps[27]);
             if (!want) continue;
-            auto src = p.step_src[stp];
-            std::vector<float> tmp;
+            const Plan::StepSrc &src = p.step_src[stp];
+            std::vector<float> tmp, padded;
             float *dst = steps[stp];
             if (!dst) {
-                tmp.resize(src.second);
+                tmp.resize(src.planes * src.plane);
                 dst = tmp.data();
             }
             // a step is complete when every stream has drained
             for (hipStream_t q : st)
                 if (!check(hip_->hipStreamSynchronize(q), "hipStreamSynchronize", err)) return false;
-            if (!check(hip_->hipMemcpyAsync(dst, src.first, src.second * 4, hipMemcpyDeviceToHost, s), "hipMemcpy(dump)", err) ||
+            // planes at a padded stride come down whole and are packed here
+            float *land = dst;
+            if (src.stride != src.plane) {
+                padded.resize(src.planes * src.stride);
+                land = padded.data();
+            }
+            if (!check(hip_->hipMemcpyAsync(land, src.src, src.planes * src.stride * 4, hipMemcpyDeviceToHost, s),
+                       "hipMemcpy(dump)", err) ||
                 !check(hip_->hipStreamSynchronize(s), "hipStreamSynchronize", err))
                 return false;
+            if (land != dst)
+                for (size_t c = 0; c < src.planes; ++c)
+                    std::memcpy(dst + c * src.plane, land + c * src.stride, src.plane * 4);
             if (stp == 26 && steps[27]) host_reflect_pad(dst, 64, p.H, p.W, 3, steps[27]);
         }
     }
@@ -1848,9 +1887,12 @@ bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipSt
 
 // forward_device on the device's scratch array instead of an allocated arena.
 // Host work only (plan layout, descriptor staging) plus copies and launches on
-// `s`: no device allocation, no event or graph creation (profiling is off for
-// these passes).  The descriptors are re-uploaded (on `s`) whenever another
-// context or another shape used the array last.
+// `s`: no device allocation, no event or graph creation (profiling and the
+// launch timeline are off for these passes).  The descriptors are re-uploaded
+// (on `s`) whenever another context or another shape used the array last.
+// A stream under capture is refused: a captured pass would replay against
+// whatever descriptors the shared array holds at replay time, which another
+// context or shape may have replaced, with the captured grid sizes.
 bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err)
 {
     if (!have_weights_) {
@@ -1859,10 +1901,17 @@ bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_ou
     }
     if (!shape_ok(h, w, err)) return false;
     if (!scratch_) {
-        err = "the no-allocation scratch array was not set up";
+        err = "the no-allocation scratch array was not set up" + (scratch_err_.empty() ? "" : ": " + scratch_err_);
         return false;
     }
     if (!s) s = stream_;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (!check(hip_->hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing", err)) return false;
+    if (cap != hipStreamCaptureStatusNone) {
+        err = "forward_device_noalloc cannot be captured into a graph: its launch descriptors live in the "
+              "device's shared scratch array, which any later call may overwrite";
+        return false;
+    }
     const bool fresh = !(na_plan_.arena && na_plan_.H == h && na_plan_.W == w);
     if (fresh) {
         uint64_t need = 0, wb = 0;
@@ -1892,8 +1941,11 @@ bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_ou
             d.w = w;
         }
     }
+    // profiling and the timeline would allocate (events, the stamp buffer)
     const uint32_t prof = prof_mask_;
+    const bool tl = timeline_;
     prof_mask_ = 0;
+    timeline_ = false;
     const bool ok =
         check(hip_->hipMemcpyAsync(na_plan_.in, d_in, 4ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(input)",
               err) &&
@@ -1901,6 +1953,7 @@ bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_ou
         check(hip_->hipMemcpyAsync(d_out, na_plan_.out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s),
               "hipMemcpy(output)", err);
     prof_mask_ = prof;
+    timeline_ = tl;
     return ok && mark_done(s, err);
 }
 
@@ -2057,6 +2110,8 @@ SpecPlan *Engine::spec_plan_for(int h, int w, std::string &err)
     fa.rows_per_block = fg.rows_per_block;
     fa.cols_per_block = fg.cols_per_block;
     fa.tmp = fg.split ? F(o_tmp) : nullptr;
+    fa.rs = (long)P;  // the isolated transform's planes are unpadded
+    fa.ss = (long)PS;
     fa.in = sp.f;
     fa.out = sp.s;
     void *d_rfft = put(&fa, sizeof fa);
@@ -2074,6 +2129,7 @@ SpecPlan *Engine::spec_plan_for(int h, int w, std::string &err)
         q.s0.IW = N;
         q.s0.nchunk = pk.nchunk;
         q.s0.wrow = pk.wrow;
+        q.s0.cs = N;
         q.M = M;
         q.OH = 1;
         q.OW = N;
@@ -2418,11 +2474,12 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.s0.IW = family == F_CONV1 ? h * w : w;
     q.s0.nchunk = pk.nchunk;
     q.s0.wrow = pk.wrow;
+    q.s0.cs = h * w;
     q.M = cout;
     q.OH = family == F_CONV1 ? 1 : oh;
     q.OW = family == F_CONV1 ? oh * ow : ow;
     int tr, tc;
-    tile_shape(family, tr, tc, wino, tile_variant(family, q.OH, q.OW, q.M));
+    tile_shape(family, tr, tc, wino, tile_variant(family, q.OH, q.OW, q.M, q.s0.cs));
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
     q.mblocks = (cout + 63) / 64;
@@ -2480,6 +2537,7 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
         c.s0.IW = w;
         c.s0.nchunk = ph[k].nchunk;
         c.s0.wrow = ph[k].wrow;
+        c.s0.cs = h * w;
         c.M = cout;
         c.OH = h;
         c.OW = w;
@@ -2552,6 +2610,8 @@ bool Engine::op_fft(bool inverse, const float *in, const float *feat, int c, int
     a.rows_per_block = g.rows_per_block;
     a.cols_per_block = g.cols_per_block;
     a.tmp = g.split ? dtmp : nullptr;
+    a.rs = (long)h * w;
+    a.ss = (long)h * Wh;
     UPLOAD(da, nullptr, (sizeof a + 3) / 4);
     if (!check(hip_->hipMemcpy(da, &a, sizeof a, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
     Plan tmp;

@@ -85,7 +85,13 @@ struct Plan {
     // 8-bit staging of the inpaint entry points (image, mask, composite), each
     // sized for H x W; a call uses its h x w prefix
     uint8_t *rgb8 = nullptr, *mask8 = nullptr, *out8 = nullptr;
-    std::vector<std::pair<const float *, size_t>> step_src;  // per step (nullptr: host-derived)
+    // per step: the device activation (nullptr: host-derived), its planes of
+    // `plane` floats `stride` floats apart
+    struct StepSrc {
+        const float *src;
+        size_t planes, plane, stride;
+    };
+    std::vector<StepSrc> step_src;
     std::vector<Launch> launches;
     Launch build_in{}, tail_u8{};  // device build_input, and the tail with the composite fused
     // what build_plan uploads into the arena (kept for a re-upload)
@@ -228,11 +234,12 @@ private:
     int wino_ = 4;
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
-    int tile_variant(int family, int OH, int OW, int M = 0) const;
+    int tile_variant(int family, int OH, int OW, int M = 0, long cs = 0) const;
     unsigned w4_lds_pad(int h8, int w8, int ks) const;
     int ksplit_force_ = 0;  // LAMA_KSPLIT: 1, 2 or 4 forces the K split of the FFC GEMMs
     int w4_ldspad_force_ = -1;  // LAMA_W4_LDSPAD: 0 or 1 forces the F(4,3) LDS padding off or on
     int edge_force_ = 0;  // LAMA_EDGE_TILE: 32 or 16 forces the stride-2 / transposed conv tile width
+    int pw_force_ = 0;    // LAMA_PW_TILE: 32 (K-half) or 64 forces the float4 pointwise tile width
     bool convt_rows_ = true;  // LAMA_CONVT_ROWS=0: the transposed convs as four phase problems (lama_convt)
     int fin_groups_force_ = 0;  // LAMA_FIN_GROUPS: 1 or 2 forces the finalize kernel's groups per thread
     int pw_ksplit_force_ = 0;  // LAMA_PW_KSPLIT: 1, 2 or 4 forces the K split of conv1 and the FourierUnit conv
@@ -271,6 +278,7 @@ private:
     // process-wide record of which context's descriptors the array holds
     Plan na_plan_;
     void *scratch_ = nullptr;
+    std::string scratch_err_;  // why the array could not be set up at open
     uint64_t id_ = 0;
     void release_scratch_owner();
     std::map<std::pair<int, int>, SpecPlan> spec_plans_;

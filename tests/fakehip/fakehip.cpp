@@ -7,7 +7,8 @@
 //   * a memcpy, memset or launch argument that points into freed memory, and a
 //     double free, count as violations (fakehip_violations);
 //   * FAKEHIP_FAIL_MALLOC_ABOVE=<bytes> makes every hipMalloc of at least that
-//     size fail with hipErrorOutOfMemory while it is set.
+//     size fail with hipErrorOutOfMemory while it is set;
+//   * FAKEHIP_CAPTURING=1 makes every stream report an active stream capture.
 // Test infrastructure only (tests/test_fake_hip.py); no product code links it.
 #include <hip/hip_runtime_api.h>
 
@@ -267,6 +268,13 @@ hipError_t hipRuntimeGetVersion(int *v)
     return hipSuccess;
 }
 hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) { return hipErrorNotSupported; }
+// FAKEHIP_CAPTURING=1: every stream reports an active capture
+hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus *st)
+{
+    const char *e = getenv("FAKEHIP_CAPTURING");
+    *st = e && atoi(e) == 1 ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
+    return hipSuccess;
+}
 hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t *) { return hipErrorNotSupported; }
 hipError_t hipGraphInstantiate(hipGraphExec_t *, hipGraph_t, hipGraphNode_t *, char *, size_t)
 {

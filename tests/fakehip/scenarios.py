@@ -94,6 +94,20 @@ def run_plan_failure():
     mallocs = fake.fakehip_mallocs()
     eng.forward_device_noalloc(d_in, 512, 512, d_out)
     out["noalloc_512_mallocs"] = fake.fakehip_mallocs() - mallocs
+    # with the launch timeline on, still no allocation
+    eng.timeline(True)
+    mallocs = fake.fakehip_mallocs()
+    eng.forward_device_noalloc(d_in, 512, 512, d_out)
+    out["noalloc_timeline_mallocs"] = fake.fakehip_mallocs() - mallocs
+    eng.timeline(False)
+    # a stream under capture is refused
+    os.environ["FAKEHIP_CAPTURING"] = "1"
+    try:
+        eng.forward_device_noalloc(d_in, 512, 512, d_out)
+        out["noalloc_capture"] = "succeeded"
+    except E.HipError as e:
+        out["noalloc_capture"] = str(e)
+    del os.environ["FAKEHIP_CAPTURING"]
     try:
         eng.forward_device_noalloc(d_in, 600, 600, d_out)
         out["noalloc_600"] = "succeeded"

@@ -70,13 +70,16 @@ def test_every_shape_plans_and_issues_its_launches(fake_lib, weights_file):
     # two element groups per thread where one would give 2.5-4 blocks per CU
     assert p["600x600"]["finalize"] == "lama_finalize_g2"
     assert p["1024x1024"]["finalize"] == "lama_finalize"
-    # 1x1 activation loads by plane alignment: 4096 (float4), 5625 (scalar);
-    # K-half tiles where 64 x 64 tiles would give at most two workgroups per CU
+    # 1x1 activation loads as float4 runs on every bottleneck plane (5625
+    # pixels at 600x600 lie 5628 floats apart); K-half tiles where 64 x 64
+    # tiles would give at most two workgroups per CU
     assert p["512x512"]["conv1x1"] == "lama_conv1x1_kh"
     assert p["512x512"]["conv1x1res"] == "lama_conv1x1_res_kh"
     assert p["1024x1024"]["conv1x1"] == "lama_conv1x1"
     assert p["1024x1024"]["conv1x1res"] == "lama_conv1x1_res"
-    assert p["600x600"]["conv1x1"] == "lama_conv1x1_s"
+    assert p["600x600"]["conv1x1"] == "lama_conv1x1_kh"
+    assert p["600x600"]["conv1x1res"] == "lama_conv1x1_res"  # 528 64 x 64 tiles: more than two per CU
+    assert p["600x592"]["conv1x1"] == "lama_conv1x1_kh"
     # arena sizes as measured on the MI355X (MiB)
     mib = {k: v["arena"] / 2**20 for k, v in p.items()}
     for shape, want in (("256x256", 69.0), ("512x512", 179.1), ("600x600", 245.8), ("1024x1024", 727.7)):
@@ -100,5 +103,7 @@ def test_failed_plan_allocation_is_an_error_and_noalloc_allocates_nothing(fake_l
     assert "hipMalloc(activations)" in o["plan"], o["plan"]
     assert o["forward_after_failed_plan"] == "ok"
     assert o["noalloc_512_mallocs"] == 0
+    assert o["noalloc_timeline_mallocs"] == 0
+    assert "captured" in o["noalloc_capture"], o["noalloc_capture"]
     assert "600" in o["noalloc_600"] or "scratch" in o["noalloc_600"], o["noalloc_600"]
     assert o["violations"] == 0
