@@ -54,6 +54,12 @@
 #define LAMA_FFT_C4 16
 #endif
 
+// The 75 x 75 single-block transforms in one LDS buffer (1: passes in place
+// through registers) or two (0: ping-pong, one barrier fewer per pass)
+#ifndef LAMA_FFT75_IP
+#define LAMA_FFT75_IP 1
+#endif
+
 // Complex values per ping-pong buffer of the single-block FFT kernels: the
 // row-pair layout [(h+1)/2][w] or the half spectrum [h][w/2+1], rounded up to
 // even so the second buffer is 16-byte aligned.  (Padding the rows against

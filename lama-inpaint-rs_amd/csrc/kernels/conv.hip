@@ -57,8 +57,11 @@ struct Cfg {
     static constexpr int NPB = (NPIX + 15) / 16;            // 16-pixel blocks
     static constexpr int P_SLOTS = NPB * 16 * KC;
     static constexpr int PITER = (P_SLOTS + LAMA_NT - 1) / LAMA_NT;
-    // staging is branch-free: slots past the data land in a dummy tail
-    static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT - W4) * 4;
+    // staging is branch-free: weight slots past the data land in a dummy
+    // tail of one float4 per lane, which every wave shares (its contents are
+    // never read), so that the stages stay small enough for four
+    // workgroups per CU
+    static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT > W4 ? 64 * 4 : 0);
     static constexpr int P_LDS = PR * PCP * KCP + 64;
     static constexpr int LDS = W_LDS + P_LDS;
     static_assert(TR * TC == 64, "pixel tile must hold 64 pixels");
@@ -102,7 +105,7 @@ __device__ __forceinline__ void make_wslots(Slots<C> &sl, const ConvSeg &sg, int
         const int idx = tid + it * LAMA_NT;
         const int row = idx / (C::WK / 4), c4 = idx % (C::WK / 4);
         const bool in = idx < C::W4;
-        sl.wl[it] = in ? row * C::WSTR + c4 * 4 : 64 * C::WSTR + (idx - C::W4) * 4;
+        sl.wl[it] = in ? row * C::WSTR + c4 * 4 : 64 * C::WSTR + (idx & 63) * 4;
         sl.wg[it] = in ? min(m0 + row, M - 1) * sg.wrow + c4 * 4 : 0;
     }
 }
@@ -852,7 +855,7 @@ struct CfgRows {
     static constexpr int NPB = (NPIX + 15) / 16;
     static constexpr int P_SLOTS = NPB * 16 * KC;
     static constexpr int PITER = (P_SLOTS + LAMA_NT - 1) / LAMA_NT;
-    static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT - W4) * 4;
+    static constexpr int W_LDS = 64 * WSTR + (WITER * LAMA_NT > W4 ? 64 * 4 : 0);  // as Cfg
     static constexpr int P_LDS = PR * PCP * KCP + 64;
     static constexpr int LDS = W_LDS + P_LDS;
     static_assert(TR * TC == 64, "pixel tile must hold 64 positions");

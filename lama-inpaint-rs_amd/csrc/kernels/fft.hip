@@ -1018,7 +1018,7 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
     }
 LAMA_FFT_CT(64, false)
 LAMA_FFT_CT(32, false)
-LAMA_FFT_CT(75, true)
+LAMA_FFT_CT(75, LAMA_FFT75_IP)
 #undef LAMA_FFT_CT
 
 // ---- split mode with compile-time shapes: square power-of-two planes -------

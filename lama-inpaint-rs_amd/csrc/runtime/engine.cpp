@@ -82,7 +82,7 @@ const char *const kPwV2Name[2] = {"lama_conv1x1_v2", "lama_conv1x1_res_v2"};
 // Single-block FFT kernels with the plane shape fixed at compile time.
 const int kFftCtSide[3] = {64, 32, 75};
 // the kernel keeps one plane buffer in LDS, not two (LAMA_FFT_CT's IP)
-const bool kFftCtInPlace[3] = {false, false, true};
+const bool kFftCtInPlace[3] = {false, false, LAMA_FFT75_IP != 0};
 const char *const kFftCtName[3][2] = {
     {"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}, {"lama_rfft2_75", "lama_irfft2_75"}};
 
