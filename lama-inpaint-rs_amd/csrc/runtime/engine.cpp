@@ -1772,18 +1772,23 @@ void Engine::free_plan(Plan &p)
     p.arena = nullptr;
 }
 
-// The plan's launch list as one HIP graph: captured from the engine's two
-// streams on the first forward at a shape (the side stream joins the capture
-// through the fork event and rejoins through the final side event), then
-// replayed with one hipGraphLaunch.  The graph holds kernel nodes and event
-// edges only.  Used when LAMA_GRAPH=1; profiling and step dumps always take
-// the per-launch path.
+// The plan's launch list as one HIP graph: captured from the engine's three
+// streams on the first forward at a shape (the side streams join the capture
+// through the fork event and rejoin through the events the main stream waits
+// for), then replayed with one hipGraphLaunch.  The graph holds kernel nodes
+// and event edges only.  Used where use_graph says; profiling, the timeline
+// and step dumps always take the per-launch path.
 bool Engine::replay(Plan &p, hipStream_t s, std::string &err)
 {
     if (!p.graph) {
+        // A capture or instantiation the runtime refuses leaves the plan on
+        // the per-launch path (the same launches, issued one by one).
         hipGraph_t g = nullptr;
-        if (!check(hip_->hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture", err))
-            return false;
+        if (hip_->hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+            hip_->hipGetLastError();
+            p.graph_failed = true;
+            return run(p, s, nullptr, err);
+        }
         std::string rerr;
         capturing_ = true;
         const bool ok = run(p, stream_, nullptr, rerr);
@@ -1794,24 +1799,31 @@ bool Engine::replay(Plan &p, hipStream_t s, std::string &err)
             err = rerr;
             return false;
         }
-        if (!check(e, "hipStreamEndCapture", err)) return false;
-        const hipError_t ei = hip_->hipGraphInstantiate(&p.graph, g, nullptr, nullptr, 0);
-        hip_->hipGraphDestroy(g);
-        if (!check(ei, "hipGraphInstantiate", err)) {
+        const hipError_t ei = e == hipSuccess ? hip_->hipGraphInstantiate(&p.graph, g, nullptr, nullptr, 0) : e;
+        if (g) hip_->hipGraphDestroy(g);
+        if (ei != hipSuccess) {
+            hip_->hipGetLastError();
             p.graph = nullptr;
-            return false;
+            p.graph_failed = true;
+            return run(p, s, nullptr, err);
         }
     }
     return check(hip_->hipGraphLaunch(p.graph, s), "hipGraphLaunch", err);
 }
 
-bool Engine::use_graph() const
+bool Engine::use_graph(const Plan &p) const
 {
-    // Opt-in: on ROCm 7.2 / MI355X the replayed graph measured 158.9 passes/s
-    // at 512x512 against 163.3 for the per-launch streams.
-    const char *g = getenv("LAMA_GRAPH");
-    const bool on = g && atoi(g) == 1;
-    return on && prof_mask_ == 0;
+    // LAMA_GRAPH=1 / 0 forces the replayed graph on / off.  By default it is
+    // used for inputs of at most 256 x 256, where issuing the pass's launches
+    // one by one takes the host nearly as long as the device takes to run
+    // them (256x256: 1.93-2.13 ms of enqueue against a 2.2 ms pass; one graph
+    // launch enqueues in 0.93 ms), so a slower host would make the pass
+    // host-bound.  Above that the device time dominates and the per-launch
+    // streams measured slightly faster (512x512: 282.2 vs 280.2 passes/s).
+    // Profiled and timeline passes always take the per-launch path.
+    if (prof_mask_ != 0 || timeline_ || p.graph_failed) return false;
+    if (const char *g = getenv("LAMA_GRAPH")) return atoi(g) == 1;
+    return (long)p.H * p.W <= 256L * 256;
 }
 
 // cuda.rs:1647-1662: /tmp/gpu_step_<n>.f32 (little-endian f32, as
@@ -1854,7 +1866,7 @@ bool Engine::forward_host(const float *in, int h, int w, float *out, float *cons
         fprintf(stderr, "gpu input upload: %.3fs\n", secs(t));
     }
     t = clk::now();
-    if (!(steps || flag_profile_ || !use_graph() ? run(*p, stream_, steps, err) : replay(*p, stream_, err))) return false;
+    if (!(steps || flag_profile_ || !use_graph(*p) ? run(*p, stream_, steps, err) : replay(*p, stream_, err))) return false;
     if (flag_profile_) {
         if (!check(hip_->hipStreamSynchronize(stream_), "hipStreamSynchronize", err)) return false;
         fprintf(stderr, "gpu step loop: %.3fs\n", secs(t));
@@ -1879,7 +1891,7 @@ bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipSt
     if (!s) s = stream_;
     if (!check(hip_->hipMemcpyAsync(p->in, d_in, 4ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(input)", err))
         return false;
-    if (!(use_graph() ? replay(*p, s, err) : run(*p, s, nullptr, err))) return false;
+    if (!(use_graph(*p) ? replay(*p, s, err) : run(*p, s, nullptr, err))) return false;
     if (!check(hip_->hipMemcpyAsync(d_out, p->out, 3ul * h * w * 4, hipMemcpyDeviceToDevice, s), "hipMemcpy(output)", err))
         return false;
     return mark_done(s, err);

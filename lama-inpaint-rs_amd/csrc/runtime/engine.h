@@ -99,7 +99,7 @@ struct Plan {
     std::vector<float> twr_host, twc_host;
     size_t desc_off = 0, twr_off = 0, twc_off = 0;
     hipGraphExec_t graph = nullptr;  // the launch list captured once, replayed per forward
-    bool graph_failed = false;
+    bool graph_failed = false;       // the runtime refused the capture: per-launch path
 };
 
 // The isolated SpectralTransform of each FFC (conv1 -> rfft2 -> FU conv ->
@@ -206,7 +206,7 @@ private:
     bool replay(Plan &p, hipStream_t s, std::string &err);
     static size_t arena_layout(int H, int W, const FftGeom &fg, size_t ntwr, size_t ntwc, int ksplit, int pk1, int pku,
                                ArenaLayout &L);
-    bool use_graph() const;
+    bool use_graph(const Plan &p) const;
     void free_plan(Plan &p);
     bool launch(const Launch &L, hipStream_t s, std::string &err, hipEvent_t record = nullptr);
     bool fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err);

@@ -257,11 +257,12 @@ def test_forward_2048_whole_image_against_the_oracle(pkg, engine, oracle_cal):
     assert np.array_equal(u8g[mask == 0], img[mask == 0])
 
 
-def test_graph_replays_match_eager(pkg, engine, monkeypatch):
-    """The forward captured as one HIP graph and replayed: every replay, with
-    eager work and synchronisations in between, equals the per-launch path
-    bit for bit."""
-    img, mask = _case(pkg, 128, 96, "strokes")
+@pytest.mark.parametrize("h,w", [(128, 96), (256, 256), (512, 512)])
+def test_graph_replays_match_eager(pkg, engine, monkeypatch, h, w):
+    """The forward captured as one HIP graph and replayed (the default at
+    256 x 256 and below, LAMA_GRAPH=1 above): every replay, with eager work and
+    synchronisations in between, equals the per-launch path bit for bit."""
+    img, mask = _case(pkg, h, w, "strokes")
     x = pkg.host_api.build_input(img, mask)
     monkeypatch.setenv("LAMA_GRAPH", "0")
     eng0 = pkg.hip_engine.Engine()
@@ -273,14 +274,14 @@ def test_graph_replays_match_eager(pkg, engine, monkeypatch):
     eng1.load_weights(engine._store)
     rng = np.random.default_rng(3)
     d_in = eng1.malloc(x.nbytes)
-    d_out = eng1.malloc(3 * 128 * 96 * 4)
+    d_out = eng1.malloc(3 * h * w * 4)
     eng1.upload(d_in, x)
     for i in range(4):
         out = eng1.forward(x) if i % 2 == 0 else None
         if out is None:
-            eng1.forward_device(d_in, 128, 96, d_out)
+            eng1.forward_device(d_in, h, w, d_out)
             eng1.synchronize()
-            out = np.empty((3, 128, 96), np.float32)
+            out = np.empty((3, h, w), np.float32)
             eng1.download(out, d_out)
         assert np.array_equal(out, eager), f"replay {i}"
         # eager work between replays
