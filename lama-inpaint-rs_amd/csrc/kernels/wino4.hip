@@ -26,7 +26,9 @@
 // block's 32 tiles, K = (ci, ky).  K is walked in chunks of LAMA_WINO_KC = 4
 // input channels.  Each weight is an MFMA operand of exactly one wave, so the
 // waves load their transformed weights straight from global memory into
-// registers (the host packs them in operand order), one chunk ahead; only the
+// registers (the host packs them in operand order), two register sets that
+// alternate by chunk, each step pair's registers reloaded for the chunk after
+// next as soon as that pair's MFMAs have issued; only the
 // transformed input, which the two channel halves share, is staged in LDS
 // ([rows][u][tiles][4 (+2 pad)]), two stages with one barrier per chunk and
 // an even chunk count.  In the epilogue the two position halves of each
@@ -35,6 +37,14 @@
 #include <hip/hip_runtime.h>
 
 #include "common.h"
+
+// Weight reloads inside the MFMA sequence (w4_compute_ld): 1, the default,
+// measured 30.4 / 24.9 against 34.6 / 27.8 us per launch (l2l + l2g /
+// g2l, one stream, 512x512) and 181.5 against 175.4 passes/s at 600x600;
+// 0 reloads a chunk's weights after its last MFMA (w4_load_w).
+#ifndef LAMA_W4_WIL
+#define LAMA_W4_WIL 1
+#endif
 
 namespace {
 
@@ -220,6 +230,52 @@ __device__ __forceinline__ void w4_compute(f32x16 (&acc)[C::NUW], const float (&
     }
 }
 
+// w4_compute, reloading the weight registers with chunk `ckn` as the steps
+// that read them issue: steps 2q, 2q + 1 share one 16-byte load per lane
+// (LAMA_W4_WX4), so load q follows step 2q + 1's MFMAs and has the rest of
+// this chunk and the whole next one to land, instead of the next one only.
+template <class C>
+__device__ __forceinline__ void w4_compute_ld(f32x16 (&acc)[C::NUW], float (&w)[2 * C::NS], const float *vl,
+                                              const LAMA_GLOBAL float *wb, int ckn)
+{
+    static_assert(C::NS == 9 && LAMA_W4_WX4, "four step pairs and a last step, 16-byte weight loads");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wu = wave & 1, g = lane >> 5, j = lane & 31;
+    const int r = j / C::NTR, t = j % C::NTR;
+    const float *vrow = vl + t * C::KCP + C::H * g;
+    const LAMA_GLOBAL float *p = wb + (long)ckn * C::WCH;
+    float b[2][C::H];
+    auto rd = [&](int s, int buf) {
+        const int ky = s / C::NUW, u = C::NUW * wu + s % C::NUW;
+        lds_vec<C::H>(b[buf], vrow + (r + ky) * C::VRS + u * C::NTR * C::KCP);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+        const int cur = s & 1;
+        if (s + 1 < C::NS) rd(s + 1, cur ^ 1);
+        const int q = s % C::NUW;
+#pragma unroll
+        for (int c = 0; c < C::H; ++c)
+            acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[2 * s + c], b[cur][c], acc[q], 0, 0, 0);
+        if (s & 1) {
+            const int h = s >> 1;
+            const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(p + h * 256 + lane * 4);
+            w[4 * h] = v.x;
+            w[4 * h + 1] = v.y;
+            w[4 * h + 2] = v.z;
+            w[4 * h + 3] = v.w;
+            // keep the load here: the scheduler would otherwise sink it below
+            // the chunk's last MFMA
+            __builtin_amdgcn_sched_barrier(0);
+        } else if (s == C::NS - 1) {
+            const float2 v = *reinterpret_cast<const LAMA_GLOBAL float2 *>(p + 1024 + lane * 2);
+            w[16] = v.x;
+            w[17] = v.y;
+        }
+    }
+}
+
 // One 64-channel x RW-row x 4*NTR-pixel block of problem P (s1 absent).
 template <class C>
 __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds, float *epl)
@@ -276,13 +332,21 @@ __device__ __forceinline__ void w4_tile(const ConvProblem &P, int b, float *lds,
         __syncthreads();
         // n is even (the weights are packed in pairs of chunks): one loop exit
         for (int ck = 0; ck < n; ck += 2) {
+#if LAMA_W4_WIL
+            w4_compute_ld<C>(acc, w0, l0, wb, min(ck + 2, last));
+#else
             w4_compute<C>(acc, w0, l0);
             w4_load_w<C>(w0, wb, min(ck + 2, last));
+#endif
             w4_store_v<C>(r1, sl, l1);
             w4_load_d<C>(r1, sl, sg, min(ck + 3, last));
             __syncthreads();
+#if LAMA_W4_WIL
+            w4_compute_ld<C>(acc, w1, l1, wb, min(ck + 3, last));
+#else
             w4_compute<C>(acc, w1, l1);
             w4_load_w<C>(w1, wb, min(ck + 3, last));
+#endif
             w4_store_v<C>(r0, sl, l0);
             w4_load_d<C>(r0, sl, sg, min(ck + 4, last));
             __syncthreads();
