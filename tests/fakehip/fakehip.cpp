@@ -205,18 +205,21 @@ hipError_t hipFree(void *p)
     free(p);
     return hipSuccess;
 }
-static hipError_t copy(void *d, const void *s, size_t n)
+// Only the device side(s) of a copy are checked: the fake device memory is
+// host heap, so a host buffer may later occupy the range of a freed device
+// allocation.
+static hipError_t copy(void *d, const void *s, size_t n, hipMemcpyKind k)
 {
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        check_ptr(d, "memcpy destination");
-        check_ptr(s, "memcpy source");
+        if (k != hipMemcpyDeviceToHost) check_ptr(d, "memcpy destination");
+        if (k != hipMemcpyHostToDevice) check_ptr(s, "memcpy source");
     }
     memmove(d, s, n);
     return hipSuccess;
 }
-hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind) { return copy(d, s, n); }
-hipError_t hipMemcpyAsync(void *d, const void *s, size_t n, hipMemcpyKind, hipStream_t) { return copy(d, s, n); }
+hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind k) { return copy(d, s, n, k); }
+hipError_t hipMemcpyAsync(void *d, const void *s, size_t n, hipMemcpyKind k, hipStream_t) { return copy(d, s, n, k); }
 hipError_t hipMemset(void *d, int v, size_t n)
 {
     {
