@@ -788,7 +788,128 @@ __device__ __forceinline__ float2 ct_twiddle_fetch(const FftArgs &A)
 // IP: one plane buffer instead of two (passes and reorderings in place
 // through registers), for planes whose two buffers would keep a block from
 // sharing a CU with two FFC GEMM workgroups
-template <int N, bool IP>
+// ---- 64-point rows as wavefront-shuffle FFTs --------------------------------
+//
+// lama_rfft2_64s / lama_irfft2_64s (the plan takes them with LAMA_FFT64_SHFL=1;
+// the default keeps the LDS passes, which measured faster beside the FFC GEMM:
+// 286.5 against 285.0 passes/s at 512 x 512, while alone these are 7% and 13%
+// faster -- the lane moves are VALU instructions, which wait behind the GEMM's
+// MFMAs, where LDS accesses do not).  A row pair's 64-point transform runs in the
+// registers of 16 lanes of one wave, four values per lane, with no LDS pass
+// and no barrier: the index is split as x = 4 l + m (lane l, register m).
+// Forward (natural input): a 16-point DIF transform across the 16 lanes for
+// each m, radix 2, the partner value fetched with DPP lane moves (xor 1 and 2:
+// quad_perm; xor 4: row_shl / row_shr 4 by bank; xor 8: row_ror 8), leaves
+// lane l with Y_m[brev4(l)]; the twiddles W64^(m k1) and a radix-4 DFT over m
+// in registers give X[brev4(l) + 16 k2] in register k2.  Inverse: lane l
+// starts from x[brev4(l) + 16 m] and runs the same steps in the reverse order
+// (radix 4, twiddles, 16-point DIT across the lanes), ending with the natural
+// quad X[4 l .. 4 l + 3].  Twiddles come from the row table (exp(-2 pi i k/64),
+// f64-built, read from global memory in the prologue); the exponent sign
+// follows the plane's rule as in the LDS passes.
+
+__device__ __forceinline__ int brev4(int l) { return ((l & 1) << 3) | ((l & 2) << 1) | ((l & 4) >> 1) | ((l & 8) >> 3); }
+
+// the value of lane l ^ D of the same 16-lane row
+template <int D>
+__device__ __forceinline__ float row_xor(float v)
+{
+    const int x = __float_as_int(v);
+    int r;
+    if constexpr (D == 1)
+        r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    else if constexpr (D == 2)
+        r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+    else if constexpr (D == 4) {
+        r = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);  // row_shl 4 into banks 0, 2
+        r = __builtin_amdgcn_update_dpp(r, x, 0x114, 0xF, 0xA, false);  // row_shr 4 into banks 1, 3
+    } else {
+        static_assert(D == 8, "lane distance 1, 2, 4 or 8");
+        r = __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false);  // row_ror 8
+    }
+    return __int_as_float(r);
+}
+template <int D>
+__device__ __forceinline__ float2 row_xor2(float2 v)
+{
+    return make_float2(row_xor<D>(v.x), row_xor<D>(v.y));
+}
+
+// A lane's twiddles of the 64-point row transform: W16^((l mod D) 8 / D) for
+// the stages of half-span D = 8, 4, 2 (D = 1 needs none) and W64^(m k) for
+// m = 1, 2, 3 (k = brev4(l)), read from the row table in global memory before
+// the data arrive, so the transform waits on no barrier.
+struct Tw64 {
+    float2 s[3], m[3];
+};
+template <int SIGN>
+__device__ __forceinline__ Tw64 tw64_load(const FftArgs &A, int l)
+{
+    const LAMA_GLOBAL float2 *g = gp(reinterpret_cast<const float2 *>(A.row.tw));
+    const int k = brev4(l);
+    const int e[6] = {4 * (l % 8), 8 * (l % 4), 16 * (l % 2), k, 2 * k, 3 * k};
+    float2 v[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        v[i] = g[e[i]];
+        if (SIGN > 0) v[i].y = -v[i].y;
+    }
+    return Tw64{{v[0], v[1], v[2]}, {v[3], v[4], v[5]}};
+}
+
+// one radix-2 DIF stage of half-span D across the lanes (z: the lane's four
+// sequences; w: W16^((l mod D) 8 / D))
+template <int D>
+__device__ __forceinline__ void dif16_stage(float2 (&z)[4], int l, float2 w)
+{
+    const bool hi = (l & D) != 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float2 o = z[m], p = row_xor2<D>(o);
+        z[m] = hi ? (D == 1 ? csub(p, o) : cmul(csub(p, o), w)) : cadd(o, p);
+    }
+}
+
+// one radix-2 DIT stage of half-span D across the lanes
+template <int D>
+__device__ __forceinline__ void dit16_stage(float2 (&z)[4], int l, float2 w)
+{
+    const bool hi = (l & D) != 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float2 o = z[m], t = D == 1 ? o : cmul(o, w);
+        const float2 r = row_xor2<D>(hi ? t : o);
+        z[m] = hi ? csub(r, t) : cadd(o, r);
+    }
+}
+
+// forward: z[m] = x[4 l + m] in, z[k2] = X[brev4(l) + 16 k2] out
+template <int SIGN>
+__device__ __forceinline__ void row64_fwd(float2 (&z)[4], int l, const Tw64 &w)
+{
+    dif16_stage<8>(z, l, w.s[0]);
+    dif16_stage<4>(z, l, w.s[1]);
+    dif16_stage<2>(z, l, w.s[2]);
+    dif16_stage<1>(z, l, make_float2(1.f, 0.f));
+#pragma unroll
+    for (int m = 1; m < 4; ++m) z[m] = cmul(z[m], w.m[m - 1]);
+    dft<4>(z, SIGN);
+}
+
+// inverse direction of the same split: z[m] = x[brev4(l) + 16 m] in, z[m] = X[4 l + m] out
+template <int SIGN>
+__device__ __forceinline__ void row64_inv(float2 (&z)[4], int l, const Tw64 &w)
+{
+    dft<4>(z, SIGN);
+#pragma unroll
+    for (int m = 1; m < 4; ++m) z[m] = cmul(z[m], w.m[m - 1]);
+    dit16_stage<1>(z, l, make_float2(1.f, 0.f));
+    dit16_stage<2>(z, l, w.s[2]);
+    dit16_stage<4>(z, l, w.s[1]);
+    dit16_stage<8>(z, l, w.s[0]);
+}
+
+template <int N, bool IP, bool SH = false>
 __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
 {
     using P = CtPlane<N>;
@@ -798,6 +919,8 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
     const int c = blockIdx.x;
     // prologue: every global load before the first LDS write
     float2 tv = ct_twiddle_fetch<N>(A);
+    Tw64 tw64{};
+    if constexpr (SH) tw64 = tw64_load<SF>(A, threadIdx.x & 15);
     const LAMA_GLOBAL float *src = gp(A.in) + (long)c * A.rs;
     const KsIn kin = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, c);
     if constexpr (P::VEC) {
@@ -811,16 +934,29 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
             qb[k] = ks_ld4(src, (2 * p + 1) * W + x, kin);
         }
         ct_twiddles<N>(A, twr, twc, tv);
+        if constexpr (SH) {
+            // each thread's quad is lanes l = t mod 16 of row pair t / 16:
+            // the row transform in registers, the spectrum row to LDS
+            static_assert(RQ == 1 && W4 == 16, "one quad per thread, 16 lanes per row pair");
+            const int t = threadIdx.x, p = t >> 4, l = t & 15;
+            float2 z[4] = {make_float2(qa[0].x, qb[0].x), make_float2(qa[0].y, qb[0].y), make_float2(qa[0].z, qb[0].z),
+                           make_float2(qa[0].w, qb[0].w)};
+            row64_fwd<SF>(z, l, tw64);
+            const int k1 = brev4(l);
 #pragma unroll
-        for (int k = 0; k < RQ; ++k) {
-            const int q = threadIdx.x + k * NT;
-            if (NQ % NT != 0 && q >= NQ) break;
-            const int p = q / W4, x = (q % W4) * 4;
-            float2 *d = b0 + p * W + x;
-            d[0] = make_float2(qa[k].x, qb[k].x);
-            d[1] = make_float2(qa[k].y, qb[k].y);
-            d[2] = make_float2(qa[k].z, qb[k].z);
-            d[3] = make_float2(qa[k].w, qb[k].w);
+            for (int k2 = 0; k2 < 4; ++k2) b0[p * W + k1 + 16 * k2] = z[k2];
+        } else {
+#pragma unroll
+            for (int k = 0; k < RQ; ++k) {
+                const int q = threadIdx.x + k * NT;
+                if (NQ % NT != 0 && q >= NQ) break;
+                const int p = q / W4, x = (q % W4) * 4;
+                float2 *d = b0 + p * W + x;
+                d[0] = make_float2(qa[k].x, qb[k].x);
+                d[1] = make_float2(qa[k].y, qb[k].y);
+                d[2] = make_float2(qa[k].z, qb[k].z);
+                d[3] = make_float2(qa[k].w, qb[k].w);
+            }
         }
     } else {
         // the plane in memory order; value (y, x) goes to part y & 1 of row
@@ -843,7 +979,11 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
             for (int x = threadIdx.x; x < W; x += NT) b0[(HP - 1) * W + x].y = 0.f;
     }
     __syncthreads();
-    float2 *r = ct_stockham<W, 1, HP, W, 1, SF, IP>(b0, b1, twr);
+    float2 *r;
+    if constexpr (SH)
+        r = b0;  // the rows are transformed already
+    else
+        r = ct_stockham<W, 1, HP, W, 1, SF, IP>(b0, b1, twr);
     float2 *o = r == b0 ? b1 : b0;
     // split each row pair into the two half spectra
     auto split = [&](int idx) {
@@ -881,7 +1021,7 @@ __device__ __forceinline__ void rfft2_ct(const FftArgs &A, float2 *sm)
     }
 }
 
-template <int N, bool IP>
+template <int N, bool IP, bool SH = false>
 __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
 {
     using P = CtPlane<N>;
@@ -893,6 +1033,8 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
     const int c = blockIdx.x;
     // prologue: twiddles, this block's spectrum and the `f +` addend
     float2 tv = ct_twiddle_fetch<N>(A);
+    Tw64 tw64{};
+    if constexpr (SH) tw64 = tw64_load<-SF>(A, threadIdx.x & 15);
     const LAMA_GLOBAL float *sre = gp(A.in) + (long)(2 * c) * A.ss, *sim = sre + A.ss;
     const LAMA_GLOBAL float *f = gp(A.feat) + (long)c * A.rs;
     const KsIn kre = ks_in(A.in_np, A.in_pstride, A.in_scale, A.in_shift, 2 * c);
@@ -900,7 +1042,13 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
     const KsIn kf = ks_in(A.feat_np, A.feat_pstride, A.feat_scale, A.feat_shift, c);
     using FT = typename std::conditional<P::VEC, float4, float>::type;
     FT fpre[FP];
-    if constexpr (P::VEC) {
+    if constexpr (SH) {
+        // the quads this thread stores: rows 2p, 2p + 1 of its row pair p at x = 4 l
+        static_assert(FP == 2, "two quads per thread");
+        const int t = threadIdx.x, p = t >> 4, l = t & 15;
+#pragma unroll
+        for (int k = 0; k < FP; ++k) fpre[k] = ks_ld4(f, (long)(2 * p + k) * W + 4 * l, kf);
+    } else if constexpr (P::VEC) {
         constexpr int N4 = H * W / 4;
 #pragma unroll
         for (int k = 0; k < FP; ++k) fpre[k] = ks_ld4(f, 4L * min((int)threadIdx.x + k * NT, N4 - 1), kf);
@@ -967,6 +1115,22 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
         for (int idx = threadIdx.x; idx < HP * W; idx += NT) o[idx] = herm(idx);
     }
     __syncthreads();
+    if constexpr (SH) {
+        // row pair p in lanes l = t mod 16: x[brev4(l) + 16 m] in, the quad X[4 l ..] out
+        const int t = threadIdx.x, p = t >> 4, l = t & 15, x1 = brev4(l);
+        float2 z[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) z[m] = o[p * W + x1 + 16 * m];
+        row64_inv<-SF>(z, l, tw64);
+        LAMA_GLOBAL float4 *d4 = reinterpret_cast<LAMA_GLOBAL float4 *>(gp(A.out) + (long)c * A.rs);
+        const float4 re = make_float4(z[0].x * A.scale + fpre[0].x, z[1].x * A.scale + fpre[0].y,
+                                      z[2].x * A.scale + fpre[0].z, z[3].x * A.scale + fpre[0].w);
+        const float4 im = make_float4(z[0].y * A.scale + fpre[1].x, z[1].y * A.scale + fpre[1].y,
+                                      z[2].y * A.scale + fpre[1].z, z[3].y * A.scale + fpre[1].w);
+        d4[(2 * p) * (W / 4) + l] = re;
+        d4[(2 * p + 1) * (W / 4) + l] = im;
+        return;
+    }
     float2 *q = ct_stockham<W, 1, HP, W, 1, -SF, IP>(o, r, twr);
     if constexpr (P::VEC) {
         constexpr int N4 = H * W / 4;
@@ -1001,24 +1165,28 @@ __device__ __forceinline__ void irfft2_ct(const FftArgs &A, float2 *sm)
 
 // IP (in place) must match the host's LDS size for the kernel
 // (Engine::fft_geom: kFftCtInPlace)
-#define LAMA_FFT_CT(N, IP)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS)  \
+#define LAMA_FFT_CT(N, IP, SFX, SH)                                                                              \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_rfft2_##N##SFX(const FftArgs *__restrict__ args,      \
+                                                                                  LAMA_STAMP_PARAMS)                     \
     {                                                                                                           \
         side_priority();                                                                                        \
         LAMA_STAMP_SCOPE;                                                                                       \
         extern __shared__ float2 sm[];                                                                          \
-        rfft2_ct<N, IP>(*args, sm);                                                                             \
+        rfft2_ct<N, IP, SH>(*args, sm);                                                                         \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_##N(const FftArgs *__restrict__ args, LAMA_STAMP_PARAMS) \
+    extern "C" __global__ void __launch_bounds__(LAMA_FFT_NT) lama_irfft2_##N##SFX(const FftArgs *__restrict__ args,     \
+                                                                                   LAMA_STAMP_PARAMS)                    \
     {                                                                                                           \
         side_priority();                                                                                        \
         LAMA_STAMP_SCOPE;                                                                                       \
         extern __shared__ float2 sm[];                                                                          \
-        irfft2_ct<N, IP>(*args, sm);                                                                            \
+        irfft2_ct<N, IP, SH>(*args, sm);                                                                        \
     }
-LAMA_FFT_CT(64, false)
-LAMA_FFT_CT(32, false)
-LAMA_FFT_CT(75, LAMA_FFT75_IP)
+LAMA_FFT_CT(64, false, , false)
+LAMA_FFT_CT(32, false, , false)
+LAMA_FFT_CT(75, LAMA_FFT75_IP, , false)
+// the 64 x 64 transforms with wavefront-shuffle rows (LAMA_FFT64_SHFL=1 at plan time)
+LAMA_FFT_CT(64, false, s, true)
 #undef LAMA_FFT_CT
 
 // ---- split mode with compile-time shapes: square power-of-two planes -------

@@ -80,11 +80,14 @@ const char *const kPwAnyName[2] = {"lama_conv1x1_s", "lama_conv1x1_res_s"};
 const char *const kPwV2Name[2] = {"lama_conv1x1_v2", "lama_conv1x1_res_v2"};
 
 // Single-block FFT kernels with the plane shape fixed at compile time.
-const int kFftCtSide[3] = {64, 32, 75};
+// The fourth, 64 x 64 with wavefront-shuffle rows, only with LAMA_FFT64_SHFL=1.
+const int kFftCtSide[4] = {64, 32, 75, 64};
 // the kernel keeps one plane buffer in LDS, not two (LAMA_FFT_CT's IP)
-const bool kFftCtInPlace[3] = {false, false, LAMA_FFT75_IP != 0};
-const char *const kFftCtName[3][2] = {
-    {"lama_rfft2_64", "lama_irfft2_64"}, {"lama_rfft2_32", "lama_irfft2_32"}, {"lama_rfft2_75", "lama_irfft2_75"}};
+const bool kFftCtInPlace[4] = {false, false, LAMA_FFT75_IP != 0, false};
+const char *const kFftCtName[4][2] = {{"lama_rfft2_64", "lama_irfft2_64"},
+                                      {"lama_rfft2_32", "lama_irfft2_32"},
+                                      {"lama_rfft2_75", "lama_irfft2_75"},
+                                      {"lama_rfft2_64s", "lama_irfft2_64s"}};
 
 // The first workgroup of each problem after the first, for a grouped launch.
 ProbStarts prob_starts(const ConvProblem *q, size_t n)
@@ -515,7 +518,7 @@ bool Engine::open(std::string &err)
     if (const char *t = getenv("LAMA_CONVT_ROWS")) convt_rows_ = atoi(t) != 0;
     if (const char *t = getenv("LAMA_HEAD_R")) head_r_ = atoi(t) != 0;
 
-    for (int s = 0; s < 3; ++s)
+    for (int s = 0; s < 4; ++s)
         for (int f = 0; f < 2; ++f)
             if (!get_fn(fn_fft_ct_[s][f], kFftCtName[s][f], err))
                 return false;
@@ -887,10 +890,11 @@ bool Engine::fft_geom(int C, int H, int W, FftGeom &g, std::string &err) const
         // square 64, 32 or 75 planes have kernels with the shape compiled in
         // (LAMA_FFT_GENERIC=1 keeps the runtime-shaped ones, for tests)
         const char *gen = getenv("LAMA_FFT_GENERIC");
+        const char *shfl = getenv("LAMA_FFT64_SHFL");
         if (H == W && !(gen && atoi(gen) == 1))
             for (int s = 0; s < 3; ++s)
                 if (H == kFftCtSide[s]) {
-                    g.ct = s + 1;
+                    g.ct = (s == 0 && shfl && atoi(shfl) == 1) ? 4 : s + 1;
                     if (kFftCtInPlace[s]) g.lds = ((size_t)lama_fft_nb(H, W) + H + W) * f2;
                 }
         return true;

@@ -223,7 +223,7 @@ private:
     hipFunction_t fn_split_[4] = {};
     hipFunction_t fn_pw_any_[2] = {};  // 1x1 kernels for planes that are not float4-aligned
     hipFunction_t fn_pw_v2_[2] = {};   // 1x1 kernels for float2-aligned planes of even length
-    hipFunction_t fn_fft_ct_[3][2] = {};  // [64x64, 32x32, 75x75][rfft2, irfft2]
+    hipFunction_t fn_fft_ct_[4][2] = {};  // [64x64, 32x32, 75x75, 64x64 shuffle rows][rfft2, irfft2]
     hipFunction_t fn_split_ct_[2][4] = {};  // [256x256, 128x128][as fn_split_]
     // FFC 3x3 convolutions as Winograd F(2,3) along x (lama_conv3x3w), or
     // with LAMA_FFC_WINO=0 as the direct implicit GEMM (lama_conv3x3); chosen

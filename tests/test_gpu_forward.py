@@ -210,6 +210,24 @@ def test_compiled_shape_fft_equals_generic(pkg, engine, monkeypatch, size):
     assert rel_err(b, a) < 1e-5
 
 
+def test_forward_512_shuffle_row_fft(pkg, engine, monkeypatch):
+    """With LAMA_FFT64_SHFL=1 the 512x512 plan takes the 64 x 64 transforms
+    whose rows are wavefront-shuffle FFTs in registers; the forward agrees
+    with the default (LDS-pass) transforms to float rounding."""
+    print("case 512x512 strokes (shuffle-row vs LDS-pass 64x64 FFT)", flush=True)
+    img, mask = _case(pkg, 512, 512, "strokes")
+    x = pkg.host_api.build_input(img, mask)
+    a = engine.forward(x)
+    monkeypatch.setenv("LAMA_FFT64_SHFL", "1")
+    eng2 = pkg.hip_engine.Engine()
+    eng2.load_weights(engine._store)
+    b = eng2.forward(x)
+    assert eng2.kernel_name(512, 512, "rfft2") == "lama_rfft2_64s"
+    assert eng2.kernel_name(512, 512, "irfft2") == "lama_irfft2_64s"
+    eng2.close()
+    assert rel_err(b, a) < 1e-5
+
+
 def test_forward_2048_whole_image(pkg, engine):
     """configs[4] at its full size (bottleneck 512 x 256 x 256): checked by
     size-independent properties -- finite, bitwise repeatable, sigmoid range,

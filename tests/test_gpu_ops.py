@@ -166,6 +166,27 @@ def test_irfft2(engine, fft_mode, h, w):
     assert rel_err(got, ref) < TOL
 
 
+@pytest.mark.parametrize("inverse", [False, True])
+def test_fft64_shuffle_rows(engine, monkeypatch, inverse):
+    """The 64 x 64 transforms whose rows run as wavefront-shuffle FFTs in
+    registers (lama_rfft2_64s / lama_irfft2_64s, taken with LAMA_FFT64_SHFL=1)
+    against the oracle, as test_rfft2 / test_irfft2."""
+    monkeypatch.setenv("LAMA_FFT64_SHFL", "1")
+    rng = np.random.default_rng(6464 + inverse)
+    c = 5
+    if not inverse:
+        x = rng.standard_normal((c, 64, 64), np.float32)
+        got = engine.op_rfft2(x)
+        ref = np.concatenate([O.rfft2_ortho(x[i]) for i in range(c)], axis=0)
+    else:
+        spec = rng.standard_normal((2 * c, 64, 33), np.float32)
+        feat = rng.standard_normal((c, 64, 64), np.float32)
+        got = engine.op_irfft2(spec, 64, feat)
+        ref = np.stack([O.irfft2_ortho(spec[2 * i:2 * i + 2], 64) for i in range(c)]) + feat
+    assert got.shape == ref.shape
+    assert rel_err(got, ref) < TOL
+
+
 # cin 7 and 1: odd channel counts leave the kernel's second channel half idle
 # in the last step; 9 x 70 spans two column tiles with a partial row tile
 @pytest.mark.parametrize("h,w,cin", [(16, 64, 64), (24, 40, 64), (8, 8, 64), (64, 128, 64), (24, 40, 7),
