@@ -97,17 +97,20 @@ def main():
     # direct-convolution FLOPs, 2 Cin Cout 9 H W; the algorithm's own MFMA
     # products are the fraction `issued` of that: F(4,3) multiplies 6
     # transformed positions x 3 kernel rows per 4 output pixels (18 of the
-    # direct 36 products, 1/2), F(2,3) 4 x 3 per 2 (12 of 18, 2/3)
+    # direct 36 products, 1/2), F(2,3) 4 x 3 per 2 (12 of 18, 2/3), F(2x4, 3x3)
+    # (LAMA_FFC_WINO=42) 4 x 6 positions per 2 x 4 pixels (24 of 72, 1/3)
     wv = os.environ.get("LAMA_FFC_WINO", "4")
-    wino = 0 if wv == "0" else 2 if wv == "2" else 4
+    wino = 0 if wv == "0" else 2 if wv == "2" else 42 if wv == "42" else 4
     # the plan's own kernel for the FFC GEMMs at this size (the F(4,3) block
     # shape is chosen per plane: 2 x 64, 4 x 32 or 8 x 16 output pixels)
     dom_kernel = eng.kernel_name(S, S, "conv3x3")
-    issued = {0: 1.0, 2: 2.0 / 3.0, 4: 0.5}[wino]
+    issued = {0: 1.0, 2: 2.0 / 3.0, 4: 0.5, 42: 1.0 / 3.0}[wino]
     block = {"lama_conv3x3": "64 px", "lama_conv3x3w": "2 rows x 64 px", "lama_conv3x3w4": "2 rows x 64 px",
-             "lama_conv3x3w4n": "4 rows x 32 px", "lama_conv3x3w4q": "8 rows x 16 px"}[dom_kernel]
+             "lama_conv3x3w4n": "4 rows x 32 px", "lama_conv3x3w4q": "8 rows x 16 px",
+             "lama_conv3x3w42": "4 rows x 64 px"}[dom_kernel]
     geometry = "workgroups of 64 channels x " + block
-    method = {0: "direct implicit GEMM", 2: "Winograd F(2,3) along x", 4: "Winograd F(4,3) along x"}[wino]
+    method = {0: "direct implicit GEMM", 2: "Winograd F(2,3) along x", 4: "Winograd F(4,3) along x",
+              42: "Winograd F(2x4, 3x3)"}[wino]
     eng.profile_reset()
     eng.synchronize()
     t0 = time.perf_counter()

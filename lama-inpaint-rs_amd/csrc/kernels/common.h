@@ -109,6 +109,14 @@ static inline constexpr int lama_convt_kc(int phase)
 #ifndef LAMA_WINO_KC
 #define LAMA_WINO_KC 4
 #endif
+#ifndef LAMA_W42_KC
+// input channels per K chunk of the F(2x4, 3x3) kernel, 4 or 8 (4: 170
+// registers, 33.5 KB of LDS; 8: 222 and 58 KB, and 3% slower at 2048x2048)
+#define LAMA_W42_KC 4
+#endif
+#ifndef LAMA_W42_CH
+#define LAMA_W42_CH 64  // output channels per F(2x4, 3x3) workgroup: 32 (4 waves) or 64 (8 waves)
+#endif
 
 // output tile of the 7x7 tail kernel (rows x columns) and the adjacent
 // pixels each thread of its two channel halves computes

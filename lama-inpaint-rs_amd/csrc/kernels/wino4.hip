@@ -67,7 +67,8 @@ struct W4Cfg {
     static constexpr int H = KC / 2;             // channels per lane half and MFMA K slot
     static constexpr int KCP = KC + 2;           // LDS floats per (row, u, tile)
     static constexpr int NITEM = KC * IR * NTR;  // (ci, row, tile) input items per chunk
-    static constexpr int VITER = (NITEM + LAMA_NT - 1) / LAMA_NT;
+    static constexpr int NT = LAMA_NT;           // threads per workgroup
+    static constexpr int VITER = (NITEM + NT - 1) / NT;
     static constexpr int VRS = NU * NTR * KCP;   // LDS stride of an input row
     static constexpr int V_LDS = IR * VRS + NU * 64;  // per stage, + a dummy tail for items past NITEM
     // epilogue exchange: per channel half, two pixels x 16 registers x 64 lanes from each position half
@@ -97,7 +98,7 @@ __device__ __forceinline__ void w4_slots(W4Slots<C> &sl, const ConvSeg &sg, int 
     for (int it = 0; it < C::VITER; ++it) {
         // items past NITEM (a partial last round) read clamped, valid
         // addresses and land in the dummy tail of the V region
-        const int idx = tid + it * LAMA_NT, q = min(idx, C::NITEM - 1);
+        const int idx = tid + it * C::NT, q = min(idx, C::NITEM - 1);
         const int t = q % C::NTR, r = (q / C::NTR) % C::IR, ci = q / (C::NTR * C::IR);
         const int iy = reflect1(oy0 - 1 + r, sg.IH);
 #pragma unroll
@@ -488,3 +489,270 @@ LAMA_W4_KERNEL(lama_conv3x3w4, 16)
 LAMA_W4_KERNEL(lama_conv3x3w4n, 8)
 LAMA_W4_KERNEL(lama_conv3x3w4q, 4)
 #undef LAMA_W4_KERNEL
+
+// ---------------------------------------------------------------------------
+// FFC 3x3 convolutions as a two-dimensional Winograd F(2x4, 3x3): F(2,3)
+// along y (points 0, 1, -1, infinity) times the F(4,3) above along x.  An
+// output tile is 2 rows x 4 pixels, read from input rows r0..r3 x the six
+// columns d0..d5 of each:
+//     V_x(r) = B_x^T d(r)                        (the input transform above)
+//     V(0) = V_x(r0) - V_x(r2)   V(1) = V_x(r1) + V_x(r2)
+//     V(2) = V_x(r2) - V_x(r1)   V(3) = V_x(r1) - V_x(r3)       (B_y^T)
+//     U(vy, u) = sum over (ky, kx) of G_y[vy][ky] G_x[u][kx] g[ky][kx]
+//         G_y = (1, 0, 0; 1/2, 1/2, 1/2; 1/2, -1/2, 1/2; 0, 0, 1)   (host, f64)
+//     m(vy, u) = sum over ci of U(vy, u) V(vy, u)               (24 GEMMs)
+//     out(row 0) = A_x^T (m(0) + m(1) + m(2)),  out(row 1) = A_x^T (m(1) - m(2) - m(3))
+// 24 multiplications per 8 outputs and input channel: 2/3 of the
+// one-dimensional F(4,3)'s, 1/3 of the direct sum's.
+//
+// A workgroup (8 waves) computes 64 output channels x 32 tiles: RP = 32 / NTR
+// row pairs of NTR tiles.  Wave (wm, vy) owns channels wm*32 .. +32 and the
+// six positions (vy, 0..5) as six 32 x 32 accumulators of
+// v_mfma_f32_32x32x2f32 (GEMM columns: the block's 32 tiles).  The input rows
+// are staged x-transformed in LDS exactly as in the one-dimensional kernel;
+// each MFMA's B operand is the sum or difference of two staged rows (row vy
+// of B_y^T), formed as the operands are read.  Each wave loads its own 12
+// transformed weights per chunk into registers, reloading each 16-byte group
+// as soon as its MFMAs have issued.  The epilogue runs in four rounds, one
+// per pixel column of the tiles: every wave applies that column of A_x^T to
+// its six accumulators and parks the 16 results in LDS; each wave then
+// finishes four of the 16 register rows of its channel half, both output
+// rows, from the four y positions.
+namespace {
+
+template <int NTR_, bool V4_ = false>
+struct W42Cfg {
+    static constexpr bool V4 = V4_;               // 16-byte input loads (plane width a multiple of 4)
+    static constexpr int KC = LAMA_W42_KC;        // input channels per chunk
+    static constexpr int NU = 6, NUY = 4;         // x positions, y positions
+    static constexpr int NTR = NTR_;              // tiles per row pair
+    static constexpr int RP = 32 / NTR;           // row pairs per block
+    static constexpr int TR = 2 * RP, TC = 4 * NTR;  // output rows x pixels per block
+    static constexpr int IR = TR + 2;             // input rows per block
+    static constexpr int WK = NU * NUY * KC;      // weights per output channel and chunk (96)
+    static constexpr int WCH = 64 * WK;           // packed weights per 64-channel block and chunk
+    static constexpr int H = KC / 2;              // channels per lane half and MFMA K slot
+    static constexpr int WW = NU * H;             // weight registers per wave and chunk (12 or 24)
+    static constexpr int KCP = KC == 4 ? 6 : 12;  // LDS floats per (row, u, tile): 8- or 16-byte operand reads
+    static constexpr int NITEM = KC * IR * NTR;   // (ci, row, tile) input items per chunk
+    static constexpr int CH = LAMA_W42_CH;        // output channels per workgroup (32 or 64)
+    static constexpr int WMS = CH / 32;           // channel halves per workgroup
+    static constexpr int NT = 256 * WMS;          // threads per workgroup (4 waves per channel half)
+    static constexpr int VITER = (NITEM + NT - 1) / NT;
+    static constexpr int VRS = NU * NTR * KCP;    // LDS stride of an input row
+    static constexpr int V_LDS = IR * VRS + NU * 64;  // per stage, + a dummy tail for items past NITEM
+    static constexpr int X_LDS = 4 * WMS * 16 * 64;  // epilogue: one pixel column, 16 registers x 64 lanes per wave
+    static constexpr int LDS = 2 * V_LDS > X_LDS ? 2 * V_LDS : X_LDS;  // floats
+    static_assert(NTR * RP == 32, "32 tiles per block");
+    static_assert(KC == 4 || KC == 8, "two or four channels per lane half");
+    static_assert(CH == 32 || CH == 64, "one or two channel halves");
+};
+
+// The wave's WW weight operands of chunk `ck` (w[H u + c]: position u, K slot
+// c), as WW / 4 16-byte loads per lane.
+template <class C>
+__device__ __forceinline__ void w42_load_w(float (&w)[C::WW], const LAMA_GLOBAL float *wb, int ck)
+{
+    const int lane = threadIdx.x & 63;
+    const LAMA_GLOBAL float *p = wb + (long)ck * C::WCH;
+#pragma unroll
+    for (int h = 0; h < C::WW / 4; ++h) {
+        const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(p + h * 256 + lane * 4);
+        w[4 * h] = v.x;
+        w[4 * h + 1] = v.y;
+        w[4 * h + 2] = v.z;
+        w[4 * h + 3] = v.w;
+    }
+}
+
+// MFMAs of one chunk for wave (wm, vy): for each x position u, lane half g
+// reads its H channels of staged rows ra and rb (one 8- or 16-byte read each,
+// a position ahead) and feeds ra + sb * rb -- row vy of B_y^T -- to H MFMAs
+// as K slot g; each 16-byte group of the weight registers is reloaded with
+// chunk `ckn` right after the last MFMA that reads it issues.
+template <class C>
+__device__ __forceinline__ void w42_compute_ld(f32x16 (&acc)[C::NU], float (&w)[C::WW], const float *vl,
+                                               const LAMA_GLOBAL float *wb, int ckn)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int vy = wave & 3, g = lane >> 5, j = lane & 31;
+    const int p = j / C::NTR, t = j % C::NTR;  // the MFMA column's row pair and tile within the block
+    // B_y^T rows (1, 0, -1, 0), (0, 1, 1, 0), (0, -1, 1, 0), (0, 1, 0, -1)
+    const int ra = 2 * p + (vy == 0 ? 0 : vy == 2 ? 2 : 1);
+    const int rb = 2 * p + (vy == 2 ? 1 : vy == 3 ? 3 : 2);
+    const float sb = vy == 1 ? 1.f : -1.f;
+    const float *va = vl + ra * C::VRS + t * C::KCP + C::H * g;
+    const float *vb = vl + rb * C::VRS + t * C::KCP + C::H * g;
+    const LAMA_GLOBAL float *pw = wb + (long)ckn * C::WCH;
+    float a[2][C::H], b[2][C::H];
+    auto rd = [&](int u, int buf) {
+        lds_vec<C::H>(a[buf], va + u * C::NTR * C::KCP);
+        lds_vec<C::H>(b[buf], vb + u * C::NTR * C::KCP);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int u = 0; u < C::NU; ++u) {
+        const int cur = u & 1;
+        if (u + 1 < C::NU) rd(u + 1, cur ^ 1);
+#pragma unroll
+        for (int c = 0; c < C::H; ++c)
+            acc[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[C::H * u + c], fmaf(sb, b[cur][c], a[cur][c]), acc[u], 0,
+                                                          0, 0);
+        if ((C::H * (u + 1)) % 4 == 0) {
+            const int h = C::H * (u + 1) / 4 - 1;
+            const float4 v = *reinterpret_cast<const LAMA_GLOBAL float4 *>(pw + h * 256 + lane * 4);
+            w[4 * h] = v.x;
+            w[4 * h + 1] = v.y;
+            w[4 * h + 2] = v.z;
+            w[4 * h + 3] = v.w;
+            // keep the load here: the scheduler would otherwise sink it below
+            // the chunk's last MFMA
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// One 64-channel x TR-row x TC-pixel block of problem P (s1 absent).
+template <class C>
+__device__ __forceinline__ void w42_tile(const ConvProblem &P, int b, float *lds, float *epl)
+{
+    // K slice of a split problem: the blocks of slice ks follow those of ks - 1
+    int ks = 0;
+    if (P.ksplit > 1) {
+        const int per = P.mblocks * P.tiles_x * P.tiles_y;
+        ks = b / per;
+        b -= ks * per;
+    }
+#if LAMA_W4_XCD
+    const int ntile = P.tiles_x * P.tiles_y, mb = b / ntile, tt = b - mb * ntile;
+#else
+    const int mb = b % P.mblocks, tt = b / P.mblocks;
+#endif
+    const int tx = tt % P.tiles_x, ty = tt / P.tiles_x;
+    const int m0 = mb * C::CH, oy0 = ty * C::TR, ox0 = tx * C::TC;
+    const float ep = epi_param_load(P, m0);
+    f32x16 acc[C::NU];
+#pragma unroll
+    for (int u = 0; u < C::NU; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+    ConvSeg sg = P.s0;  // held in registers across the barriers
+    if (P.ksplit > 1) {
+        const int c0 = ks * P.kchunks * C::KC;
+        sg.src += (long)c0 * sg.cs;
+        sg.wt += (long)ks * P.kchunks * C::WCH;
+        sg.C -= c0;
+        sg.nchunk = P.kchunks;
+    }
+    const int n = sg.nchunk, last = n - 1;
+    {
+        W4Slots<C> sl;
+        w4_slots<C>(sl, sg, oy0, ox0);
+        // the 64-row block's weights (64 rows of wrow floats), then wave
+        // (wm, vy)'s WW * 64 per chunk (a 32-channel block is half wm of its
+        // 64-row block)
+        const int wave = threadIdx.x >> 6 | (m0 & 32) >> 3;
+        const LAMA_GLOBAL float *wb = gp(sg.wt) + (long)(m0 >> 6) * 64 * sg.wrow + wave * (C::WW * 64);
+        float *l0 = lds, *l1 = lds + C::V_LDS;
+        float w0[C::WW], w1[C::WW];
+        W4Stage<C> r0, r1;
+        // weights one chunk ahead, inputs two; the prefetches past the last
+        // chunk re-read it (uniform control flow)
+        w42_load_w<C>(w0, wb, 0);
+        w4_load_d<C>(r0, sl, sg, 0);
+        w42_load_w<C>(w1, wb, min(1, last));
+        w4_load_d<C>(r1, sl, sg, min(1, last));
+        w4_store_v<C>(r0, sl, l0);
+        w4_load_d<C>(r0, sl, sg, min(2, last));
+        __syncthreads();
+        // n is even (the weights are packed in pairs of chunks): one loop exit
+        for (int ck = 0; ck < n; ck += 2) {
+            w42_compute_ld<C>(acc, w0, l0, wb, min(ck + 2, last));
+            w4_store_v<C>(r1, sl, l1);
+            w4_load_d<C>(r1, sl, sg, min(ck + 3, last));
+            __syncthreads();
+            w42_compute_ld<C>(acc, w1, l1, wb, min(ck + 3, last));
+            w4_store_v<C>(r0, sl, l0);
+            w4_load_d<C>(r0, sl, sg, min(ck + 4, last));
+            __syncthreads();
+        }
+    }
+    // epilogue: four rounds, one per pixel column o of the tiles (the staging
+    // buffers are free once every wave has left the K loop)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 2, vy = wave & 3, g = lane >> 5, j = lane & 31;
+    const int p = j / C::NTR, t = j % C::NTR;
+    const int oyp = oy0 + 2 * p, oxt = ox0 + 4 * t;
+    float *xl = lds;
+    if (threadIdx.x < 192) epl[threadIdx.x] = ep;
+    LAMA_GLOBAL float *out = gp(P.out) + (long)ks * P.out_kstride;
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        // column o of A_x^T: (1, 1, 1, 1, 1, 0), (0, 1, -1, 2, -2, 0),
+        // (0, 1, 1, 4, 4, 0), (0, 1, -1, 8, -8, 1)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float m0v = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r], m4 = acc[4][r],
+                        m5 = acc[5][r];
+            float v;
+            if (o == 0)
+                v = m0v + m1 + m2 + m3 + m4;
+            else if (o == 1)
+                v = m1 - m2 + 2.f * (m3 - m4);
+            else if (o == 2)
+                v = m1 + m2 + 4.f * (m3 + m4);
+            else
+                v = m1 - m2 + 8.f * (m3 - m4) + m5;
+            xl[((wm * 4 + vy) * 16 + r) * 64 + lane] = v;
+        }
+        __syncthreads();
+        const int ox = oxt + o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // register row r = 4 vy + i: output channel wm*32 + 8 vy + 4 g + i
+            const int r = 4 * vy + i, cl = wm * 32 + 8 * vy + 4 * g + i;
+            const float q0 = xl[((wm * 4 + 0) * 16 + r) * 64 + lane], q1 = xl[((wm * 4 + 1) * 16 + r) * 64 + lane],
+                        q2 = xl[((wm * 4 + 2) * 16 + r) * 64 + lane], q3 = xl[((wm * 4 + 3) * 16 + r) * 64 + lane];
+            if (m0 + cl >= P.M || ox >= P.OW) continue;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int oy = oyp + e;
+                if (oy >= P.OH) continue;
+                float x = e == 0 ? q0 + q1 + q2 : q1 - q2 - q3;
+                const long ofs = (long)(m0 + cl) * P.out_cstride + (long)oy * P.outW + ox;
+                if (P.bias) x += epl[cl];
+                for (int k = 0; k < P.naddend; ++k) x += gp(P.addend)[ofs + k * P.addend_kstride];
+                if (P.scale) x = x * epl[64 + cl] + epl[128 + cl];
+                if (P.relu) x = fmaxf(x, 0.f);
+                if (P.res) x += gp(P.res)[ofs];
+                out[ofs] = x;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+// The F(2x4, 3x3) kernel: blocks of LAMA_W42_CH output channels x 4 rows x
+// 64 pixels (16 tiles per row pair), four waves per 32 channels.
+#define LAMA_W42_KERNEL(NAME, NTR)                                                          \
+    extern "C" __global__ void __launch_bounds__(8 * LAMA_W42_CH) NAME(LAMA_CONV_PARAMS)  \
+    {                                                                                       \
+        LAMA_CONV_STARTS;                                                                   \
+        LAMA_STAMP_BEGIN;                                                                   \
+        using C = W42Cfg<NTR>;                                                              \
+        using C4 = W42Cfg<NTR, true>;                                                       \
+        static_assert(C4::LDS == C::LDS, "one LDS layout");                                \
+        __shared__ __attribute__((aligned(16))) float lds[C::LDS];                          \
+        __shared__ float epl[192];                                                          \
+        int b = w4_xcd_order(blockIdx.x, gridDim.x);                                        \
+        int pi = find_problem(ps, b);                                                       \
+        if (probs[pi].vec_in && (probs[pi].s0.IW & 3) == 0)                                  \
+            w42_tile<C4>(probs[pi], b, lds, epl);                                           \
+        else                                                                                \
+            w42_tile<C>(probs[pi], b, lds, epl);                                            \
+        LAMA_STAMP_END;                                                                     \
+    }
+LAMA_W42_KERNEL(lama_conv3x3w42, 16)
+#undef LAMA_W42_KERNEL

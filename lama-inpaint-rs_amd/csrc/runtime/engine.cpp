@@ -24,6 +24,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <thread>
 
 namespace lama {
 
@@ -115,7 +116,10 @@ int pw_kc(int v) { return v == 0 ? 2 * LAMA_PW_KC : LAMA_PW_KC; }
 
 void tile_shape(int family, int &tr, int &tc, int wino = 0, int w4v = 0)
 {
-    if ((family == F_CONV3 || family == F_CONV3G) && wino == 4) {  // lama_conv3x3w4 / w4n / w4q
+    if ((family == F_CONV3 || family == F_CONV3G) && wino == 42) {  // lama_conv3x3w42: 4 x 64
+        tr = 4;
+        tc = 64;
+    } else if ((family == F_CONV3 || family == F_CONV3G) && wino == 4) {  // lama_conv3x3w4 / w4n / w4q
         tr = 2 << w4v;                                              // 2 x 64, 4 x 32 or 8 x 16
         tc = 128 / tr;
     } else if ((family == F_CONV3 || family == F_CONV3G) && wino) {  // lama_conv3x3w: 2 rows x 64 px
@@ -273,6 +277,19 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
     return p;
 }
 
+// Runs f(r0, r1) over [0, n) split into contiguous ranges on up to 16
+// host threads (the Winograd weight transforms, one output channel row per
+// index: rows never share packed floats).
+template <class F>
+void parallel_rows(int n, F f)
+{
+    const int nt = std::max(1, std::min({16, n, (int)std::thread::hardware_concurrency()}));
+    std::vector<std::thread> th;
+    for (int t = 1; t < nt; ++t) th.emplace_back(f, (int)((long)n * t / nt), (int)((long)n * (t + 1) / nt));
+    f(0, (int)((long)n / nt));
+    for (std::thread &x : th) x.join();
+}
+
 // 3x3 weights for lama_conv3x3w4 / w4n / w4q, transformed by
 // U_u = sum over kx of G[u][kx] * w[ky][kx] with
 // G = (1/4, 0, 0; -1/6, -1/6, -1/6; -1/6, 1/6, -1/6; 1/24, 1/12, 1/6;
@@ -285,7 +302,8 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
 // u = 3 wu + q (with LAMA_W4_WX4, steps 2p and 2p + 1 of a wave interleaved
 // as [p][lane][step 2p + h][c], step 8 after them as [lane][c]).  A chunk is 64 x 72 floats (T * KC); the block stride is 64
 // rows of wrow = nchunk * 72.
-Packed pack_wino4(Arena &A, int M, int C, const std::function<float(int, int, int)> &get)
+template <class Get>
+Packed pack_wino4(Arena &A, int M, int C, const Get &get)
 {
     static const double G[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
                                    {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
@@ -299,30 +317,82 @@ Packed pack_wino4(Arena &A, int M, int C, const std::function<float(int, int, in
     p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
     p.wrow = p.nchunk * WK;
     const int mblocks = (M + 63) / 64;
-    p.off = A.add((size_t)mblocks * 64 * p.wrow);
+    p.off = A.add((size_t)mblocks * 64 * p.wrow);  // zero: rows past M, channels past C
     float *d = A.h.data() + p.off;
-    for (int mb = 0; mb < mblocks; ++mb)
-        for (int ck = 0; ck < p.nchunk; ++ck) {
-            float *blk = d + ((size_t)mb * p.nchunk + ck) * 64 * WK;
-            for (int wave = 0; wave < 4; ++wave)
-                for (int st = 0; st < 9; ++st)
-                    for (int lane = 0; lane < 64; ++lane)
-                        for (int c = 0; c < 2; ++c) {
-                            const int wm = wave >> 1, wu = wave & 1, g = lane >> 5, j = lane & 31;
-                            const int co = mb * 64 + wm * 32 + j, ci = ck * KC + 2 * g + c;
-                            const int ky = st / 3, u = 3 * wu + st % 3;
-                            double v = 0;
-                            if (co < M && ci < C)
-                                for (int kx = 0; kx < 3; ++kx) v += G[u][kx] * (double)get(co, ci, ky * 3 + kx);
-                            // LAMA_W4_WX4: steps 2q, 2q + 1 interleaved per lane (one 16-byte
-                            // load), step 8 after them
-                            const size_t at = LAMA_W4_WX4 ? (size_t)wave * 9 * 128 +
-                                                                (st < 8 ? (st / 2) * 256 + lane * 4 + (st % 2) * 2
-                                                                        : 1024 + lane * 2)
-                                                          : ((size_t)(wave * 9 + st) * 64 + lane) * 2;
-                            blk[at + c] = (float)v;
-                        }
+    parallel_rows(M, [&](int r0, int r1) {
+        for (int co = r0; co < r1; ++co) {
+            const int mb = co / 64, wm = co % 64 / 32, j = co % 32;
+            for (int ci = 0; ci < C; ++ci) {
+                double g[9];
+                for (int k = 0; k < 9; ++k) g[k] = (double)get(co, ci, k);
+                const int ck = ci / KC, lg = ci % KC / 2, c = ci % 2, lane = lg * 32 + j;
+                float *blk = d + ((size_t)mb * p.nchunk + ck) * 64 * WK;
+                for (int u = 0; u < 6; ++u)
+                    for (int ky = 0; ky < 3; ++ky) {
+                        const double v = G[u][0] * g[ky * 3] + G[u][1] * g[ky * 3 + 1] + G[u][2] * g[ky * 3 + 2];
+                        const int wave = wm * 2 + u / 3, st = ky * 3 + u % 3;
+                        // LAMA_W4_WX4: steps 2q, 2q + 1 interleaved per lane (one 16-byte
+                        // load), step 8 after them
+                        const size_t at = LAMA_W4_WX4 ? (size_t)wave * 9 * 128 +
+                                                            (st < 8 ? (st / 2) * 256 + lane * 4 + (st % 2) * 2
+                                                                    : 1024 + lane * 2)
+                                                      : ((size_t)(wave * 9 + st) * 64 + lane) * 2;
+                        blk[at + c] = (float)v;
+                    }
+            }
         }
+    });
+    return p;
+}
+
+// 3x3 weights for lama_conv3x3w42 (Winograd F(2x4, 3x3)): U(vy, u) =
+// sum over (ky, kx) of Gy[vy][ky] Gx[u][kx] w[ky][kx], Gx the F(4,3) transform
+// of pack_wino4 and Gy = (1, 0, 0; 1/2, 1/2, 1/2; 1/2, -1/2, 1/2; 0, 0, 1) the
+// F(2,3) one, evaluated in f64 and rounded once to f32, in the order the
+// kernel's waves load them: per block of 64 output channels (rows past M
+// zero) and chunk of KC = LAMA_W42_KC input channels (H = KC / 2 per lane
+// half), [wave (wm, vy)][group h][lane (g, j)][k] holds U(vy, u) for output
+// channel 32 wm + j and input channel H g + c of the chunk, with
+// H u + c = 4 h + k.  A chunk is 64 x 24 KC floats; the block stride is 64
+// rows of wrow = nchunk * 24 KC.
+template <class Get>
+Packed pack_wino42(Arena &A, int M, int C, const Get &get)
+{
+    static const double Gx[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+                                    {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
+    static const double Gy[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    constexpr int KC = LAMA_W42_KC, H = KC / 2, WK = 24 * KC, WW = 6 * H;
+    static_assert(KC == 4 || KC == 8, "two or four channels per lane half");
+    Packed p;
+    p.M = M;
+    p.C = C;
+    p.KC = KC;
+    p.T = 64 * WK / KC;  // chunk stride T * KC = one 64-row block's chunk
+    p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
+    p.wrow = p.nchunk * WK;
+    const int mblocks = (M + 63) / 64;
+    p.off = A.add((size_t)mblocks * 64 * p.wrow);  // zero: rows past M, channels past C
+    float *d = A.h.data() + p.off;
+    parallel_rows(M, [&](int r0, int r1) {
+        for (int co = r0; co < r1; ++co) {
+            const int mb = co / 64, wm = co % 64 / 32, j = co % 32;
+            for (int ci = 0; ci < C; ++ci) {
+                double g[3][3], t[4][3];
+                for (int k = 0; k < 9; ++k) g[k / 3][k % 3] = (double)get(co, ci, k);
+                for (int vy = 0; vy < 4; ++vy)  // G_y g
+                    for (int kx = 0; kx < 3; ++kx)
+                        t[vy][kx] = Gy[vy][0] * g[0][kx] + Gy[vy][1] * g[1][kx] + Gy[vy][2] * g[2][kx];
+                const int ck = ci / KC, lg = ci % KC / H, c = ci % KC % H;
+                float *blk = d + ((size_t)mb * p.nchunk + ck) * 64 * WK;
+                for (int vy = 0; vy < 4; ++vy)
+                    for (int u = 0; u < 6; ++u) {  // (G_y g) G_x^T
+                        const double v = Gx[u][0] * t[vy][0] + Gx[u][1] * t[vy][1] + Gx[u][2] * t[vy][2];
+                        const int idx = H * u + c, wave = wm * 4 + vy, lane = lg * 32 + j;
+                        blk[(size_t)wave * WW * 64 + (idx / 4) * 256 + lane * 4 + idx % 4] = (float)v;
+                    }
+            }
+        }
+    });
     return p;
 }
 
@@ -489,7 +559,7 @@ bool Engine::open(std::string &err)
     if (!get_fn(fn_wino_, "lama_conv3x3w", err) ||
         !get_fn(fn_wino4_[0], "lama_conv3x3w4", err) ||
         !get_fn(fn_wino4_[1], "lama_conv3x3w4n", err) ||
-        !get_fn(fn_wino4_[2], "lama_conv3x3w4q", err) ||
+        !get_fn(fn_wino4_[2], "lama_conv3x3w4q", err) || !get_fn(fn_wino42_, "lama_conv3x3w42", err) ||
 
         !get_fn(fn_tail_u8_, "lama_tail_u8", err) ||
         !get_fn(fn_finalize_ks_[0], "lama_finalize10", err) ||
@@ -506,8 +576,10 @@ bool Engine::open(std::string &err)
     fn_build_in_ = fn_[F_INPUT];
     if (const char *wv = getenv("LAMA_FFC_WINO")) {
         const int v = atoi(wv);
-        wino_ = v == 0 ? 0 : v == 4 ? 4 : 2;
+        wino_ = v == 0 ? 0 : v == 4 ? 4 : v == 42 ? 42 : 2;
+        w42_packed_ = false;  // a forced algorithm runs on every plane
     }
+    if (const char *t = getenv("LAMA_W42")) w42_packed_ = w42_packed_ && atoi(t) != 0;
     if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
@@ -602,11 +674,19 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
                 return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
             };
             auto l2gw = [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; };
-            F.local = wino_ == 4 ? pack_wino4(A, 128, 512, local)
-                      : wino_   ? pack_wino(A, 128, 512, local)
-                                : pack(A, 128, 512, 9, 8, local);
-            F.l2g = wino_ == 4 ? pack_wino4(A, 384, 128, l2gw) : wino_ ? pack_wino(A, 384, 128, l2gw)
-                                                                     : pack(A, 384, 128, 9, 8, l2gw);
+            // the F(2x4) packs beside the default F(4,3) ones, for the large planes
+            if (w42_packed_) {
+                F.local42 = pack_wino42(A, 128, 512, local);
+                F.l2g42 = pack_wino42(A, 384, 128, l2gw);
+            }
+            F.local = wino_ == 42  ? pack_wino42(A, 128, 512, local)
+                      : wino_ == 4 ? pack_wino4(A, 128, 512, local)
+                      : wino_      ? pack_wino(A, 128, 512, local)
+                                   : pack(A, 128, 512, 9, 8, local);
+            F.l2g = wino_ == 42  ? pack_wino42(A, 384, 128, l2gw)
+                    : wino_ == 4 ? pack_wino4(A, 384, 128, l2gw)
+                    : wino_      ? pack_wino(A, 384, 128, l2gw)
+                                 : pack(A, 384, 128, 9, 8, l2gw);
             // rows of C channels in order: each launch sets the chunk count of
             // its kernel (pw_kc)
             F.conv2 = pack(A, 384, 192, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
@@ -714,12 +794,14 @@ bool Engine::fft_len(int n, FftLen &L, std::vector<float> &tw, std::string &err)
 // block holding at most LAMA_FFT_SPLIT_LDS bytes of ping-pong buffers.
 // The kernel of a conv launch: the 1x1 families use float4 activation loads
 // only when every plane is 16-byte aligned and a multiple of 4 floats long.
-hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n) const
+hipFunction_t Engine::conv_fn(int family, const ConvProblem *probs, size_t n, int wino) const
 {
+    if (wino < 0) wino = wino_;
     // the head as one chunk and one M block: the kernel with register-resident weights
     if (family == F_CONV7 && head_r_ && n == 1 && probs[0].s0.nchunk == 1 && probs[0].mblocks == 1) return fn_head_r_;
-    if ((family == F_CONV3 || family == F_CONV3G) && wino_ == 4) return fn_wino4_[w4_variant(probs[0].OH, probs[0].OW)];
-    if ((family == F_CONV3 || family == F_CONV3G) && wino_) return fn_wino_;
+    if ((family == F_CONV3 || family == F_CONV3G) && wino == 42) return fn_wino42_;
+    if ((family == F_CONV3 || family == F_CONV3G) && wino == 4) return fn_wino4_[w4_variant(probs[0].OH, probs[0].OW)];
+    if ((family == F_CONV3 || family == F_CONV3G) && wino) return fn_wino_;
     if (family == F_CONVT && convt_rows_) return fn_convt_rows_[tile_variant(family, probs[0].OH, probs[0].OW)];
     if ((family == F_CONV3S2 || family == F_CONVT) && tile_variant(family, probs[0].OH, probs[0].OW) == 1)
         return fn_edge_q_[family == F_CONVT];
@@ -818,14 +900,33 @@ unsigned Engine::w4_lds_pad(int h8, int w8, int ks) const
 // 1, 2, 4 that keeps A and B within two workgroups per CU.
 int Engine::ksplit_for(int h, int w) const
 {
-    if (wino_ != 4) return 1;
+    const int wm = wino_for(h / 8, w / 8);
+    if (wm != 4 && wm != 42) return 1;
     if (ksplit_force_ == 1 || ksplit_force_ == 2 || ksplit_force_ == 4) return ksplit_force_;
     int tr, tc;
-    tile_shape(F_CONV3, tr, tc, 4, w4_variant(h / 8, w / 8));
+    tile_shape(F_CONV3, tr, tc, wm, w4_variant(h / 8, w / 8));
     const int tiles = ((w / 8 + tc - 1) / tc) * ((h / 8 + tr - 1) / tr);
+    // every slice an even number of chunks: the l2l and l2g ranges (128
+    // channels) and each of the g2l ranges (384 / LAMA_G2L_RANGES)
+    const int kc = wm == 42 ? LAMA_W42_KC : LAMA_WINO_KC;
+    auto even = [&](int s) { return (128 / kc) % (2 * s) == 0 && (384 / LAMA_G2L_RANGES / kc) % (2 * s) == 0; };
     int s = 1;
-    while (s < LAMA_KSPLIT_MAX && 16 * tiles * (2 * s) <= 2 * LAMA_CUS) s *= 2;
+    while (s < LAMA_KSPLIT_MAX && 16 * tiles * (2 * s) <= 2 * LAMA_CUS && even(2 * s)) s *= 2;
     return s;
+}
+
+// The FFC 3x3 algorithm of an h8 x w8 bottleneck plane: LAMA_FFC_WINO's,
+// except that the default F(4,3) hands the plane to F(2x4, 3x3) where the
+// l2l + l2g launch has at least two of its workgroups (64 channels x 4 rows
+// x 64 pixels) per CU: 1024 x 1024 inputs and up.  Measured (passes/s,
+// F(4,3) / F(2x4)): 2048x2048 21.3-21.6 / 22.3-22.5, 1024x1024 80.9-81.2 /
+// 84.1-84.6, 512x512 286.7 / 249.6 (128 workgroups); LAMA_W42=0 (read at
+// open) keeps F(4,3) everywhere.
+int Engine::wino_for(int h8, int w8) const
+{
+    if (wino_ != 4 || !w42_packed_) return wino_;
+    const long blocks = (long)((h8 + 3) / 4) * ((w8 + 63) / 64) * (512 / 64);
+    return blocks >= 2 * LAMA_CUS ? 42 : 4;
 }
 
 // Groups of 4 elements per finalize thread (1 or 2): two where one group per
@@ -1107,7 +1208,8 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
 
     ArenaLayout lay;
     const int ks = ksplit_for(H, W);
-    const unsigned w4_shmem = w4_lds_pad(H8, W8, ks);
+    const int wm = wino_for(H8, W8);  // the FFC 3x3 algorithm of this plane
+    const unsigned w4_shmem = wm == 4 ? w4_lds_pad(H8, W8, ks) : 0u;
     int pk1, pku;  // K split of the SpectralTransform conv1 and of the FourierUnit conv
     pw_ksplit_for(H, W, fg, pk1, pku);
     p.arena_bytes = arena_layout(H, W, fg, twr.size(), twc.size(), ks, pk1, pku, lay);
@@ -1162,10 +1264,12 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         q.OH = OH;
         q.OW = OW;
         int tr, tc;
-        tile_shape(family, tr, tc, wino_, tile_variant(family, OH, OW, M, s0.cs));
+        tile_shape(family, tr, tc, wm, tile_variant(family, OH, OW, M, s0.cs));
         q.tiles_x = (OW + tc - 1) / tc;
         q.tiles_y = (OH + tr - 1) / tr;
-        q.mblocks = (M + 63) / 64;
+        // output channels per block: 64, or the F(2x4) kernel's LAMA_W42_CH
+        const int mw = (family == F_CONV3 || family == F_CONV3G) && wm == 42 ? LAMA_W42_CH : 64;
+        q.mblocks = (M + mw - 1) / mw;
         q.nblocks = q.tiles_x * q.tiles_y * q.mblocks;
         if (family == F_CONV1 || family == F_CONV1R) {
             // the chunk count of the kernel's chunk size over the packed row
@@ -1187,7 +1291,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
                            int stream = S_MAIN, int wait_ev = -1, int record_ev = -1) {
         Launch L{};
         if (probs.size() == 1) pw_xcd_pad(family, probs[0]);
-        L.fn = conv_fn(family, probs.data(), probs.size());
+        L.fn = conv_fn(family, probs.data(), probs.size(), wm);
         L.family = family;
         L.stream = stream;
         L.wait_ev = wait_ev;
@@ -1203,14 +1307,15 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
             if (q.s0.cs < q.s0.IH * q.s0.IW || (q.s1.nchunk > 0 && q.s1.cs < q.s1.IH * q.s1.IW)) bad_problem = true;
             const int tx = pw && q.ksplit <= 1 && q.nblocks == pw_xcd_blocks(q) ? (q.tiles_x + 7) / 8 * 8 : q.tiles_x;
             if (q.nblocks != std::max(1, q.ksplit) * tx * q.tiles_y * q.mblocks ||
-                (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2] &&
+                (q.ksplit > 1 && L.fn != fn_wino4_[0] && L.fn != fn_wino4_[1] && L.fn != fn_wino4_[2] && L.fn != fn_wino42_ &&
                  family != F_CONV1))
                 bad_problem = true;
         }
         // the head kernels walk their tiles: three (register weights) or two
         // (weights in LDS) resident workgroups per CU
         L.grid = family == F_CONV7 ? std::min(nb, (L.fn == fn_head_r_ ? (unsigned)LAMA_HEAD_WGS : 2u) * LAMA_CUS) : nb;
-        L.shmem = (family == F_CONV3 || family == F_CONV3G) && wino_ == 4 ? w4_shmem : 0;
+        L.shmem = (family == F_CONV3 || family == F_CONV3G) && wm == 4 ? w4_shmem : 0;
+        L.block = L.fn == fn_wino42_ ? 8 * LAMA_W42_CH : 0;  // the F(2x4) kernel's 4 waves per 32 channels
         L.arg = put(probs.data(), probs.size() * sizeof(ConvProblem));
         L.ps = prob_starts(probs.data(), probs.size());
         if (probs.size() > LAMA_MAX_PROBS) bad_problem = true;
@@ -1327,9 +1432,10 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
     auto part = [&](int k, int q) {
         const FfcW &Fw = ffc_[k];
         constexpr int RC = 384 / LAMA_G2L_RANGES;  // channels per g2l K range
-        static_assert(RC % 8 == 0 && RC % (2 * LAMA_WINO_KC) == 0, "whole K chunks (Winograd: chunk pairs) per range");
+        static_assert(RC % 8 == 0 && RC % (2 * LAMA_WINO_KC) == 0 && RC % (2 * LAMA_W42_KC) == 0,
+                      "whole K chunks (Winograd: chunk pairs) per range");
         const int c0 = q == 0 ? 0 : 128 + RC * (q - 1), nch = q == 0 ? 128 : RC;
-        const Packed &pk = Fw.local;
+        const Packed &pk = wm == 42 && wino_ != 42 ? Fw.local42 : Fw.local;
         ConvSeg sq = seg(ffc_src(k) + (size_t)c0 * P8s, pk, nch, H8, W8, P8s);
         sq.wt = wp(pk.off) + (size_t)(c0 / pk.KC) * pk.T * pk.KC;  // chunk c0/KC of the packed rows
         sq.nchunk = nch / pk.KC;
@@ -1339,11 +1445,12 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         const FfcW &Fw = ffc_[k];
         std::vector<ConvProblem> probs{
             kslices(part(k, 0), ks, (long)128 * P8s),
-            kslices(raw(problem(F_CONV3, seg(ffc_src(k), Fw.l2g, 128, H8, W8, P8s), 384, H8, W8, 0, 0, gc_buf(k), P8s,
+            kslices(raw(problem(F_CONV3, seg(ffc_src(k), wm == 42 && wino_ != 42 ? Fw.l2g42 : Fw.l2g, 128, H8, W8, P8s),
+                                384, H8, W8, 0, 0, gc_buf(k), P8s,
                                 W8, nullptr)),
                     ks, (long)384 * P8s)};
         // 16-byte input loads where the plane width allows (B: LAMA_W4_VEC_B)
-        for (ConvProblem &q : probs) q.vec_in = wino_ == 4 && W8 % 4 == 0;
+        for (ConvProblem &q : probs) q.vec_in = (wm == 4 || wm == 42) && W8 % 4 == 0;
         conv_launch(F_CONV3, probs, -1, 2.0 * P8 * (128.0 * 128 * 9 + 384.0 * 128 * 9),
                     f4 * (128 * P8 + 128 * P8 + 384 * P8 + 128 * 128 * 9 + 384 * 128 * 9), S_MAIN, -1,
                     k % 2 ? EV_A1 : EV_A0);
@@ -1356,7 +1463,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         if (ks > 1) {
             // split: the g2l ranges as the K slices of one problem (F(4,3) kernels)
             const FfcW &Fw = ffc_[k];
-            const Packed &pk = Fw.local;
+            const Packed &pk = wm == 42 && wino_ != 42 ? Fw.local42 : Fw.local;
             ConvSeg sq = seg(ffc_src(k) + (size_t)128 * P8s, pk, 384, H8, W8, P8s);
             sq.wt = wp(pk.off) + (size_t)(128 / pk.KC) * pk.T * pk.KC;
             sq.nchunk = 384 / pk.KC;
@@ -1369,7 +1476,7 @@ bool Engine::build_plan(Plan &p, void *arena, std::string &err)
         // records EV_B for finalize(k); else in the main stream's order
         const int xg = k == 0 ? EV_FORK : ((k - 1) % 2 ? EV_S1 : EV_S0);
         if (LAMA_W4_VEC_B)
-            for (ConvProblem &q : probs) q.vec_in = wino_ == 4 && W8 % 4 == 0;
+            for (ConvProblem &q : probs) q.vec_in = (wm == 4 || wm == 42) && W8 % 4 == 0;
         conv_launch(F_CONV3G, probs, -1, 2.0 * P8 * (128.0 * 384 * 9),
                     f4 * (384 * P8 + LAMA_G2L_RANGES * 128 * P8 + 128 * 384 * 9),
                     b_stream ? S_G2L : S_MAIN, b_stream || k > 0 ? xg : -1, b_stream ? (k % 2 ? EV_B1 : EV_B0) : -1);
@@ -2460,7 +2567,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     const int pad = k / 2;
     const int oh = (h + 2 * pad - k) / stride + 1, ow = (w + 2 * pad - k) / stride + 1;
     const int wino = family == F_CONV3 ? wino_ : 0;
-    const int KC = family == F_CONV1 ? pw_kc(tile_variant(F_CONV1, 1, h * w, cout)) : family == F_CONV7 ? 4 : wino ? LAMA_WINO_KC : family == F_CONV3S2 ? LAMA_S2_KC : 8;
+    const int KC = family == F_CONV1 ? pw_kc(tile_variant(F_CONV1, 1, h * w, cout)) : family == F_CONV7 ? 4 : wino == 42 ? LAMA_W42_KC : wino ? LAMA_WINO_KC : family == F_CONV3S2 ? LAMA_S2_KC : 8;
     if ((size_t)4 * KC * h * w >= ((size_t)1 << 32)) {  // 32-bit staging offsets within a K chunk
         err = "op_conv2d: plane too large";
         return false;
@@ -2468,7 +2575,8 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     Arena A;
     const int T = k * k;
     auto getw = [&](int co, int ci, int t) { return wt[((size_t)co * cin + ci) * T + t]; };
-    Packed pk = wino == 4 ? pack_wino4(A, cout, cin, getw)
+    Packed pk = wino == 42 ? pack_wino42(A, cout, cin, getw)
+                : wino == 4 ? pack_wino4(A, cout, cin, getw)
                 : wino    ? pack_wino(A, cout, cin, getw)
                           : pack(A, cout, cin, T, KC, getw);
     size_t bn = A.add(2 * (size_t)cout);
@@ -2498,7 +2606,8 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     tile_shape(family, tr, tc, wino, tile_variant(family, q.OH, q.OW, q.M, q.s0.cs));
     q.tiles_x = (q.OW + tc - 1) / tc;
     q.tiles_y = (q.OH + tr - 1) / tr;
-    q.mblocks = (cout + 63) / 64;
+    const int mw = wino == 42 ? LAMA_W42_CH : 64;  // output channels per block
+    q.mblocks = (cout + mw - 1) / mw;
     q.nblocks = q.tiles_x * q.tiles_y * q.mblocks;
     q.bias = bias ? dw + bo : nullptr;
     q.scale = scale ? dw + bn : nullptr;
@@ -2508,7 +2617,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     q.out_cstride = (long)oh * ow;
     q.outW = q.OW;
     q.oy_mul = q.ox_mul = 1;
-    q.vec_in = wino == 4 && family == F_CONV3 && w % 4 == 0;  // both F(4,3) load paths, by width
+    q.vec_in = (wino == 4 || wino == 42) && family == F_CONV3 && w % 4 == 0;  // both Winograd load paths, by width
     pw_xcd_pad(family, q);
     UPLOAD(dq, nullptr, (sizeof q + 3) / 4);
     if (!check(hip_->hipMemcpy(dq, &q, sizeof q, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
@@ -2516,6 +2625,7 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
     L.fn = conv_fn(family, &q, 1);
     L.family = family;
     L.grid = (unsigned)q.nblocks;
+    L.block = L.fn == fn_wino42_ ? 8 * LAMA_W42_CH : 0;
     L.arg = dq;
     L.ps = prob_starts(&q, 1);
     L.nparams = 2;

@@ -185,6 +185,7 @@ public:
 private:
     struct FfcW {
         Packed local, l2g, conv2, conv1, fu;
+        Packed local42, l2g42;  // F(2x4, 3x3) packs for the large planes (when w42_packed_)
         size_t bn1, fu_bn, bn_l, bn_g;  // folded: scale at off, shift at off + n
     };
     struct UpW {
@@ -230,8 +231,12 @@ private:
     // at open, since the weights are packed for one or the other
     // LAMA_FFC_WINO: 0 direct; 2 F(2,3) (lama_conv3x3w); 4 (default) F(4,3)
     // in blocks of 2 x 64, 4 x 32 or 8 x 16 output pixels (lama_conv3x3w4,
-    // w4n, w4q), chosen per plane shape
+    // w4n, w4q), chosen per plane shape; 42 F(2x4, 3x3) in blocks of 4 x 64
+    // (lama_conv3x3w42)
     int wino_ = 4;
+    // the default mode also packs F(2x4, 3x3) weights and takes that kernel
+    // on large planes (wino_for); LAMA_W42=0 (read at open) keeps F(4,3)
+    bool w42_packed_ = true;
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
     int tile_variant(int family, int OH, int OW, int M = 0, long cs = 0) const;
@@ -250,7 +255,10 @@ private:
     // would leave CUs idle)
     int ksplit_for(int h, int w) const;
     hipFunction_t fn_wino_ = nullptr, fn_wino4_[3] = {};
-    hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n) const;
+    hipFunction_t fn_wino42_ = nullptr;  // lama_conv3x3w42 (LAMA_FFC_WINO=42)
+    // wino < 0: the engine's LAMA_FFC_WINO mode
+    hipFunction_t conv_fn(int family, const ConvProblem *probs, size_t n, int wino = -1) const;
+    int wino_for(int h8, int w8) const;
     size_t max_lds_ = 64 * 1024;  // bytes of LDS one block may use on this device
     hipStream_t stream_ = nullptr, side_ = nullptr, g2l_ = nullptr;
     hipEvent_t ev_[EV_COUNT] = {};

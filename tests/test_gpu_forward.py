@@ -348,11 +348,12 @@ def test_forward_tiny_bottleneck_planes(pkg, engine, oracle_cal, h, w):
     assert rel_err(got, ref) < STEP_TOL
 
 
-@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16")],
-                ids=["f23", "f43w64", "f43w32", "f43w16"])
+@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16"), ("42", "")],
+                ids=["f23", "f43w64", "f43w32", "f43w16", "f2x4"])
 def w4_forward_engine(pkg, weights_dir, request):
-    """The forward with each Winograd kernel forced: F(2,3) (LAMA_FFC_WINO=2)
-    and F(4,3) in 64-, 32- or 16-pixel blocks (LAMA_W4_TILE)."""
+    """The forward with each Winograd kernel forced: F(2,3) (LAMA_FFC_WINO=2),
+    F(4,3) in 64-, 32- or 16-pixel blocks (LAMA_W4_TILE) and F(2x4, 3x3)
+    (LAMA_FFC_WINO=42)."""
     with pytest.MonkeyPatch.context() as mp:
         mp.setenv("LAMA_FFC_WINO", request.param[0])
         mp.setenv("LAMA_W4_TILE", request.param[1])
@@ -446,13 +447,16 @@ def test_forward_ksplit_variants_256(pkg, engine, oracle_cal, monkeypatch, ks):
                                             (600, 600, "lama_conv3x3w4q", "lama_rfft2_75"),
                                             (600, 592, "lama_conv3x3w4q", "lama_rfft2"),
                                             (256, 256, "lama_conv3x3w4n", "lama_rfft2_32"),
-                                            (16, 1024, "lama_conv3x3w4", "lama_rfft2")])
+                                            (16, 1024, "lama_conv3x3w4", "lama_rfft2"),
+                                            (1024, 1024, "lama_conv3x3w42", "lama_rfft2_rows_128")])
 def test_ffc_block_shape_per_plane(pkg, engine, h, w, kernel, fft):
     """The FFC GEMMs take the F(4,3) block shape that covers the bottleneck
     plane with the fewest blocks of 32 tiles (2 x 64 px on a tie): 75-rows
     planes 10 x 5 blocks of 8 x 16 instead of 19 x 3 of 4 x 32; a plane of 2
-    rows and 128 columns 2 blocks of 2 x 64 instead of 4 of 4 x 32.  Square
-    32, 64 and 75 planes take the FFT kernels with the shape compiled in."""
+    rows and 128 columns 2 blocks of 2 x 64 instead of 4 of 4 x 32.  From
+    128 x 128 bottleneck planes (1024 x 1024 inputs) on they run as F(2x4,
+    3x3).  Square 32, 64 and 75 planes take the FFT kernels with the shape
+    compiled in."""
     print(f"case block shape {h}x{w}", flush=True)
     x = np.zeros((4, h, w), np.float32)
     engine.forward(x)

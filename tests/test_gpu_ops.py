@@ -251,12 +251,13 @@ def test_conv3x3_direct(direct_engine, cin, cout, h, w):
     assert rel_err(got, ref) < TOL
 
 
-@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16")],
-                ids=["f23", "f43w64", "f43w32", "f43w16"])
+@pytest.fixture(scope="module", params=[("2", ""), ("4", "64"), ("4", "32"), ("4", "16"), ("42", "")],
+                ids=["f23", "f43w64", "f43w32", "f43w16", "f2x4"])
 def w4_engine(pkg, request):
-    """Each Winograd kernel: F(2,3) (LAMA_FFC_WINO=2, lama_conv3x3w) and F(4,3)
-    (LAMA_FFC_WINO=4) with 64-, 32- or 16-pixel blocks (LAMA_W4_TILE); both are
-    read when the context opens."""
+    """Each Winograd kernel: F(2,3) (LAMA_FFC_WINO=2, lama_conv3x3w), F(4,3)
+    (LAMA_FFC_WINO=4) with 64-, 32- or 16-pixel blocks (LAMA_W4_TILE) and
+    F(2x4, 3x3) (LAMA_FFC_WINO=42, lama_conv3x3w42); both are read when the
+    context opens."""
     with pytest.MonkeyPatch.context() as mp:
         mp.setenv("LAMA_FFC_WINO", request.param[0])
         mp.setenv("LAMA_W4_TILE", request.param[1])
@@ -279,10 +280,10 @@ W4_CASES = WINO_CASES + [
 
 @pytest.mark.parametrize("cin,cout,h,w", W4_CASES)
 def test_conv3x3_winograd_f43(w4_engine, cin, cout, h, w):
-    """The FFC 3x3 convolution as Winograd F(2,3) (lama_conv3x3w) and F(4,3)
-    along x (lama_conv3x3w4 / w4n / w4q) against the oracle's direct sum, the same
-    1e-5 relative bound: F(4,3)'s larger transform constants round a little
-    more than F(2,3)'s."""
+    """The FFC 3x3 convolution as Winograd F(2,3) (lama_conv3x3w), F(4,3)
+    along x (lama_conv3x3w4 / w4n / w4q) and F(2x4, 3x3) (lama_conv3x3w42)
+    against the oracle's direct sum, the same 1e-5 relative bound: F(4,3)'s
+    larger transform constants round a little more than F(2,3)'s."""
     rng = np.random.default_rng(cin * 100 + cout + w)
     x = rng.standard_normal((cin, h, w), np.float32)
     wt = (rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32)
