@@ -7,8 +7,9 @@ blurred-noise image with a ~25% brush-stroke mask.  A "step" is one forward
 pass; the input tensor is resident in HBM before the timed region starts.
 
 Prints one JSON line: passes/s, the roofline of the dominant kernel (the FFC
-3x3 convolutions as Winograd F(4,3) along x: the FLOPs of that algorithm's
-MFMA products per launch / mean launch time on the device clock, against the
+3x3 convolutions as Winograd F(4,3) along x, F(2x4, 3x3) on the bottleneck
+planes of 1024x1024 inputs and up: the FLOPs of that algorithm's MFMA
+products per launch / mean launch time on the device clock, against the
 157.3 TFLOP/s FP32 MFMA peak; the direct-convolution equivalent rate beside
 it), the host enqueue time of one pass, and the CPU baseline (the C
 restatement of the reference CPU engine, timed on this host's cores: median
@@ -92,18 +93,19 @@ def main():
     # both launches of each FFC: A = l2l + l2g (family conv3x3) and B = g2l
     # (family conv3x3g2l), one kernel
     dom_fams = ["conv3x3", "conv3x3g2l"]
-    # the FFC 3x3 convolutions run as Winograd F(4,3) along x (LAMA_FFC_WINO=2:
-    # F(2,3); 0: the direct implicit GEMM).  The engine counts each launch's
-    # direct-convolution FLOPs, 2 Cin Cout 9 H W; the algorithm's own MFMA
-    # products are the fraction `issued` of that: F(4,3) multiplies 6
-    # transformed positions x 3 kernel rows per 4 output pixels (18 of the
-    # direct 36 products, 1/2), F(2,3) 4 x 3 per 2 (12 of 18, 2/3), F(2x4, 3x3)
-    # (LAMA_FFC_WINO=42) 4 x 6 positions per 2 x 4 pixels (24 of 72, 1/3)
-    wv = os.environ.get("LAMA_FFC_WINO", "4")
-    wino = 0 if wv == "0" else 2 if wv == "2" else 42 if wv == "42" else 4
-    # the plan's own kernel for the FFC GEMMs at this size (the F(4,3) block
-    # shape is chosen per plane: 2 x 64, 4 x 32 or 8 x 16 output pixels)
+    # the FFC 3x3 convolutions run as Winograd F(4,3) along x, or F(2x4, 3x3)
+    # on bottleneck planes of 128 x 128 and up (LAMA_FFC_WINO=2: F(2,3); 0:
+    # the direct implicit GEMM; 4 / 42 force one Winograd form everywhere).
+    # The engine counts each launch's direct-convolution FLOPs, 2 Cin Cout 9 H
+    # W; the algorithm's own MFMA products are the fraction `issued` of that:
+    # F(4,3) multiplies 6 transformed positions x 3 kernel rows per 4 output
+    # pixels (18 of the direct 36 products, 1/2), F(2,3) 4 x 3 per 2 (12 of
+    # 18, 2/3), F(2x4, 3x3) 4 x 6 positions per 2 x 4 pixels (24 of 72, 1/3).
+    # The plan's own kernel for the FFC GEMMs at this size names the
+    # algorithm (and the F(4,3) block shape, chosen per plane: 2 x 64, 4 x 32
+    # or 8 x 16 output pixels).
     dom_kernel = eng.kernel_name(S, S, "conv3x3")
+    wino = {"lama_conv3x3": 0, "lama_conv3x3w": 2, "lama_conv3x3w42": 42}.get(dom_kernel, 4)
     issued = {0: 1.0, 2: 2.0 / 3.0, 4: 0.5, 42: 1.0 / 3.0}[wino]
     block = {"lama_conv3x3": "64 px", "lama_conv3x3w": "2 rows x 64 px", "lama_conv3x3w4": "2 rows x 64 px",
              "lama_conv3x3w4n": "4 rows x 32 px", "lama_conv3x3w4q": "8 rows x 16 px",
@@ -206,7 +208,7 @@ def main():
         launch_ms = launch_ms_events_a
         flops_launch = dA["flops"] / max(1, dA["launches"])
         clock_a = clock_b = None
-    # the F(4,3) algorithm's FLOPs (its MFMA products) per launch, and the
+    # the Winograd algorithm's FLOPs (its MFMA products) per launch, and the
     # direct-convolution count the same launch replaces
     exec_launch = flops_launch * issued
     achieved = exec_launch / (launch_ms * 1e-3) / 1e12
@@ -223,7 +225,8 @@ def main():
     conv_fams = ["conv7x7", "conv3x3s2", "conv3x3", "conv3x3g2l", "conv1x1", "convt", "conv1x1res"]
     conv_flops = sum(fam[f]["flops"] for f in conv_fams) / 3
     # executed MFMA work: the Winograd FFC families at the fraction `issued`
-    # of their direct-convolution FLOPs (1/2 for F(4,3), 2/3 for F(2,3))
+    # of their direct-convolution FLOPs (1/2 for F(4,3), 2/3 for F(2,3), 1/3
+    # for F(2x4, 3x3))
     wino_fams = ("conv3x3", "conv3x3g2l")
     conv_flops_exec = conv_flops - sum(fam[f]["flops"] for f in wino_fams) / 3 * (1.0 - issued)
     fft_ms = sum(fam[f]["ms"] for f in ("rfft2", "irfft2")) / 3
