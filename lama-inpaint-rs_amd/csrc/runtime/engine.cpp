@@ -918,7 +918,8 @@ int Engine::ksplit_for(int h, int w) const
 // The FFC 3x3 algorithm of an h8 x w8 bottleneck plane: LAMA_FFC_WINO's,
 // except that the default F(4,3) hands the plane to F(2x4, 3x3) where the
 // l2l + l2g launch has at least two of its workgroups (64 channels x 4 rows
-// x 64 pixels) per CU: 1024 x 1024 inputs and up.  Measured (passes/s,
+// x 64 pixels) per CU and its 64-pixel columns overhang the plane by at most
+// an eighth of its width: 1024 x 1024 inputs and up.  Measured (passes/s,
 // F(4,3) / F(2x4)): 2048x2048 21.3-21.6 / 22.3-22.5, 1024x1024 80.9-81.2 /
 // 84.1-84.6, 512x512 286.7 / 249.6 (128 workgroups); LAMA_W42=0 (read at
 // open) keeps F(4,3) everywhere.
@@ -926,7 +927,8 @@ int Engine::wino_for(int h8, int w8) const
 {
     if (wino_ != 4 || !w42_packed_) return wino_;
     const long blocks = (long)((h8 + 3) / 4) * ((w8 + 63) / 64) * (512 / 64);
-    return blocks >= 2 * LAMA_CUS ? 42 : 4;
+    const int overhang = (w8 + 63) / 64 * 64 - w8;
+    return blocks >= 2 * LAMA_CUS && 8 * overhang <= w8 ? 42 : 4;
 }
 
 // Groups of 4 elements per finalize thread (1 or 2): two where one group per
