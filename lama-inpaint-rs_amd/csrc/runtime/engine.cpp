@@ -24,6 +24,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <system_error>
 #include <thread>
 
 namespace lama {
@@ -279,14 +280,21 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
 
 // Runs f(r0, r1) over [0, n) split into contiguous ranges on up to 16
 // host threads (the Winograd weight transforms, one output channel row per
-// index: rows never share packed floats).
+// index: rows never share packed floats).  A range whose thread cannot be
+// started runs on the calling thread (no exception leaves the C ABI).
 template <class F>
 void parallel_rows(int n, F f)
 {
     const int nt = std::max(1, std::min({16, n, (int)std::thread::hardware_concurrency()}));
+    auto lo = [&](int t) { return (int)((long)n * t / nt); };
     std::vector<std::thread> th;
-    for (int t = 1; t < nt; ++t) th.emplace_back(f, (int)((long)n * t / nt), (int)((long)n * (t + 1) / nt));
-    f(0, (int)((long)n / nt));
+    int t = 1;
+    try {
+        for (; t < nt; ++t) th.emplace_back(f, lo(t), lo(t + 1));
+    } catch (const std::system_error &) {
+        f(lo(t), lo(nt));  // the ranges no thread took
+    }
+    f(0, lo(1));
     for (std::thread &x : th) x.join();
 }
 
