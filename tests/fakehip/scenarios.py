@@ -29,7 +29,7 @@ def run_plans():
     eng = E.Engine()
     eng.load_weights(H.Store(weights))
     shapes = [(64, 64), (128, 96), (256, 256), (512, 512), (600, 600), (600, 592), (1024, 1024), (16, 1024),
-              (8, 8), (64, 1024)]
+              (8, 8), (64, 1024), (1024, 1088)]
     res = {}
     for h, w in shapes:
         before = fake.fakehip_launches(None)

@@ -58,8 +58,11 @@ def test_every_shape_plans_and_issues_its_launches(fake_lib, weights_file):
     assert p["600x600"]["conv3x3"] == "lama_conv3x3w4q"
     assert p["600x592"]["conv3x3"] == "lama_conv3x3w4q"
     assert p["16x1024"]["conv3x3"] == "lama_conv3x3w4"
-    # 1024x1024 and up: Winograd F(2x4, 3x3) (at least two of its blocks per CU)
+    # 1024x1024 and up: Winograd F(2x4, 3x3) (at least two of its blocks per CU),
+    # unless its 64-pixel columns overhang the plane by more than an eighth
+    # (136 columns in three blocks of 64: F(4,3), in its 8 x 16 blocks there)
     assert p["1024x1024"]["conv3x3"] == "lama_conv3x3w42"
+    assert p["1024x1088"]["conv3x3"] == "lama_conv3x3w4q"
     # transforms with the plane shape compiled in, runtime-shaped, split
     assert p["256x256"]["rfft2"] == "lama_rfft2_32" and p["256x256"]["irfft2"] == "lama_irfft2_32"
     assert p["512x512"]["rfft2"] == "lama_rfft2_64"
