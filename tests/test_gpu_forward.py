@@ -394,6 +394,33 @@ def test_forward_winograd_f43_matches_f23_512(pkg, w4_forward_engine, engine):
     assert rel_err(a, b) < 1e-4
 
 
+def test_forward_f2x4_matches_f43_1536(pkg, weights_dir, engine):
+    """At 1536 x 1536 the bottleneck planes are 192 wide, three of the
+    F(2x4, 3x3) kernel's 64-pixel block columns: the default forward, which
+    takes that kernel there, within float rounding of the F(4,3) one
+    (LAMA_W42=0), with the composite within 1/255."""
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_W42", "0")
+        e43 = pkg.hip_engine.Engine()
+    try:
+        e43.load_weights(pkg.host_api.Store(weights_dir["cal"]))
+        img, mask = _case(pkg, 1536, 1536, "strokes")
+        x = pkg.host_api.build_input(img, mask)
+        print("case f2x4 vs f43 1536x1536", flush=True)
+        a = engine.forward(x)
+        assert engine.kernel_name(1536, 1536, "conv3x3") == "lama_conv3x3w42"
+        b = e43.forward(x)
+        assert e43.kernel_name(1536, 1536, "conv3x3").startswith("lama_conv3x3w4")
+        assert e43.kernel_name(1536, 1536, "conv3x3") != "lama_conv3x3w42"
+        assert rel_err(a, b) < 1e-4
+        ua = pkg.host_api.composite(img, mask, a, 0, 0)
+        ub = pkg.host_api.composite(img, mask, b, 0, 0)
+        d = np.abs(ua.astype(int) - ub.astype(int))
+        assert d.max() <= 1, d.max()
+    finally:
+        e43.close()
+
+
 def test_timeline_records_every_launch(pkg, engine):
     """lama_hip_timeline: one pass's 296 launches in issue order, each with a
     kernel-clock window; launches on one stream never overlap, and the
