@@ -296,7 +296,7 @@ def main():
                "pass_s_256": [round(v, 3) for v in cpu_ts256]}
 
     line = {
-        "metric": "512x512 inpaint passes/sec (FP32, batch 1)",
+        "metric": f"{S}x{S} inpaint passes/sec (FP32, batch 1)",
         "value": round(args.steps / elapsed, 3),
         "unit": "passes/s",
         "n_gpus": 1,
