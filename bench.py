@@ -11,12 +11,15 @@ Prints one JSON line: passes/s, the roofline of the dominant kernel (the FFC
 planes of 1024x1024 inputs and up: the FLOPs of that algorithm's MFMA
 products per launch / mean launch time on the device clock, against the
 157.3 TFLOP/s FP32 MFMA peak; the direct-convolution equivalent rate beside
-it), the host enqueue time of one pass, and the CPU baseline (the C
-restatement of the reference CPU engine, timed on this host's cores: median
-of three passes at 512x512 and at 256x256).
+it), the host enqueue time of one pass, the wall time of the lama-inpaint
+command on the reference's published case (2048x2048 image, 300x300 hole,
+whole image and --tile) beside the reference's own figures, and the CPU
+baseline (the C restatement of the reference CPU engine, timed on this host's
+cores: median of three passes at 512x512 and at 256x256).
 """
 import argparse
 import json
+import shutil
 import subprocess
 import os
 import sys
@@ -30,6 +33,44 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
 PEAK_HBM = 8000.0  # GB/s
+# The reference's only published timings of this path (README.md:78-79): one
+# run of its binary on a 2048x2048 image with a 300x300 hole, whole image and
+# --tile (one 600x600 window), on a GTX 1080.
+REF_CLI_S = {"whole": 4.58, "tile": 0.67}
+
+
+def cli_wall_times(H, wpath, tmp, reps=3):
+    """Wall time of this build's lama-inpaint on the reference's published case:
+    a 2048x2048 image with a seeded 300x300 hole, whole image and --tile, each
+    a fresh process (start-up, weight file read, packing and upload, PNG
+    decode and encode included), `reps` runs each."""
+    cli = os.path.join(ROOT, "lama-inpaint-rs_amd", "bin", "lama-inpaint")
+    img = H.synth_image(2048, 2048, 1)
+    mask, _ = H.synth_mask_rect(2048, 2048, 300, 300, 2)
+    ip, mp = os.path.join(tmp, "in2048.png"), os.path.join(tmp, "mask2048.png")
+    H.png_write_rgb(ip, img)
+    H.png_write_rgb(mp, np.repeat(mask[..., None], 3, -1))
+    runs = {}
+    for mode, extra in (("whole", []), ("tile", ["--tile"])):
+        op = os.path.join(tmp, f"out2048_{mode}.png")
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            p = subprocess.run([cli, "--image", ip, "--mask", mp, "--output", op, "--weights", wpath, "--gpu",
+                                *extra], capture_output=True, timeout=300)
+            ts.append(time.perf_counter() - t)
+            if p.returncode != 0:
+                raise RuntimeError(f"lama-inpaint {mode} failed ({p.returncode}): "
+                                   + p.stderr.decode(errors="replace")[-400:])
+        runs[mode] = ts
+    return {"whole_s": round(float(np.median(runs["whole"])), 3),
+            "tile_s": round(float(np.median(runs["tile"])), 3),
+            "runs_s": {m: [round(v, 3) for v in ts] for m, ts in runs.items()},
+            "reference_gtx1080_s": REF_CLI_S,
+            "speedup_vs_reference": {m: round(REF_CLI_S[m] / float(np.median(runs[m])), 2) for m in runs},
+            "case": ("lama-inpaint-rs_amd/bin/lama-inpaint --gpu [--tile] on a 2048x2048 synthetic image with a "
+                     "seeded 300x300 hole (README.md:78-79's case), synthetic weights; wall time of each "
+                     f"process, median of {reps}; the reference's figures are its README's, on a GTX 1080")}
 
 
 def main():
@@ -39,6 +80,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--size", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cli", action="store_true",
+                    help="skip the command-line wall times (2048x2048 image, 300x300 hole, whole and --tile)")
     ap.add_argument("--cpu-size", type=int, default=0, help="CPU sample size (default: the workload size)")
     ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "traffic_conv3x3_512.json"),
                     help="JSON with the measured HBM bytes per launch of the dominant kernel")
@@ -240,6 +283,8 @@ def main():
                       "clock_ms_per_pass": round(v["clock_ms"] / 3, 4) if v.get("clock_launches") else None}
                   for f, v in fam.items()}
 
+    cli = None if args.no_cli else cli_wall_times(H, wpath, tmp)
+
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -353,12 +398,14 @@ def main():
         "spectral_block_workload": f"BASELINE configs[2]: SpectralTransform of FFCs 0..17 on 384x{h8}x{h8}, "
                                    "conv1 -> rfft2 -> FU conv -> irfft2 -> conv2, one stream",
         "per_family": per_family,
+        "cli_2048": cli,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     eng.free(d_in)
     eng.free(d_out)
     eng.close()
+    shutil.rmtree(tmp, ignore_errors=True)
 
 
 if __name__ == "__main__":

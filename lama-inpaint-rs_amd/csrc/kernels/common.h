@@ -322,6 +322,19 @@ struct TailArgs {
     uint8_t *out_u8;      // lama_tail_u8: composite, HWC [h][w][3]
 };
 
+// One FFC 3x3 weight matrix W[M][C][3][3] to pack into a Winograd kernel's
+// layout on the device (lama_pack_wino): input channels ci < C0 come from
+// src0 [M][C0][9], the rest from src1 [M][C - C0][9] (the FFC's local GEMM
+// concatenates l2l and g2l along K).  kind 4: the F(4,3) layout of
+// lama_conv3x3w4*; kind 42: the F(2x4, 3x3) layout of lama_conv3x3w42.
+// dst is pre-zeroed (rows past M, channels past C stay zero).
+struct WinoPackJob {
+    const float *src0, *src1;
+    float *dst;
+    int M, C, C0, nchunk, kind;
+    int pad_;
+};
+
 // Device build_input: the 8-bit image and mask (h x w, HWC RGB) to the
 // network input [4][H][W], H >= h, W >= w, reflect-padded bottom/right.
 struct InputArgs {

@@ -6,3 +6,4 @@
 #include "kernels/fft.hip"
 #include "kernels/tail.hip"
 #include "kernels/eltwise.hip"
+#include "kernels/pack.hip"

@@ -158,10 +158,20 @@ struct WeightSrc {
     bool get(const std::string &name, std::initializer_list<int64_t> shape, std::vector<float> &out,
              std::string &err) const
     {
+        const lama_tensor_info *t = find(name, shape, err);
+        if (!t) return false;
+        out.resize(t->nbytes / 4);
+        std::memcpy(out.data(), blob + t->offset, t->nbytes);
+        return true;
+    }
+    // The tensor `name`, checked against `shape`, left in the blob.
+    const lama_tensor_info *find(const std::string &name, std::initializer_list<int64_t> shape,
+                                 std::string &err) const
+    {
         auto it = idx.find(name);
         if (it == idx.end()) {
             err = "missing tensor in weight blob: " + name;  // weights.rs:116-120
-            return false;
+            return nullptr;
         }
         const lama_tensor_info *t = it->second;
         bool ok = (size_t)t->ndim == shape.size();
@@ -175,21 +185,69 @@ struct WeightSrc {
             for (int64_t d : shape) want += (want.empty() ? "" : ",") + std::to_string(d);
             for (int d = 0; d < t->ndim; ++d) got += (d ? "," : "") + std::to_string(t->shape[d]);
             err = "tensor " + name + ": expected shape [" + want + "], found [" + got + "]";
-            return false;
+            return nullptr;
         }
-        out.resize(n);
-        std::memcpy(out.data(), blob + t->offset, n * 4);
-        return true;
+        return t;
     }
 };
 
+// The host image of a device weight arena.  add() lays regions out on
+// 64-float (256-byte) boundaries of the device arena; the host side lives in
+// zero-filled blocks that never move (a region never spans two), so packing
+// writes each float once and a growing layout copies nothing.  The blocks
+// come from calloc: their pages are zeroed when first written, by the threads
+// that pack them.
 struct Arena {
-    std::vector<float> h;
-    size_t add(size_t n)
+    static constexpr size_t BLOCK = (size_t)16 << 20;  // floats per block (64 MiB)
+    struct Block {
+        size_t start, cap;
+        float *d;
+    };
+    std::vector<Block> blocks;
+    size_t n = 0;  // floats laid out: the device arena's size
+
+    Arena() = default;
+    Arena(const Arena &) = delete;
+    Arena &operator=(const Arena &) = delete;
+    ~Arena()
     {
-        size_t off = (h.size() + 63) / 64 * 64;
-        h.resize(off + n, 0.f);
+        for (Block &b : blocks) free(b.d);
+    }
+    size_t add(size_t k)
+    {
+        const size_t off = (n + 63) / 64 * 64;
+        // block starts and capacities are multiples of 64 floats, so the
+        // aligned offset never lies past the current block's end
+        if (blocks.empty() || off + k > blocks.back().start + blocks.back().cap) {
+            const size_t cap = (std::max(BLOCK, k) + 63) / 64 * 64;
+            float *d = static_cast<float *>(calloc(cap, sizeof(float)));
+            if (!d) throw std::bad_alloc();
+            blocks.push_back({off, cap, d});
+        }
+        n = off + k;
         return off;
+    }
+    float *at(size_t off)
+    {
+        for (size_t i = blocks.size(); i-- > 0;)
+            if (blocks[i].start <= off) return blocks[i].d + (off - blocks[i].start);
+        return nullptr;
+    }
+    size_t size() const { return n; }
+    // the layout into device memory of size() floats: each block up to the
+    // next one's start (alignment gaps included, as zeros)
+    bool upload(const HipApi *hip, float *dev, std::string &err) const
+    {
+        for (size_t i = 0; i < blocks.size(); ++i) {
+            const size_t end = i + 1 < blocks.size() ? blocks[i + 1].start : n;
+            const hipError_t e = hip->hipMemcpy(dev + blocks[i].start, blocks[i].d, (end - blocks[i].start) * 4,
+                                                hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                err = hip_error(*hip, e, "hipMemcpy(weights)");
+                return false;
+            }
+        }
+        return true;
     }
 };
 
@@ -203,7 +261,7 @@ Packed pack(Arena &A, int M, int C, int T, int KC, const std::function<float(int
     p.nchunk = (C + KC - 1) / KC;
     p.wrow = p.nchunk * T * KC;
     p.off = A.add((size_t)M * p.wrow);
-    float *d = A.h.data() + p.off;
+    float *d = A.at(p.off);
     for (int co = 0; co < M; ++co)
         for (int ck = 0; ck < p.nchunk; ++ck)
             for (int t = 0; t < T; ++t)
@@ -263,7 +321,7 @@ Packed pack_wino(Arena &A, int M, int C, const std::function<float(int, int, int
     p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
     p.wrow = p.nchunk * 12 * KC;
     p.off = A.add((size_t)M * p.wrow);
-    float *d = A.h.data() + p.off;
+    float *d = A.at(p.off);
     for (int co = 0; co < M; ++co)
         for (int ck = 0; ck < p.nchunk; ++ck)
             for (int u = 0; u < 4; ++u)
@@ -310,11 +368,10 @@ void parallel_rows(int n, F f)
 // u = 3 wu + q (with LAMA_W4_WX4, steps 2p and 2p + 1 of a wave interleaved
 // as [p][lane][step 2p + h][c], step 8 after them as [lane][c]).  A chunk is 64 x 72 floats (T * KC); the block stride is 64
 // rows of wrow = nchunk * 72.
-template <class Get>
-Packed pack_wino4(Arena &A, int M, int C, const Get &get)
+// The F(4,3) layout's shape (p.off unset).  The same floats are written on
+// the device by lama_pack_wino (kind 4).
+Packed wino4_shape(int M, int C)
 {
-    static const double G[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
-                                   {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
     constexpr int KC = LAMA_WINO_KC, WK = 72;
     static_assert(KC == 4, "two channels per lane half");
     Packed p;
@@ -324,9 +381,21 @@ Packed pack_wino4(Arena &A, int M, int C, const Get &get)
     p.T = 64 * WK / KC;  // chunk stride T * KC = one 64-row block's chunk
     p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
     p.wrow = p.nchunk * WK;
-    const int mblocks = (M + 63) / 64;
-    p.off = A.add((size_t)mblocks * 64 * p.wrow);  // zero: rows past M, channels past C
-    float *d = A.h.data() + p.off;
+    return p;
+}
+
+// floats of a Winograd pack: 64-row blocks (rows past M zero)
+size_t wino_floats(const Packed &p) { return (size_t)((p.M + 63) / 64) * 64 * p.wrow; }
+
+template <class Get>
+Packed pack_wino4(Arena &A, int M, int C, const Get &get)
+{
+    static const double G[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+                                   {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
+    constexpr int KC = LAMA_WINO_KC, WK = 72;
+    Packed p = wino4_shape(M, C);
+    p.off = A.add(wino_floats(p));  // zero: rows past M, channels past C
+    float *d = A.at(p.off);
     parallel_rows(M, [&](int r0, int r1) {
         for (int co = r0; co < r1; ++co) {
             const int mb = co / 64, wm = co % 64 / 32, j = co % 32;
@@ -363,13 +432,11 @@ Packed pack_wino4(Arena &A, int M, int C, const Get &get)
 // channel 32 wm + j and input channel H g + c of the chunk, with
 // H u + c = 4 h + k.  A chunk is 64 x 24 KC floats; the block stride is 64
 // rows of wrow = nchunk * 24 KC.
-template <class Get>
-Packed pack_wino42(Arena &A, int M, int C, const Get &get)
+// The F(2x4, 3x3) layout's shape (p.off unset).  The same floats are written
+// on the device by lama_pack_wino (kind 42).
+Packed wino42_shape(int M, int C)
 {
-    static const double Gx[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
-                                    {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
-    static const double Gy[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
-    constexpr int KC = LAMA_W42_KC, H = KC / 2, WK = 24 * KC, WW = 6 * H;
+    constexpr int KC = LAMA_W42_KC, WK = 24 * KC;
     static_assert(KC == 4 || KC == 8, "two or four channels per lane half");
     Packed p;
     p.M = M;
@@ -378,9 +445,19 @@ Packed pack_wino42(Arena &A, int M, int C, const Get &get)
     p.T = 64 * WK / KC;  // chunk stride T * KC = one 64-row block's chunk
     p.nchunk = ((C + KC - 1) / KC + 1) & ~1;  // even: the kernel runs its K loop in chunk pairs
     p.wrow = p.nchunk * WK;
-    const int mblocks = (M + 63) / 64;
-    p.off = A.add((size_t)mblocks * 64 * p.wrow);  // zero: rows past M, channels past C
-    float *d = A.h.data() + p.off;
+    return p;
+}
+
+template <class Get>
+Packed pack_wino42(Arena &A, int M, int C, const Get &get)
+{
+    static const double Gx[6][3] = {{0.25, 0, 0},           {-1.0 / 6, -1.0 / 6, -1.0 / 6}, {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+                                    {1.0 / 24, 1.0 / 12, 1.0 / 6}, {1.0 / 24, -1.0 / 12, 1.0 / 6}, {0, 0, 1}};
+    static const double Gy[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    constexpr int KC = LAMA_W42_KC, H = KC / 2, WK = 24 * KC, WW = 6 * H;
+    Packed p = wino42_shape(M, C);
+    p.off = A.add(wino_floats(p));  // zero: rows past M, channels past C
+    float *d = A.at(p.off);
     parallel_rows(M, [&](int r0, int r1) {
         for (int co = r0; co < r1; ++co) {
             const int mb = co / 64, wm = co % 64 / 32, j = co % 32;
@@ -429,7 +506,7 @@ bool fold_bns(Arena &A, const WeightSrc &S, const std::vector<std::pair<std::str
         if (!S.get(p.first + ".weight", {c}, w, err) || !S.get(p.first + ".bias", {c}, b, err) ||
             !S.get(p.first + ".running_mean", {c}, m, err) || !S.get(p.first + ".running_var", {c}, v, err))
             return false;
-        fold_into(w, b, m, v, A.h.data() + off + at, A.h.data() + off + n + at);
+        fold_into(w, b, m, v, A.at(off) + at, A.at(off) + n + at);
         at += p.second;
     }
     return true;
@@ -579,7 +656,7 @@ bool Engine::open(std::string &err)
         !get_fn(fn_pw_kh_[1], "lama_conv1x1_res_kh", err) || !get_fn(fn_edge_q_[0], "lama_conv3x3s2_q", err) ||
         !get_fn(fn_edge_q_[1], "lama_convt_q", err) ||
         !get_fn(fn_convt_rows_[0], "lama_convt_rows", err) ||
-        !get_fn(fn_convt_rows_[1], "lama_convt_rows_q", err))
+        !get_fn(fn_convt_rows_[1], "lama_convt_rows_q", err) || !get_fn(fn_pack_, "lama_pack_wino", err))
         return false;
     fn_build_in_ = fn_[F_INPUT];
     if (const char *wv = getenv("LAMA_FFC_WINO")) {
@@ -588,6 +665,7 @@ bool Engine::open(std::string &err)
         w42_packed_ = false;  // a forced algorithm runs on every plane
     }
     if (const char *t = getenv("LAMA_W42")) w42_packed_ = w42_packed_ && atoi(t) != 0;
+    if (const char *t = getenv("LAMA_HOST_PACK")) dev_pack_ = atoi(t) == 0;
     if (const char *t = getenv("LAMA_W4_TILE")) w4_force_ = atoi(t);
     if (const char *t = getenv("LAMA_KSPLIT")) ksplit_force_ = atoi(t);
     if (const char *t = getenv("LAMA_PW_KSPLIT")) pw_ksplit_force_ = atoi(t);
@@ -664,6 +742,25 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
         return co < 128 ? w[((size_t)co * 256 + ci) * 9 + t] : w2[((size_t)(co - 128) * 256 + ci) * 9 + t];
     });
     if (!fold_bns(A, S, {{"model.4.bn_l", 128}, {"model.4.bn_g", 384}}, down_bn_[2], err)) return false;
+    // The Winograd packs of the FFC 3x3 convolutions (F(4,3), and F(2x4, 3x3)
+    // for the large planes: 692 of the 749 MB of packed weights) are made on
+    // the device from the raw weights (149 MB), laid out after the host-packed
+    // part of the arena (offsets relative to that part's end until the upload).
+    struct DevJob {
+        Packed *p;
+        const lama_tensor_info *s0, *s1;
+        int kind;
+    };
+    std::vector<DevJob> dev;
+    size_t dev_n = 0;  // floats of the device-packed part
+    auto dev_job = [&](Packed &p, const Packed &shape, int kind, const lama_tensor_info *s0,
+                       const lama_tensor_info *s1) {
+        p = shape;
+        p.off = (dev_n + 63) / 64 * 64;
+        dev_n = p.off + wino_floats(p);
+        dev.push_back({&p, s0, s1, kind});
+    };
+    const bool dev_wino = dev_pack_ && (wino_ == 4 || wino_ == 42);
     // model.5..22: 36 FFC_BN_ACT (model.rs:157-165), ratio 0.75: 128 local / 384 global
     for (int i = 5; i <= 22; ++i)
         for (int s = 1; s <= 2; ++s) {
@@ -671,30 +768,43 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
             const std::string pb = "model." + std::to_string(i) + ".conv" + std::to_string(s);
             const std::string pf = pb + ".ffc";
             std::vector<float> l2l, g2l, l2g, c1, c2, fu;
-            if (!S.get(pf + ".convl2l.weight", {128, 128, 3, 3}, l2l, err) ||
-                !S.get(pf + ".convg2l.weight", {128, 384, 3, 3}, g2l, err) ||
-                !S.get(pf + ".convl2g.weight", {384, 128, 3, 3}, l2g, err) ||
+            const lama_tensor_info *tl2l = S.find(pf + ".convl2l.weight", {128, 128, 3, 3}, err);
+            const lama_tensor_info *tg2l = tl2l ? S.find(pf + ".convg2l.weight", {128, 384, 3, 3}, err) : nullptr;
+            const lama_tensor_info *tl2g = tg2l ? S.find(pf + ".convl2g.weight", {384, 128, 3, 3}, err) : nullptr;
+            if (!tl2g || (!dev_wino && (!S.get(pf + ".convl2l.weight", {128, 128, 3, 3}, l2l, err) ||
+                                        !S.get(pf + ".convg2l.weight", {128, 384, 3, 3}, g2l, err) ||
+                                        !S.get(pf + ".convl2g.weight", {384, 128, 3, 3}, l2g, err))) ||
                 !S.get(pf + ".convg2g.conv1.0.weight", {192, 384, 1, 1}, c1, err) ||
                 !S.get(pf + ".convg2g.fu.conv_layer.weight", {384, 384, 1, 1}, fu, err) ||
                 !S.get(pf + ".convg2g.conv2.weight", {384, 192, 1, 1}, c2, err))
                 return false;
-            auto local = [&](int co, int ci, int t) {
-                return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t] : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
-            };
-            auto l2gw = [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; };
-            // the F(2x4) packs beside the default F(4,3) ones, for the large planes
-            if (w42_packed_) {
-                F.local42 = pack_wino42(A, 128, 512, local);
-                F.l2g42 = pack_wino42(A, 384, 128, l2gw);
+            if (dev_wino) {
+                // the F(2x4) packs beside the default F(4,3) ones, for the large planes
+                if (w42_packed_) {
+                    dev_job(F.local42, wino42_shape(128, 512), 42, tl2l, tg2l);
+                    dev_job(F.l2g42, wino42_shape(384, 128), 42, tl2g, nullptr);
+                }
+                dev_job(F.local, wino_ == 42 ? wino42_shape(128, 512) : wino4_shape(128, 512), wino_, tl2l, tg2l);
+                dev_job(F.l2g, wino_ == 42 ? wino42_shape(384, 128) : wino4_shape(384, 128), wino_, tl2g, nullptr);
+            } else {
+                auto local = [&](int co, int ci, int t) {
+                    return ci < 128 ? l2l[((size_t)co * 128 + ci) * 9 + t]
+                                    : g2l[((size_t)co * 384 + ci - 128) * 9 + t];
+                };
+                auto l2gw = [&](int co, int ci, int t) { return l2g[((size_t)co * 128 + ci) * 9 + t]; };
+                if (w42_packed_) {
+                    F.local42 = pack_wino42(A, 128, 512, local);
+                    F.l2g42 = pack_wino42(A, 384, 128, l2gw);
+                }
+                F.local = wino_ == 42  ? pack_wino42(A, 128, 512, local)
+                          : wino_ == 4 ? pack_wino4(A, 128, 512, local)
+                          : wino_      ? pack_wino(A, 128, 512, local)
+                                       : pack(A, 128, 512, 9, 8, local);
+                F.l2g = wino_ == 42  ? pack_wino42(A, 384, 128, l2gw)
+                        : wino_ == 4 ? pack_wino4(A, 384, 128, l2gw)
+                        : wino_      ? pack_wino(A, 384, 128, l2gw)
+                                     : pack(A, 384, 128, 9, 8, l2gw);
             }
-            F.local = wino_ == 42  ? pack_wino42(A, 128, 512, local)
-                      : wino_ == 4 ? pack_wino4(A, 128, 512, local)
-                      : wino_      ? pack_wino(A, 128, 512, local)
-                                   : pack(A, 128, 512, 9, 8, local);
-            F.l2g = wino_ == 42  ? pack_wino42(A, 384, 128, l2gw)
-                    : wino_ == 4 ? pack_wino4(A, 384, 128, l2gw)
-                    : wino_      ? pack_wino(A, 384, 128, l2gw)
-                                 : pack(A, 384, 128, 9, 8, l2gw);
             // rows of C channels in order: each launch sets the chunk count of
             // its kernel (pw_kc)
             F.conv2 = pack(A, 384, 192, 1, LAMA_PW_KC, [&](int co, int ci, int) { return c2[(size_t)co * 192 + ci]; });
@@ -722,24 +832,88 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
             for (int ph = 0; ph < 4; ++ph) U.ph[ph] = pack_convt_phase(A, U.cout, U.cin, ph, w.data());
         }
         U.bias = A.add(U.cout);
-        std::copy(bias.begin(), bias.end(), A.h.begin() + U.bias);
+        std::copy(bias.begin(), bias.end(), A.at(U.bias));
         if (!fold_bns(A, S, {{"model." + std::to_string(ups[u][0] + 1), U.cout}}, U.bn, err)) return false;
     }
     // model.34: 7x7 64 -> 3 with bias
     std::vector<float> tb;
     if (!S.get("model.34.weight", {3, 64, 7, 7}, w, err) || !S.get("model.34.bias", {3}, tb, err)) return false;
     tail_w_ = A.add(w.size());
-    std::copy(w.begin(), w.end(), A.h.begin() + tail_w_);
+    std::copy(w.begin(), w.end(), A.at(tail_w_));
     tail_b_ = A.add(3);
-    std::copy(tb.begin(), tb.end(), A.h.begin() + tail_b_);
+    std::copy(tb.begin(), tb.end(), A.at(tail_b_));
 
     // one upload (cuda.rs:330-369 does one HtoD of the raw file), into a new
     // arena: the engine's state changes only once it has succeeded, so a
     // failed load leaves the previous weights and their plans usable
+    const size_t dev_base = (A.size() + 63) / 64 * 64, total = dev.empty() ? A.size() : dev_base + dev_n;
+    for (DevJob &j : dev) j.p->off += dev_base;
+    // The device-packed part: zeroed (rows past M, channels past C), the raw
+    // matrices copied once each into a temporary buffer, one lama_pack_wino
+    // launch over all jobs, then the temporaries freed.
+    auto pack_on_device = [&](float *w) {
+        if (dev.empty()) return true;
+        std::map<const lama_tensor_info *, size_t> raw_off;
+        size_t raw_n = 0;
+        for (const DevJob &j : dev)
+            for (const lama_tensor_info *t : {j.s0, j.s1})
+                if (t && !raw_off.count(t)) {
+                    raw_off[t] = raw_n;
+                    raw_n += (t->nbytes / 4 + 63) / 64 * 64;
+                }
+        float *raw = nullptr;
+        WinoPackJob *djobs = nullptr;
+        auto done = [&](bool ok) {
+            if (raw) hip_->hipFree(raw);
+            if (djobs) hip_->hipFree(djobs);
+            return ok;
+        };
+        if (!check(hip_->hipMemset(w + dev_base, 0, dev_n * 4), "hipMemset(weights)", err) ||
+            !check(hip_->hipMalloc((void **)&raw, raw_n * 4), "hipMalloc(raw weights)", err))
+            return done(false);
+        for (const auto &kv : raw_off)
+            if (!check(hip_->hipMemcpy(raw + kv.second, blob + kv.first->offset, kv.first->nbytes,
+                                       hipMemcpyHostToDevice),
+                       "hipMemcpy(raw weights)", err))
+                return done(false);
+        std::vector<WinoPackJob> jobs(dev.size());
+        long most = 0;
+        for (size_t i = 0; i < dev.size(); ++i) {
+            const DevJob &d = dev[i];
+            WinoPackJob &J = jobs[i];
+            J = WinoPackJob{};
+            J.src0 = raw + raw_off[d.s0];
+            J.src1 = d.s1 ? raw + raw_off[d.s1] : nullptr;
+            J.dst = w + d.p->off;
+            J.M = d.p->M;
+            J.C = d.p->C;
+            J.C0 = (int)d.s0->shape[1];  // input channels from src0; the rest from src1
+            J.nchunk = d.p->nchunk;
+            J.kind = d.kind;
+            if ((J.C0 < J.C) != (d.s1 != nullptr) || d.s0->shape[0] != J.M ||
+                (d.s1 && (d.s1->shape[0] != J.M || d.s1->shape[1] != J.C - J.C0))) {
+                err = "internal: inconsistent weight pack job";
+                return done(false);
+            }
+            most = std::max(most, (long)J.M * J.C);
+        }
+        if (!check(hip_->hipMalloc((void **)&djobs, jobs.size() * sizeof(WinoPackJob)), "hipMalloc(pack jobs)",
+                   err) ||
+            !check(hip_->hipMemcpy(djobs, jobs.data(), jobs.size() * sizeof(WinoPackJob), hipMemcpyHostToDevice),
+                   "hipMemcpy(pack jobs)", err))
+            return done(false);
+        void *params[1] = {&djobs};
+        const unsigned gx = (unsigned)std::min<long>(256, (most + 255) / 256);
+        if (!check(hip_->hipModuleLaunchKernel(fn_pack_, gx, (unsigned)jobs.size(), 1, 256, 1, 1, 0, stream_, params,
+                                               nullptr),
+                   "lama_pack_wino", err) ||
+            !check(hip_->hipStreamSynchronize(stream_), "lama_pack_wino", err))
+            return done(false);
+        return done(true);
+    };
     float *fresh = nullptr;
-    if (!check(hip_->hipMalloc((void **)&fresh, A.h.size() * 4), "hipMalloc(weights)", err)) return false;
-    if (!check(hip_->hipMemcpy(fresh, A.h.data(), A.h.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(weights)",
-               err)) {
+    if (!check(hip_->hipMalloc((void **)&fresh, total * 4), "hipMalloc(weights)", err)) return false;
+    if (!A.upload(hip_, fresh, err) || !pack_on_device(fresh)) {
         hip_->hipFree(fresh);
         return false;
     }
@@ -757,7 +931,7 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
     release_scratch_owner();
     if (warena_) hip_->hipFree(warena_);
     warena_ = fresh;
-    warena_bytes_ = A.h.size() * 4;
+    warena_bytes_ = total * 4;
     have_weights_ = true;
     return true;
 }
@@ -2591,14 +2765,15 @@ bool Engine::op_conv2d(const float *x, int cin, int h, int w, const float *wt, c
                           : pack(A, cout, cin, T, KC, getw);
     size_t bn = A.add(2 * (size_t)cout);
     for (int i = 0; i < cout; ++i) {
-        A.h[bn + i] = scale ? scale[i] : 1.f;
-        A.h[bn + cout + i] = scale ? shift[i] : 0.f;
+        A.at(bn)[i] = scale ? scale[i] : 1.f;
+        A.at(bn)[cout + i] = scale ? shift[i] : 0.f;
     }
     size_t bo = A.add(cout);
-    if (bias) std::copy(bias, bias + cout, A.h.begin() + bo);
+    if (bias) std::copy(bias, bias + cout, A.at(bo));
     Scratch sc{hip_, {}};
     UPLOAD(dx, x, (size_t)cin * h * w);
-    UPLOAD(dw, A.h.data(), A.h.size());
+    UPLOAD(dw, nullptr, A.size());
+    if (!A.upload(hip_, dw, err)) return false;
     UPLOAD(dout, nullptr, (size_t)cout * oh * ow);
     ConvProblem q{};
     q.s0.src = dx;
@@ -2653,13 +2828,14 @@ bool Engine::op_convt(const float *x, int cin, int h, int w, const float *wt, co
         ph[k] = convt_rows_ ? pack_convt_rows(A, cout, cin, k, wt) : pack_convt_phase(A, cout, cin, k, wt);
     size_t bn = A.add(2 * (size_t)cout), bo = A.add(cout);
     for (int i = 0; i < cout; ++i) {
-        A.h[bn + i] = scale ? scale[i] : 1.f;
-        A.h[bn + cout + i] = scale ? shift[i] : 0.f;
-        A.h[bo + i] = bias ? bias[i] : 0.f;
+        A.at(bn)[i] = scale ? scale[i] : 1.f;
+        A.at(bn)[cout + i] = scale ? shift[i] : 0.f;
+        A.at(bo)[i] = bias ? bias[i] : 0.f;
     }
     Scratch sc{hip_, {}};
     UPLOAD(dx, x, (size_t)cin * h * w);
-    UPLOAD(dw, A.h.data(), A.h.size());
+    UPLOAD(dw, nullptr, A.size());
+    if (!A.upload(hip_, dw, err)) return false;
     UPLOAD(dout, nullptr, (size_t)cout * 4 * h * w);
     ConvProblem q[4]{};
     unsigned nb = 0;

@@ -237,6 +237,11 @@ private:
     // the default mode also packs F(2x4, 3x3) weights and takes that kernel
     // on large planes (wino_for); LAMA_W42=0 (read at open) keeps F(4,3)
     bool w42_packed_ = true;
+    // the Winograd weight transforms of the FFC 3x3 convolutions run on the
+    // device (lama_pack_wino) from the raw weights; LAMA_HOST_PACK=1 (read at
+    // open) packs them on the host instead (the same floats)
+    bool dev_pack_ = true;
+    hipFunction_t fn_pack_ = nullptr;
     int w4_force_ = 0;  // LAMA_W4_TILE: 64, 32 or 16 forces the F(4,3) block width
     int w4_variant(int OH, int OW) const;  // index into fn_wino4_
     int tile_variant(int family, int OH, int OW, int M = 0, long cs = 0) const;

@@ -421,6 +421,30 @@ def test_forward_f2x4_matches_f43_1536(pkg, weights_dir, engine):
         e43.close()
 
 
+def test_device_packed_weights_match_host_packed(pkg, weights_dir, engine):
+    """The FFC 3x3 weights packed for the Winograd kernels on the device
+    (lama_pack_wino, the default) and on the host (LAMA_HOST_PACK=1): the same
+    floats, so forwards through the F(4,3) packs (128 x 96) and through the
+    F(2x4, 3x3) packs (1024 x 1024) are bit-identical."""
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("LAMA_HOST_PACK", "1")
+        eh = pkg.hip_engine.Engine()
+    try:
+        eh.load_weights(pkg.host_api.Store(weights_dir["cal"]))
+        for (h, w), f2x4 in (((128, 96), False), ((1024, 1024), True)):
+            img, mask = _case(pkg, h, w, "strokes")
+            x = pkg.host_api.build_input(img, mask)
+            print(f"case device vs host packs {h}x{w}", flush=True)
+            a = engine.forward(x)
+            b = eh.forward(x)
+            kern = engine.kernel_name(h, w, "conv3x3")
+            assert kern == eh.kernel_name(h, w, "conv3x3")
+            assert kern.startswith("lama_conv3x3w4") and (kern == "lama_conv3x3w42") == f2x4, kern
+            assert np.array_equal(a, b)
+    finally:
+        eh.close()
+
+
 def test_timeline_records_every_launch(pkg, engine):
     """lama_hip_timeline: one pass's 296 launches in issue order, each with a
     kernel-clock window; launches on one stream never overlap, and the
