@@ -462,6 +462,70 @@ def test_png_decodes_pil_variants(H, tmp_path, mode):
     assert np.array_equal(gray, want[..., 0])  # the mask is the red channel
 
 
+def _png_filtered(rgb, filters, bpp=3):
+    """An RGB8 PNG whose row y uses filter filters[y % len(filters)] (PNG spec
+    section 9), built here with zlib."""
+    import struct
+    import zlib
+
+    h, w, _ = rgb.shape
+    rows = rgb.reshape(h, w * bpp).astype(np.int32)
+    out = bytearray()
+    prev = np.zeros(w * bpp, np.int32)
+    for y in range(h):
+        ft = filters[y % len(filters)]
+        cur = rows[y]
+        a = np.concatenate([np.zeros(bpp, np.int32), cur[:-bpp]])
+        c = np.concatenate([np.zeros(bpp, np.int32), prev[:-bpp]])
+        if ft == 0:
+            f = cur
+        elif ft == 1:
+            f = cur - a
+        elif ft == 2:
+            f = cur - prev
+        elif ft == 3:
+            f = cur - (a + prev) // 2
+        else:
+            p = a + prev - c
+            pa, pb, pc = np.abs(p - a), np.abs(p - prev), np.abs(p - c)
+            f = cur - np.where((pa <= pb) & (pa <= pc), a, np.where(pb <= pc, prev, c))
+        out.append(ft)
+        out += (f & 0xFF).astype(np.uint8).tobytes()
+        prev = cur
+
+    def chunk(t, d):
+        return struct.pack(">I", len(d)) + t + d + struct.pack(">I", zlib.crc32(t + d) & 0xFFFFFFFF)
+
+    ihdr = struct.pack(">IIBBBBB", w, h, 8, 2, 0, 0, 0)
+    return b"\x89PNG\r\n\x1a\n" + chunk(b"IHDR", ihdr) + chunk(b"IDAT", zlib.compress(bytes(out), 6)) + \
+        chunk(b"IEND", b"")
+
+
+@pytest.mark.parametrize("filters", [[0], [1], [2], [3], [4], [0, 1, 2, 3, 4], [4, 3, 2, 1, 0]])
+def test_png_decodes_every_scanline_filter(H, tmp_path, filters):
+    rng = np.random.default_rng(3)
+    img = rng.integers(0, 256, (23, 31, 3), dtype=np.uint8)
+    img[5:15, 4:20] = H.synth_image(10, 16, 2)  # smooth patch beside noise
+    p = tmp_path / "f.png"
+    p.write_bytes(_png_filtered(img, filters))
+    assert np.array_equal(H.png_read_rgb(str(p)), img)
+
+
+def test_png_writer_bands_read_back(H, tmp_path):
+    """The writer deflates 1 MiB bands on several threads into one zlib
+    stream: images of one band, several bands and a ragged last band read
+    back exactly, through this decoder and PIL's."""
+    PIL = pytest.importorskip("PIL.Image")
+    rng = np.random.default_rng(4)
+    for h, w in ((1, 1), (600, 700), (1100, 1000)):
+        img = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+        img[: h // 2] = H.synth_image(h // 2, w, 5) if h > 1 else img[: h // 2]
+        p = str(tmp_path / f"b{h}.png")
+        H.png_write_rgb(p, img)
+        assert np.array_equal(H.png_read_rgb(p), img)
+        assert np.array_equal(np.asarray(PIL.open(p).convert("RGB")), img)
+
+
 def test_png_rejects_garbage(H, tmp_path):
     p = tmp_path / "x.png"
     p.write_bytes(b"not a png at all")
