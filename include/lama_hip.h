@@ -71,10 +71,12 @@ int lama_hip_forward_device(lama_hip_ctx *ctx, const float *d_input, int h, int 
  * descriptors the shared array holds at replay time.
  * The pass's activations, partial sums, FFT scratch and launch descriptors
  * live in a device array of LAMA_SCRATCH_BYTES = 192 MiB (`lama_scratch`, a
- * code object of its own that lama_hip_open loads once per device per
- * process, so every process that opens a context holds it on that device
- * until it ends; if that load fails, the open still succeeds and only this
- * entry point returns the error).  Shapes whose arena
+ * code object of its own that this entry point's first call on a device
+ * loads, once per device per process: that call is the one that loads it,
+ * so make it before any phase that must not allocate; the process then holds
+ * the array on that device until it ends.  Processes that never call this
+ * entry point do not hold it.  If the load fails, that call returns the
+ * error and the next call tries again).  Shapes whose arena
  * exceeds it are rejected with an error: up to 512 x 512 fits (177 MiB).
  * The call makes no hipMalloc, hipFree, event or graph creation (and no
  * per-family profiling or launch timeline); the caller passes device input and output as for

@@ -566,8 +566,14 @@ extern "C" const unsigned char lama_hsaco_start[];
 extern "C" const unsigned char lama_hsaco_end[];
 extern "C" const unsigned char lama_scratch_hsaco_start[];
 
+namespace {
+using Clock = std::chrono::steady_clock;
+double since(Clock::time_point a) { return std::chrono::duration<double>(Clock::now() - a).count(); }
+}  // namespace
+
 bool Engine::open(std::string &err)
 {
+    const auto t_open = Clock::now();
     hip_ = hip_api(err);
     if (!hip_) return false;
     if (!check(hip_->hipInit(0), "hipInit", err)) return false;
@@ -591,44 +597,11 @@ bool Engine::open(std::string &err)
               "; this backend carries gfx950 (MI355X) code only";
         return false;
     }
+    const double t_runtime = since(t_open);
+    const auto t_mod = Clock::now();
     if (!check(hip_->hipModuleLoadData(&module_, lama_hsaco_start), "hipModuleLoadData", err)) return false;
-    // The no-allocation entry point's array: set up once per device per
-    // process, with that device current -- its code object is loaded and the
-    // array's address on this device looked up (hipModuleGetGlobal, the
-    // module-loaded form of hipGetSymbolAddress); every later use goes through
-    // that address.  A failed set-up (for instance no room on a nearly full
-    // device) is not an error of the open: only forward_device_noalloc then
-    // fails, with this message.
+    const double t_kernels = since(t_mod);
     id_ = ++g_engine_ids;
-    {
-        std::lock_guard<std::mutex> lk(g_scratch_mu);
-        DeviceScratch &d = g_scratch[device_];
-        if (!d.ptr) {
-            std::string serr;
-            hipModule_t m = nullptr;
-            hipDeviceptr_t p = nullptr;
-            size_t n = 0;
-            if (!check(hip_->hipModuleLoadData(&m, lama_scratch_hsaco_start), "hipModuleLoadData(scratch)", serr)) {
-                m = nullptr;
-            } else if (!check(hip_->hipModuleGetGlobal(&p, &n, m, "lama_scratch"), "hipModuleGetGlobal(lama_scratch)",
-                              serr)) {
-                p = nullptr;
-            } else if (!p || n < LAMA_SCRATCH_BYTES) {
-                serr = "lama_scratch: " + std::to_string(n) + " bytes, expected " + std::to_string(LAMA_SCRATCH_BYTES);
-                p = nullptr;
-            }
-            if (p) {
-                d.mod = m;
-                d.ptr = p;
-                d.bytes = n;
-            } else {
-                if (m) hip_->hipModuleUnload(m);
-                hip_->hipGetLastError();  // the failure is reported by the entry point, not by a later call
-                scratch_err_ = serr;
-            }
-        }
-        scratch_ = d.ptr;
-    }
     for (int f = 0; f < F_COUNT; ++f)
         if (!get_fn(fn_[f], kKernelName[f], err)) return false;
     for (int f = 0; f < 4; ++f)
@@ -712,11 +685,15 @@ bool Engine::open(std::string &err)
         dump_step_ = (end != d && *end == 0 && v >= 0 && v < kSteps) ? (int)v : -1;  // parse().ok()
     }
     if (flag_profile_ops_ || flag_profile_sub_) prof_mask_ = (1u << F_COUNT) - 1;
+    if (flag_profile_)
+        fprintf(stderr, "gpu open: %.3fs (runtime and device %.3fs, kernels %.3fs)\n", since(t_open), t_runtime,
+                t_kernels);
     return true;
 }
 
 bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_info *t, size_t n, std::string &err)
 {
+    const auto t_load = Clock::now();
     WeightSrc S{blob, len, {}};
     for (size_t i = 0; i < n; ++i) S.idx[t[i].name] = &t[i];
     Arena A;
@@ -911,12 +888,21 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
             return done(false);
         return done(true);
     };
+    const double t_host = since(t_load);
+    const auto t_up = Clock::now();
     float *fresh = nullptr;
     if (!check(hip_->hipMalloc((void **)&fresh, total * 4), "hipMalloc(weights)", err)) return false;
-    if (!A.upload(hip_, fresh, err) || !pack_on_device(fresh)) {
+    if (!A.upload(hip_, fresh, err)) {
         hip_->hipFree(fresh);
         return false;
     }
+    const double t_upload = since(t_up);
+    const auto t_dev = Clock::now();
+    if (!pack_on_device(fresh)) {
+        hip_->hipFree(fresh);
+        return false;
+    }
+    const double t_device = since(t_dev);
     // plans hold pointers into the old arena; no pass may still read it
     if (!check(hip_->hipDeviceSynchronize(), "hipDeviceSynchronize", err)) {
         hip_->hipFree(fresh);
@@ -932,6 +918,11 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
     if (warena_) hip_->hipFree(warena_);
     warena_ = fresh;
     warena_bytes_ = total * 4;
+    if (flag_profile_)
+        fprintf(stderr,
+                "gpu weights: %.3fs, %.1f MB resident (host packing %.3fs, upload of %.1f MB %.3fs, "
+                "raw 3x3 upload and Winograd packing on the device %.3fs)\n",
+                since(t_load), total * 4 / 1e6, t_host, A.size() * 4 / 1e6, t_upload, t_device);
     have_weights_ = true;
     return true;
 }
@@ -2200,6 +2191,45 @@ bool Engine::forward_device(const float *d_in, int h, int w, float *d_out, hipSt
 // A stream under capture is refused: a captured pass would replay against
 // whatever descriptors the shared array holds at replay time, which another
 // context or shape may have replaced, with the captured grid sizes.
+// The no-allocation entry point's array, set up by its first call on a
+// device, once per device per process, with that device current: its code
+// object is loaded and the array's address on this device looked up
+// (hipModuleGetGlobal, the module-loaded form of hipGetSymbolAddress); every
+// later use goes through that address.  A failed set-up (for instance no room
+// on a nearly full device) fails that call, and the next call tries again.
+bool Engine::scratch_setup(std::string &err)
+{
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    DeviceScratch &d = g_scratch[device_];
+    if (!d.ptr) {
+        hipModule_t m = nullptr;
+        hipDeviceptr_t p = nullptr;
+        size_t n = 0;
+        std::string serr;
+        if (!check(hip_->hipSetDevice(device_), "hipSetDevice", serr) ||
+            !check(hip_->hipModuleLoadData(&m, lama_scratch_hsaco_start), "hipModuleLoadData(scratch)", serr)) {
+            m = nullptr;
+        } else if (!check(hip_->hipModuleGetGlobal(&p, &n, m, "lama_scratch"), "hipModuleGetGlobal(lama_scratch)",
+                          serr)) {
+            p = nullptr;
+        } else if (!p || n < LAMA_SCRATCH_BYTES) {
+            serr = "lama_scratch: " + std::to_string(n) + " bytes, expected " + std::to_string(LAMA_SCRATCH_BYTES);
+            p = nullptr;
+        }
+        if (!p) {
+            if (m) hip_->hipModuleUnload(m);
+            hip_->hipGetLastError();  // reported here, not by a later call
+            err = "the no-allocation scratch array could not be set up: " + serr;
+            return false;
+        }
+        d.mod = m;
+        d.ptr = p;
+        d.bytes = n;
+    }
+    scratch_ = d.ptr;
+    return true;
+}
+
 bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_out, hipStream_t s, std::string &err)
 {
     if (!have_weights_) {
@@ -2207,10 +2237,6 @@ bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_ou
         return false;
     }
     if (!shape_ok(h, w, err)) return false;
-    if (!scratch_) {
-        err = "the no-allocation scratch array was not set up" + (scratch_err_.empty() ? "" : ": " + scratch_err_);
-        return false;
-    }
     if (!s) s = stream_;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (!check(hip_->hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing", err)) return false;
@@ -2219,6 +2245,7 @@ bool Engine::forward_device_noalloc(const float *d_in, int h, int w, float *d_ou
               "device's shared scratch array, which any later call may overwrite";
         return false;
     }
+    if (!scratch_ && !scratch_setup(err)) return false;
     const bool fresh = !(na_plan_.arena && na_plan_.H == h && na_plan_.W == w);
     if (fresh) {
         uint64_t need = 0, wb = 0;

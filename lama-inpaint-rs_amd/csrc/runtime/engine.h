@@ -290,9 +290,9 @@ private:
     // array), the array's address, and this engine's identity in the
     // process-wide record of which context's descriptors the array holds
     Plan na_plan_;
-    void *scratch_ = nullptr;
-    std::string scratch_err_;  // why the array could not be set up at open
+    void *scratch_ = nullptr;  // set by the entry point's first call (scratch_setup)
     uint64_t id_ = 0;
+    bool scratch_setup(std::string &err);
     void release_scratch_owner();
     std::map<std::pair<int, int>, SpecPlan> spec_plans_;
     hipFunction_t fn_build_in_ = nullptr, fn_tail_u8_ = nullptr;

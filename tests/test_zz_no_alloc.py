@@ -1,8 +1,9 @@
 """lama_hip_forward_device_noalloc through the C ABI: the forward on the
 device's lama_scratch array equals lama_hip_forward_device's bit for bit, on
 two calls in a row whose second input is smaller, and again after another
-context used the array; it allocates no device memory and rejects an input
-whose arena exceeds the array."""
+context used the array; after the first call on the device, which sets the
+array up, it allocates no device memory; it rejects an input whose arena
+exceeds the array."""
 import ctypes
 
 import numpy as np
@@ -29,6 +30,16 @@ def test_noalloc_matches_forward_device(pkg, weights_dir):
     E = pkg.hip_engine
     eng = E.Engine()
     eng.load_weights(pkg.host_api.Store(weights_dir["cal"]))
+    # the first call on the device sets the array up (loads its code object)
+    x0 = _case(pkg, 64, 64, 9)
+    d0i, d0o = eng.malloc(x0.nbytes), eng.malloc(3 * 64 * 64 * 4)
+    eng.upload(d0i, x0)
+    print("case noalloc set-up call 64x64", flush=True)
+    rc, msg = _noalloc(pkg, eng, d0i, 64, 64, d0o)
+    assert rc == 0, msg
+    eng.synchronize()
+    eng.free(d0i)
+    eng.free(d0o)
     free0 = E.vram()[0]
     outs = {}
     for h, w, seed in [(512, 512, 1), (256, 384, 3)]:
