@@ -1,13 +1,14 @@
 // The HIP engine: the reference's cuda.rs host side rebuilt around a fused,
 // preplanned forward.
 //
-//  * Weights: derived once on the host from the container and uploaded in
-//    one copy (cuda.rs uploads the raw file and derives on every call):
-//    BatchNorms folded as cpu.rs:58-62, convolution weights packed for the
-//    MFMA kernels ([M][nchunk][taps][KC]), the FFC's local convolutions
+//  * Weights: derived once when loaded (cuda.rs uploads the raw file and
+//    derives on every call): BatchNorms folded as cpu.rs:58-62, convolution
+//    weights packed for the MFMA kernels ([M][nchunk][taps][KC]), model.4's
+//    l2l/l2g stacked along M, every ConvTranspose split into its sub-pixel
+//    phases -- built on the host and uploaded -- and the FFC 3x3 weights in
+//    the Winograd kernels' layouts, with the FFC's local convolutions
 //    concatenated along K (l2l | g2l, so out_l = l2l(x_l) + g2l(x_g) is one
-//    GEMM), model.4's l2l/l2g stacked along M, and every ConvTranspose split
-//    into its four sub-pixel phases.
+//    GEMM) -- transformed on the device from the raw weights.
 //  * Activations: one device arena per input shape with the whole plan laid
 //    out up front; local and global branches share one [512][h/8][w/8]
 //    buffer (local planes first), which makes the reference's concat free.
