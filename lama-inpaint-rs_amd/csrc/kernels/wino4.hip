@@ -9,7 +9,7 @@
 //         V0 = 4 d0 - 5 d2 + d4          V3 = -2 d1 - d2 + 2 d3 + d4
 //         V1 = -4 (d1 + d2) + d3 + d4    V4 = 2 d1 - d2 - 2 d3 + d4
 //         V2 = 4 (d1 - d2) - d3 + d4     V5 = 4 d1 - 5 d3 + d5
-//     U = G g     (weight transform, on the host in f64)
+//     U = G g     (weight transform in f64, once, by lama_pack_wino)
 //         U = (g0/4, -(g0+g1+g2)/6, -(g0-g1+g2)/6, g0/24+g1/12+g2/6, g0/24-g1/12+g2/6, g2)
 //     m_u = sum over (ci, ky) of U_u * V_u                   (six GEMMs)
 //     out = A^T m (output transform, in the epilogue)
@@ -499,7 +499,7 @@ LAMA_W4_KERNEL(lama_conv3x3w4q, 4)
 //     V(0) = V_x(r0) - V_x(r2)   V(1) = V_x(r1) + V_x(r2)
 //     V(2) = V_x(r2) - V_x(r1)   V(3) = V_x(r1) - V_x(r3)       (B_y^T)
 //     U(vy, u) = sum over (ky, kx) of G_y[vy][ky] G_x[u][kx] g[ky][kx]
-//         G_y = (1, 0, 0; 1/2, 1/2, 1/2; 1/2, -1/2, 1/2; 0, 0, 1)   (host, f64)
+//         G_y = (1, 0, 0; 1/2, 1/2, 1/2; 1/2, -1/2, 1/2; 0, 0, 1)   (f64, lama_pack_wino)
 //     m(vy, u) = sum over ci of U(vy, u) V(vy, u)               (24 GEMMs)
 //     out(row 0) = A_x^T (m(0) + m(1) + m(2)),  out(row 1) = A_x^T (m(1) - m(2) - m(3))
 // 24 multiplications per 8 outputs and input channel: 2/3 of the
