@@ -61,6 +61,8 @@ extern "C" {
 
 long fakehip_violations() { return g_violations; }
 long fakehip_mallocs() { return g_mallocs; }
+long g_modules = 0;
+long fakehip_modules() { return g_modules; }
 long fakehip_frees() { return g_frees; }
 long fakehip_live_bytes()
 {
@@ -124,6 +126,7 @@ hipError_t hipMemGetInfo(size_t *f, size_t *t)
 }
 hipError_t hipModuleLoadData(hipModule_t *m, const void *image)
 {
+    ++g_modules;
     *m = (hipModule_t)image;  // any non-null handle
     return image ? hipSuccess : hipErrorInvalidImage;
 }

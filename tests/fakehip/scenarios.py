@@ -22,6 +22,7 @@ fake = ctypes.CDLL(fake_path)
 fake.fakehip_launches.argtypes = [ctypes.c_char_p]
 fake.fakehip_launches.restype = ctypes.c_long
 fake.fakehip_live_bytes.restype = ctypes.c_long
+fake.fakehip_modules.restype = ctypes.c_long
 out = {}
 
 
@@ -78,7 +79,11 @@ def run_reload_failure():
 
 
 def run_plan_failure():
+    # opening a context loads the kernels' code object only; the no-allocation
+    # entry point's array (its own code object) waits for that entry's first call
+    modules = fake.fakehip_modules()
     eng = E.Engine()
+    out["open_modules"] = fake.fakehip_modules() - modules
     eng.load_weights(H.Store(weights))
     os.environ["FAKEHIP_FAIL_MALLOC_ABOVE"] = str(50 << 20)
     try:
@@ -91,9 +96,13 @@ def run_plan_failure():
     out["forward_after_failed_plan"] = "ok"
     # the no-allocation entry point: 512x512 runs in the scratch array, 600x600 is refused
     d_in, d_out = eng.malloc(4 * 600 * 600 * 4), eng.malloc(3 * 600 * 600 * 4)
-    mallocs = fake.fakehip_mallocs()
+    mallocs, modules = fake.fakehip_mallocs(), fake.fakehip_modules()
     eng.forward_device_noalloc(d_in, 512, 512, d_out)
     out["noalloc_512_mallocs"] = fake.fakehip_mallocs() - mallocs
+    out["noalloc_first_modules"] = fake.fakehip_modules() - modules
+    modules = fake.fakehip_modules()
+    eng.forward_device_noalloc(d_in, 512, 512, d_out)
+    out["noalloc_second_modules"] = fake.fakehip_modules() - modules
     # with the launch timeline on, still no allocation
     eng.timeline(True)
     mallocs = fake.fakehip_mallocs()

@@ -109,6 +109,9 @@ def test_failed_plan_allocation_is_an_error_and_noalloc_allocates_nothing(fake_l
     assert o["forward_after_failed_plan"] == "ok"
     assert o["noalloc_512_mallocs"] == 0
     assert o["noalloc_timeline_mallocs"] == 0
+    # the scratch array's code object: not loaded at open, loaded once by the first call
+    assert o["open_modules"] == 1
+    assert o["noalloc_first_modules"] == 1 and o["noalloc_second_modules"] == 0
     assert "captured" in o["noalloc_capture"], o["noalloc_capture"]
     assert "600" in o["noalloc_600"] or "scratch" in o["noalloc_600"], o["noalloc_600"]
     assert o["violations"] == 0
