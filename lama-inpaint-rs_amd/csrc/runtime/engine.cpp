@@ -252,7 +252,8 @@ struct Arena {
     }
 };
 
-Packed pack(Arena &A, int M, int C, int T, int KC, const std::function<float(int, int, int)> &get)
+template <class Get>
+Packed pack(Arena &A, int M, int C, int T, int KC, const Get &get)
 {
     Packed p;
     p.M = M;
