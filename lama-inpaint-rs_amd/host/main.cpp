@@ -16,6 +16,8 @@
 #include <cstring>
 #include <chrono>
 #include <string>
+#include <system_error>
+#include <thread>
 #include <vector>
 
 #include <limits.h>
@@ -382,8 +384,37 @@ void run_sections(Engine &eng, const Rgb &src, const Gray &mask, const Args &arg
 void run(const Args &args)
 {
     const auto t_start = Clock::now();
-    const Rgb src = read_rgb(args.image);
-    const Gray mask = read_gray(args.mask);
+    // the two files decode on two threads (the image's error is reported
+    // first, as when they are read in turn)
+    Rgb src;
+    Gray mask;
+    std::string mask_err;
+    auto load_mask = [&] {
+        try {
+            mask = read_gray(args.mask);
+        } catch (const Fail &f) {
+            mask_err = f.msg;
+        } catch (const std::exception &x) {
+            mask_err = args.mask + ": " + x.what();
+        }
+    };
+    std::thread tm;
+    try {
+        tm = std::thread(load_mask);
+    } catch (const std::system_error &) {
+        load_mask();
+    }
+    std::string img_err;
+    try {
+        src = read_rgb(args.image);
+    } catch (const Fail &f) {
+        img_err = f.msg;
+    } catch (const std::exception &x) {
+        img_err = args.image + ": " + x.what();
+    }
+    if (tm.joinable()) tm.join();
+    if (!img_err.empty()) throw Fail{img_err};
+    if (!mask_err.empty()) throw Fail{mask_err};
     if (mask.w != src.w || mask.h != src.h)
         throw Fail{fmt("mask is %dx%d but image is %dx%d", mask.w, mask.h, src.w, src.h)};
     const int width = src.w, height = src.h;
