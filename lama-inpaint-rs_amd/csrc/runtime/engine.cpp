@@ -922,7 +922,7 @@ bool Engine::load_weights(const uint8_t *blob, size_t len, const lama_tensor_inf
     warena_bytes_ = total * 4;
     if (flag_profile_)
         fprintf(stderr,
-                "gpu weights: %.3fs, %.1f MB resident (host packing %.3fs, upload of %.1f MB %.3fs, "
+                "gpu weights: %.3fs, %.1f MB resident (host packing %.3fs, arena allocation and upload of %.1f MB %.3fs, "
                 "raw 3x3 upload and Winograd packing on the device %.3fs)\n",
                 since(t_load), total * 4 / 1e6, t_host, A.size() * 4 / 1e6, t_upload, t_device);
     have_weights_ = true;
