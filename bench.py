@@ -43,20 +43,25 @@ def cli_wall_times(H, wpath, tmp, reps=3):
     """Wall time of this build's lama-inpaint on the reference's published case:
     a 2048x2048 image with a seeded 300x300 hole, whole image and --tile, each
     a fresh process (start-up, weight file read, packing and upload, PNG
-    decode and encode included), `reps` runs each."""
+    decode and encode included), `reps` runs each.  Beside them, configs[4]'s
+    other case, for which the reference publishes no time: --sections on the
+    same image with a seeded 1024x1024 hole (16 passes of 512x512)."""
     cli = os.path.join(ROOT, "lama-inpaint-rs_amd", "bin", "lama-inpaint")
     img = H.synth_image(2048, 2048, 1)
     mask, _ = H.synth_mask_rect(2048, 2048, 300, 300, 2)
     ip, mp = os.path.join(tmp, "in2048.png"), os.path.join(tmp, "mask2048.png")
     H.png_write_rgb(ip, img)
     H.png_write_rgb(mp, np.repeat(mask[..., None], 3, -1))
+    big, _ = H.synth_mask_rect(2048, 2048, 1024, 1024, 2)
+    mpb = os.path.join(tmp, "mask2048_1024.png")
+    H.png_write_rgb(mpb, np.repeat(big[..., None], 3, -1))
     runs = {}
-    for mode, extra in (("whole", []), ("tile", ["--tile"])):
+    for mode, m, extra in (("whole", mp, []), ("tile", mp, ["--tile"]), ("sections", mpb, ["--sections"])):
         op = os.path.join(tmp, f"out2048_{mode}.png")
         ts = []
         for _ in range(reps):
             t = time.perf_counter()
-            p = subprocess.run([cli, "--image", ip, "--mask", mp, "--output", op, "--weights", wpath, "--gpu",
+            p = subprocess.run([cli, "--image", ip, "--mask", m, "--output", op, "--weights", wpath, "--gpu",
                                 *extra], capture_output=True, timeout=300)
             ts.append(time.perf_counter() - t)
             if p.returncode != 0:
@@ -65,12 +70,15 @@ def cli_wall_times(H, wpath, tmp, reps=3):
         runs[mode] = ts
     return {"whole_s": round(float(np.median(runs["whole"])), 3),
             "tile_s": round(float(np.median(runs["tile"])), 3),
+            "sections_1024_hole_s": round(float(np.median(runs["sections"])), 3),
             "runs_s": {m: [round(v, 3) for v in ts] for m, ts in runs.items()},
             "reference_gtx1080_s": REF_CLI_S,
-            "speedup_vs_reference": {m: round(REF_CLI_S[m] / float(np.median(runs[m])), 2) for m in runs},
+            "speedup_vs_reference": {m: round(REF_CLI_S[m] / float(np.median(runs[m])), 2) for m in REF_CLI_S},
             "case": ("lama-inpaint-rs_amd/bin/lama-inpaint --gpu [--tile] on a 2048x2048 synthetic image with a "
                      "seeded 300x300 hole (README.md:78-79's case), synthetic weights; wall time of each "
-                     f"process, median of {reps}; the reference's figures are its README's, on a GTX 1080")}
+                     f"process, median of {reps}; the reference's figures are its README's, on a GTX 1080; "
+                     "sections_1024_hole_s: --sections on the same image with a seeded 1024x1024 hole "
+                     "(BASELINE configs[4], 16 passes of 512x512; no published reference time)")}
 
 
 def main():
